@@ -1,0 +1,139 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline (BASELINE metric "Q8_0 matvec HBM GB/s (% peak)"): a step is one bs=1
+pass of the Q8_0 matvec over the Qwen2.5-1.5B projection shapes
+(N x K) 1536x1536 (q/o), 256x1536 (k/v), 8960x1536 gate+up as one fused
+launch, 1536x8960 (down) and 151936x1536 (lm_head), weights resident in HBM.
+Weight copies rotate so that each step streams from HBM rather than the
+256 MB Infinity Cache. value = algorithmic bytes (weights + int8 activations
+with f32 scales + f32 outputs) of the timed steps / timed wall time.
+
+Prints one JSON line (see the repository's driver contract).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "uefi-gpu_amd"))
+
+import numpy as np  # noqa: E402
+
+import uq  # noqa: E402
+
+METRIC = "Q8_0 matvec HBM GB/s (% peak); bs=1 decode tok/s, Qwen2.5-1.5B shape"
+HBM_PEAK_GBS = 8000.0
+
+# (name, N rows, K, fused pair)
+SHAPES = [("attn_q/o", 1536, 1536, False), ("attn_k/v", 256, 1536, False),
+          ("ffn_gate+up", 8960, 1536, True), ("ffn_down", 1536, 8960, False),
+          ("lm_head", 151936, 1536, False)]
+
+
+def q8_bytes(N, K):
+    """Algorithmic bytes of one Q8_0 matvec: weights + int8 x + f32 scales + f32 y."""
+    return N * (K // 32) * 34 + K + (K // 32) * 4 + 4 * N
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(seconds=10.0):
+    """The oracle's Q8_0 matvec (the C restatement of the reference's CPU
+    arithmetic) on 1 thread over the same shapes; lm_head limited to its first
+    15,193 rows (a tenth) so one pass stays short. Repeats passes until
+    `seconds` of CPU time have elapsed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    O.set_threads(1)
+    work = []
+    for name, N, K, pair in SHAPES:
+        rows = 15193 if name == "lm_head" else N
+        for i in range(2 if pair else 1):
+            raw = uq.synth_quant(uq.KIND_Q8_0, 0xC0FFEE + i * 7 + N, rows, K)
+            x = uq.synth_normal(0x5EED0001 + K, K)
+            work.append((raw, K, rows, x))
+    total_bytes = 0
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        for raw, K, rows, x in work:
+            O.matvec(O.Q8_0, raw, K, rows, x)
+            total_bytes += q8_bytes(rows, K)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(total_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "oracle Q8_0 matvec (int8 activations, exact block sums), %d passes over q/o, k/v, "
+                      "gate, up, down and the first 15193 lm_head rows; %.1f s; host CPU %s, nproc %d"
+                      % (passes, el, cpu_model(), os.cpu_count() or 0)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus %d is not supported "
+              "(the path's multi-GPU sharding is design-only)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    uq.init(0)
+    weights, pairs, shape_of = [], [], []
+    for c in range(args.copies):
+        for name, N, K, pair in SHAPES:
+            for i in range(2 if pair else 1):
+                raw = uq.synth_quant(uq.KIND_Q8_0, (0x5EED0001 << 8) + c * 16 + i * 4 + N, N, K)
+                weights.append(uq.Weight(uq.KIND_Q8_0, K, N, raw))
+                pairs.append(1 if (pair and i == 0) else 0)
+                shape_of.append((name, N, K, pair))
+    per_copy = len(weights) // args.copies
+    step_bytes = sum(q8_bytes(N, K) * (2 if pair else 1) - (K + K // 32 * 4 if pair else 0)
+                     for _, N, K, pair in SHAPES)
+    lm_index = [i for i, s in enumerate(shape_of) if s[0] == "lm_head"][0]
+    # one timed "round" in uq_time_matvecs = every copy once = `copies` steps
+    rounds = max(1, args.steps // args.copies)
+    steps = rounds * args.copies
+    warm_rounds = max(1, args.warmup // args.copies)
+    total_ms, lm_ms = uq.time_matvecs(weights, pairs, 8960, rounds, warm_rounds, lm_index)
+    value = step_bytes * steps / (total_ms / 1e3) / 1e9
+    lm_bytes = q8_bytes(151936, 1536)
+    lm_gbs = lm_bytes / (lm_ms / 1e3) / 1e9
+
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm_rounds * args.copies, "ms_per_step": round(total_ms / steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "Q8_0 matvec sweep bs=1, Qwen2.5-1.5B shapes (NxK) 1536x1536, 256x1536, "
+                               "2x8960x1536 fused gate+up, 1536x8960, 151936x1536; %d rotating weight copies"
+                               % args.copies,
+                   "bytes_per_step": step_bytes, "seed": 0x5EED0001, "fraction_of_hbm_peak":
+                       round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "Q8_0 matvec, lm_head 151936x1536 (%d B per launch), mean of %d launches %.4f ms"
+                               % (lm_bytes, rounds, lm_ms)},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,112 @@
+/*
+ * uq -- C ABI of the MI355X (gfx950) quantized-matmul hot path.
+ *
+ * Drop-in for the call surface of the reference runtime nodnarbrox/uefi-gpu
+ * (Rust, no_std UEFI). Each entry point names the reference interface it
+ * replaces (file:line in that repository). Plain pointers and sizes only.
+ *
+ * Conventions (driver/src/llm.rs:110-273, frontier_forward.rs:10-28):
+ *  - every call returns an int status: UQ_OK (0) or a negative UQ_ERR_*;
+ *    uq_last_error() gives the message of the calling thread's last failure;
+ *  - host-pointer calls are synchronous (the reference polls each submission
+ *    to completion); *_dev calls take device pointers and enqueue on the
+ *    library stream (or the given hipStream_t) without synchronizing;
+ *  - one process context per GPU, single caller thread, no re-entrancy
+ *    (the reference's `Gpu` object is used the same way);
+ *  - weights are device resident after a verified upload (llm.rs:157-201).
+ */
+#ifndef UQ_H
+#define UQ_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. frontier_forward.rs:10 Error {Backend, Shape, NonFinite, Context},
+ * frontier_core.rs:37 Error::QuantType, llm.rs:267-269 poll timeout. */
+#define UQ_OK 0
+#define UQ_ERR_SHAPE (-1)
+#define UQ_ERR_QUANT_TYPE (-2)
+#define UQ_ERR_NONFINITE (-3)
+#define UQ_ERR_DEVICE (-4)
+#define UQ_ERR_TIMEOUT (-5)
+#define UQ_ERR_CONTEXT (-6)
+#define UQ_ERR_ARG (-7)
+
+/* GGUF tensor kinds (ggml type ids, frontier_core.rs:53-58 plus Q3_K/Q4_K). */
+#define UQ_KIND_F32 0u
+#define UQ_KIND_Q8_0 8u
+#define UQ_KIND_Q3_K 11u
+#define UQ_KIND_Q4_K 12u
+
+/* ---------------------------------------------------------------- context */
+/* Replaces the GSP/RM channel bring-up that ends in llm::run's Gpu value
+ * (driver/src/llm.rs:287-300): selects the HIP device and creates the stream. */
+int uq_init(int device);
+int uq_shutdown(void);
+const char* uq_last_error(void);
+/* Library stream as a hipStream_t (void* so the header needs no HIP includes). */
+void* uq_stream(void);
+int uq_sync(void);
+
+/* GGUF row size of `n` values (frontier_core.rs:53-58 row_bytes); <0 on error. */
+int64_t uq_row_bytes(uint32_t kind, int64_t n);
+
+/* ---------------------------------------------------------------- weights */
+typedef struct uq_weight* uq_weight_t;
+/* Upload one GGUF tensor of m rows x n values (Tensor{n, m, typ}, llm.rs:63),
+ * repack it on the device into the kernel layout, rebuild the GGUF bytes from
+ * that layout and require a byte-for-byte match (llm.rs:187-200 upload
+ * readback, gpu_prefill.rs:74-93 swizzle verify). kind: Q8_0, Q4_K, Q3_K. */
+int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, uq_weight_t* out);
+int uq_weight_free(uq_weight_t w);
+/* Device bytes held by the weight (repacked planes). */
+int64_t uq_weight_bytes(uq_weight_t w);
+
+/* ---------------------------------------------------------------- linears */
+/* Gpu::matvec (llm.rs:246-273): y = W x, x of n floats, y of m floats, host
+ * memory, synchronous. Activations are quantized per 32 to int8 (quant_act,
+ * gpu_dp4a.cu:23-31) and the dot runs on int8 (linear_dp4a, gpu_dp4a.cu:40-52).
+ * Shape rule of llm.rs:248: n % 32 == 0, n <= 16384, m <= 160000 (per kind
+ * block size for K-quants). Non-finite x -> UQ_ERR_NONFINITE. */
+int uq_matvec(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m);
+/* Gpu::batch (llm.rs:226-245): 1..3 tensors sharing one input x. */
+int uq_batch(const uq_weight_t* ws, int count, const float* x, int64_t n, float* const* ys, const int64_t* ms);
+
+/* Device forms (graph_quant / graph_linear, gpu_graph.rs:70-80). stream may be
+ * NULL for the library stream. xq: n int8, xs: n/32 floats. */
+int uq_quant_act_dev(const float* x, int64_t n, int8_t* xq, float* xs, void* stream);
+int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, void* stream);
+/* gateup_dp4a (gpu_dp4a.cu:60-64): out[r] = silu(gate_r . x) * (up_r . x). */
+int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream);
+
+/* Integer surfaces, host memory, synchronous. uq_quant_act: x (n floats) ->
+ * q (n int8) + scale (n/32 floats) on the GPU (quant_act). uq_block_dots:
+ * int32 per-block dots of W with the quantized x (Q8_0: m*(n/32) per 32-block,
+ * Q4_K: m*(n/32) per 32 sub-block with q in 0..15, Q3_K: m*(n/16) per 16
+ * sub-block with q3 in -4..3), the int32 sums of gpu_dp4a.cu:43-46 and
+ * gpu_prefill.rs:111-115. */
+int uq_quant_act(const float* x, int64_t n, int8_t* q, float* scale);
+int uq_block_dots(uq_weight_t w, const float* x, int64_t n, int32_t* dots, int64_t count);
+
+/* ---------------------------------------------------------------- memory + timing
+ * Small helpers so harnesses need no other GPU runtime binding. */
+int uq_dev_alloc(size_t bytes, void** ptr);
+int uq_dev_free(void* ptr);
+int uq_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int uq_memcpy_d2h(void* dst, const void* src, size_t bytes);
+/* Times `reps` rounds of matvecs over `count` weights (each weight its own
+ * input/output), all on the library stream, after `warmup` untimed rounds.
+ * Per-launch HIP event pairs are recorded around launches of weight index
+ * `probe` (or none if probe < 0). total_ms: whole timed region; probe_ms: mean
+ * duration of the probed launch. pairs[i] != 0 marks weight i as the gate of a
+ * gate/up pair with weight i+1 (one fused launch). */
+int uq_time_matvecs(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
+                    int probe, double* total_ms, double* probe_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

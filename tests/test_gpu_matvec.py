@@ -1,0 +1,161 @@
+"""GPU parity of the quantized matvec path against the CPU oracle, through the
+C ABI. Integer work (quantized activations, per-block int32 dots) must be
+bit-exact; f32 outputs are compared bit for bit (both sides round one exactly
+accumulated sum) and, independently, against the stated tolerance
+|gpu - oracle| <= 1e-3 * max(|oracle|, 1e-3 * max|oracle|)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import uq
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151936, 1536)]   # (N rows, K)
+
+
+def tol_ok(y, ref):
+    scale = np.abs(ref).max()
+    return bool((np.abs(y - ref) <= 1e-3 * np.maximum(np.abs(ref), 1e-3 * scale)).all())
+
+
+def ulps(a, b):
+    a = a.view(np.int32).astype(np.int64)
+    b = b.view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def test_quant_act_bit_exact(gpu):
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, 16384).astype(np.float32)
+    x[:32] = 0
+    x[32:64] = np.arange(32) - 15.5
+    x[64] = 127.0
+    x[65:73] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 126.5]
+    x[96:128] = rng.normal(0, 1e-30, 32)        # subnormal products
+    x[128:160] = rng.normal(0, 1e30, 32)
+    q, s = uq.quant_act(x)
+    qo, so = O.quant_act(x)
+    assert np.array_equal(q, qo)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,n,m", [(uq.KIND_Q8_0, 1536, 300), (uq.KIND_Q8_0, 8960, 64),
+                                      (uq.KIND_Q4_K, 1536, 300), (uq.KIND_Q4_K, 8960, 40),
+                                      (uq.KIND_Q3_K, 2048, 200), (uq.KIND_Q3_K, 768, 100)])
+def test_block_dots_bit_exact(gpu, kind, n, m):
+    raw = uq.synth_quant(kind, 1000 + kind, m, n)
+    x = uq.synth_normal(2000 + n, n)
+    w = uq.Weight(kind, n, m, raw)
+    got = uq.block_dots(w, x)
+    qx, _ = O.quant_act(x)
+    ref = O.block_dots(kind, raw, n, m, qx)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_q8_matvec_baseline_shapes(gpu, N, K):
+    raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0001 + N, N, K)
+    x = uq.synth_normal(0x5EED0001 + K, K)
+    w = uq.Weight(uq.KIND_Q8_0, K, N, raw)
+    y = uq.matvec(w, x)
+    ref = O.matvec(O.Q8_0, raw, K, N, x)
+    assert tol_ok(y, ref)
+    d = ulps(y, ref)
+    assert d.max() <= 1 and (d == 0).mean() > 0.9999, (d.max(), (d == 0).mean())
+
+
+@pytest.mark.parametrize("N,K", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151936, 1536)])
+def test_q4k_matvec_baseline_shapes(gpu, N, K):
+    raw = uq.synth_quant(uq.KIND_Q4_K, 0x5EED0001 + N, N, K)
+    x = uq.synth_normal(0x5EED0011 + K, K)
+    w = uq.Weight(uq.KIND_Q4_K, K, N, raw)
+    y = uq.matvec(w, x)
+    ref = O.matvec(O.Q4_K, raw, K, N, x)
+    assert tol_ok(y, ref)
+    assert ulps(y, ref).max() <= 1
+
+
+@pytest.mark.parametrize("N,K", [(768, 2048), (2048, 768)])
+def test_q3k_matvec_moe_shapes(gpu, N, K):
+    raw = uq.synth_quant(uq.KIND_Q3_K, 0x5EED0004 + N, N, K)
+    x = uq.synth_normal(0x5EED0014 + K, K)
+    w = uq.Weight(uq.KIND_Q3_K, K, N, raw)
+    y = uq.matvec(w, x)
+    ref = O.matvec(O.Q3_K, raw, K, N, x)
+    assert tol_ok(y, ref)
+    assert ulps(y, ref).max() <= 1
+
+
+@pytest.mark.parametrize("m,n", [(1, 32), (3, 64), (17, 96), (64, 16384), (5, 480)])
+def test_q8_matvec_ragged_shapes(gpu, m, n):
+    raw = uq.synth_quant(uq.KIND_Q8_0, 31 * m + n, m, n)
+    x = uq.synth_normal(n, n, 0.0, 3.0)
+    w = uq.Weight(uq.KIND_Q8_0, n, m, raw)
+    assert ulps(uq.matvec(w, x), O.matvec(O.Q8_0, raw, n, m, x)).max() <= 1
+
+
+def test_gateup_fused_silu(gpu):
+    import ctypes
+    N, K = 8960, 1536
+    rg = uq.synth_quant(uq.KIND_Q8_0, 71, N, K)
+    ru = uq.synth_quant(uq.KIND_Q8_0, 72, N, K)
+    x = uq.synth_normal(73, K)
+    wg, wu = uq.Weight(uq.KIND_Q8_0, K, N, rg), uq.Weight(uq.KIND_Q8_0, K, N, ru)
+    L = uq.lib()
+    buf = {}
+    for name, size in (("x", 4 * K), ("xq", K), ("xs", 4 * K // 32), ("out", 4 * N)):
+        p = ctypes.c_void_p()
+        uq._check(L.uq_dev_alloc(size, ctypes.byref(p)))
+        buf[name] = p
+    try:
+        uq._check(L.uq_memcpy_h2d(buf["x"], x.ctypes.data, 4 * K))
+        uq._check(L.uq_quant_act_dev(buf["x"], K, buf["xq"], buf["xs"], None))
+        uq._check(L.uq_gateup_q_dev(wg.handle, wu.handle, buf["xq"], buf["xs"], buf["out"], None))
+        out = np.empty(N, np.float32)
+        uq._check(L.uq_memcpy_d2h(out.ctypes.data, buf["out"], 4 * N))
+    finally:
+        for p in buf.values():
+            L.uq_dev_free(p)
+    g = O.matvec(O.Q8_0, rg, K, N, x)
+    u = O.matvec(O.Q8_0, ru, K, N, x)
+    ref = np.array([O.silu_mul(float(a), float(b)) for a, b in zip(g, u)], np.float32)
+    assert ulps(out, ref).max() <= 1
+
+
+def test_batch_and_reference_surface(gpu):
+    K = 1536
+    raws = [uq.synth_quant(uq.KIND_Q8_0, 90 + i, m, K) for i, m in enumerate((1536, 256, 256))]
+    ts = [uq.Tensor("blk.0.attn_%s.weight" % s, K, m, uq.KIND_Q8_0, r)
+          for s, m, r in zip("qkv", (1536, 256, 256), raws)]
+    g = uq.Gpu(0)
+    for t in ts:
+        g.upload(t)
+    x = uq.synth_normal(99, K)
+    ys = [np.zeros(t.m, np.float32) for t in ts]
+    assert g.batch(ts, x, ys)
+    for t, y, r in zip(ts, ys, raws):
+        assert ulps(y, O.matvec(O.Q8_0, r, K, t.m, x)).max() <= 1
+    y1 = np.zeros(1536, np.float32)
+    assert g.matvec(ts[0], x, y1) and np.array_equal(y1, ys[0])
+    # failure modes return False like the reference (llm.rs:227,248)
+    assert not g.batch(ts + ts[:1], x, ys + ys[:1])              # > 3 tensors
+    assert not g.matvec(ts[0], x[:1024], y1)                     # x length != n
+    assert not g.matvec(ts[1], x, y1)                            # y length != m
+    bad = x.copy()
+    bad[5] = np.nan
+    assert not g.matvec(ts[0], bad, y1) and "NONFINITE" in g.last_error
+
+
+def test_upload_rejects_bad_shapes(gpu):
+    raw = uq.synth_quant(uq.KIND_Q8_0, 1, 4, 64)
+    with pytest.raises(uq.UqError) as e:
+        uq.Weight(uq.KIND_Q8_0, 64, 5, raw)
+    assert e.value.status == uq.Error.SHAPE
+    with pytest.raises(uq.UqError) as e:
+        uq.Weight(14, 256, 1, np.zeros(210, np.uint8))
+    assert e.value.status == uq.Error.QUANT_TYPE
+    with pytest.raises(uq.UqError):
+        uq.Weight(uq.KIND_Q8_0, 16416, 1, np.zeros(16416 // 32 * 34, np.uint8))   # n > 16384

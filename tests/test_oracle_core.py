@@ -1,0 +1,348 @@
+"""Pins the CPU oracle (oracle/uq_oracle.c) with closed forms, textbook float64
+restatements, brute force and hand-built known-answer blocks.
+
+The reference ships no golden vectors for this path (its checks are live
+on-device gates: llm.rs:302-309, gpu_prefill.rs:95-121, gpu_graph.rs:14-23), so
+each oracle function is checked against mathematics chosen so that a dropped
+term, a wrong sign/index or a transposed operand fails.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import ggml_layouts as G
+
+RNG = np.random.default_rng(1234)
+
+
+def ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def rand_q8(rows, n, seed=7):
+    rng = np.random.default_rng(seed)
+    d = np.float16(rng.lognormal(np.log(0.01), 0.5, size=(rows, n // 32))).view(np.uint16)
+    q = rng.integers(-127, 128, size=(rows, n), dtype=np.int64).astype(np.int8)
+    return G.q8_0_pack(d, q)
+
+
+# ---------------------------------------------------------------- fp16
+def test_half_exhaustive_matches_ieee():
+    O.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([O.half(int(b)) for b in bits], np.float32)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+
+
+def test_f16_rne_matches_numpy():
+    specials = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 6.1e-5, 5.96e-8, 2.98e-8,
+                         2.9802322e-08, 8.940697e-08, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, np.inf, -np.inf,
+                         1e-30, 3.0e-5], np.float32)
+    rnd = RNG.integers(0, 2 ** 32, size=200000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    rnd = rnd[np.isfinite(rnd)]
+    xs = np.concatenate([specials, rnd, RNG.normal(0, 30, 100000).astype(np.float32)])
+    ref = xs.astype(np.float16).view(np.uint16)
+    got = np.array([O.f16_rne(float(x)) for x in xs], np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- exp
+def test_expf_within_one_ulp_of_correctly_rounded():
+    xs = np.concatenate([np.linspace(-104, 88.7, 200001, dtype=np.float32),
+                         RNG.uniform(-20, 20, 100000).astype(np.float32),
+                         np.array([0.0, -0.0, 1.0, -1.0, 1e-8, -1e-8], np.float32)])
+    got = np.array([O.expf(float(x)) for x in xs], np.float32)
+    ref = np.exp(xs.astype(np.float64)).astype(np.float32)
+    d = ulp_diff(got, ref)
+    assert d.max() <= 1
+    assert (d == 0).mean() > 0.9999
+    assert O.expf(0.0) == 1.0
+    assert O.expf(-200.0) == 0.0 and O.expf(200.0) == np.inf
+    assert np.isnan(O.expf(float("nan")))
+
+
+# ---------------------------------------------------------------- activation quant
+def test_quant_act_closed_form():
+    x = RNG.normal(0, 1, 4096).astype(np.float32)
+    x[0:32] = 0.0                                    # all-zero block
+    x[32:64] = np.linspace(-3, 3, 32)
+    x[64:96] = 1.0
+    x[96] = -5.0                                     # negative amax
+    q, s = O.quant_act(x)
+    assert s[0] == 0 and not q[0:32].any()
+    blocks = x.reshape(-1, 32)
+    amax = np.abs(blocks).max(1)
+    assert np.array_equal(s, (amax / np.float32(127)).astype(np.float32))
+    qb = q.reshape(-1, 32).astype(np.int32)
+    for b in range(1, blocks.shape[0]):
+        j = np.argmax(np.abs(blocks[b]))
+        assert abs(qb[b, j]) == 127 and np.sign(qb[b, j]) == np.sign(blocks[b, j])
+    inv = np.where(amax > 0, np.float32(127) / amax, np.float32(0)).astype(np.float32)
+    t = (blocks * inv[:, None]).astype(np.float32)
+    assert np.array_equal(qb, np.clip(np.rint(t), -127, 127).astype(np.int32))  # np.rint: half to even
+    err = np.abs(qb * s[:, None] - blocks)
+    assert (err <= s[:, None] * 0.5 + 1e-6 * np.abs(blocks)).all()
+
+
+def test_quant_act_ties_to_even():
+    # amax 127 makes inv == 1 exactly, so x*inv hits the .5 ties directly
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 126.5]
+    q, s = O.quant_act(x)
+    assert s[0] == np.float32(1.0)
+    assert list(q[1:9]) == [0, 2, 2, 0, -2, -2, 4, 126]
+
+
+# ---------------------------------------------------------------- Q8_0
+def test_row_bytes_rules():
+    # the reference's row_bytes gate (frontier_core.rs:53-58, its test :129-134)
+    assert O.lib().uqo_row_bytes(O.Q8_0, 1536) == 1632
+    assert O.lib().uqo_row_bytes(O.Q4_K, 1536) == 864
+    assert O.lib().uqo_row_bytes(O.Q3_K, 256) == 110
+    assert O.lib().uqo_row_bytes(O.F32, 3) == 12
+    assert O.lib().uqo_row_bytes(O.Q4_K, 640) < 0
+    assert O.lib().uqo_row_bytes(O.Q8_0, 0) < 0
+    assert O.lib().uqo_row_bytes(99, 256) < 0
+
+
+def test_q8_block_dots_brute_force():
+    rows, n = 24, 256
+    w = rand_q8(rows, n)
+    qx = RNG.integers(-127, 128, n).astype(np.int8)
+    dots = O.block_dots(O.Q8_0, w, n, rows, qx)
+    _, q = G.q8_0_fields(w, rows, n)
+    ref = (q.astype(np.int64) * qx.reshape(n // 32, 32).astype(np.int64)[None]).sum(-1)
+    assert np.array_equal(dots, ref)
+
+
+def test_q8_matvec_is_correctly_rounded_exact_sum():
+    rows, n = 64, 1536
+    w = rand_q8(rows, n)
+    x = RNG.normal(0, 1, n).astype(np.float32)
+    y = O.matvec(O.Q8_0, w, n, rows, x)
+    qx, xs = O.quant_act(x)
+    d, q = G.q8_0_fields(w, rows, n)
+    c = (q.astype(np.int64) * qx.reshape(-1, 32).astype(np.int64)[None]).sum(-1)
+    s = (G.f16_to_f32(d) * xs[None, :]).astype(np.float32)       # f32 product dw*dx
+    terms = c.astype(np.float64) * s.astype(np.float64)           # exact in double
+    from fractions import Fraction
+    for r in range(0, rows, 7):                                   # exact rational sum, rounded once
+        exact = sum(Fraction(float(t)) for t in terms[r])
+        assert y[r] == np.float32(float(exact)) or ulp_diff(y[r], np.float32(float(exact))) <= 1
+    ref = terms.sum(1).astype(np.float32)
+    assert ulp_diff(y, ref).max() <= 1
+
+
+def test_q8_matvec_vs_reference_literal_forms():
+    rows, n = 40, 1536
+    w = rand_q8(rows, n, seed=11)
+    x = RNG.normal(0, 1, n).astype(np.float32)
+    y = O.matvec(O.Q8_0, w, n, rows, x)
+    lit = O.q8_matvec_f32seq(w, n, rows, x)        # gpu_prefill.rs:104-116 literal f32
+    scale = np.abs(lit).max()
+    assert (np.abs(y - lit) <= 1e-3 * np.maximum(np.abs(lit), 1e-3 * scale)).all()
+    deq = O.q8_dequant_dot(w, n, rows, x)          # llm.rs:302-309 fp32 dequant dot
+    dense = G.q8_0_dequant(w, rows, n).astype(np.float64) @ x.astype(np.float64)
+    assert np.allclose(deq, dense, rtol=1e-4, atol=1e-4 * np.abs(dense).max())
+    # int8 activations vs fp32: the quantization error bound, not a bit match
+    assert np.abs(y - dense).max() < 0.02 * np.abs(dense).max()
+
+
+def test_q8_dequantize_matches_independent_layout():
+    rows, n = 3, 256
+    w = rand_q8(rows, n, seed=3)
+    got = np.concatenate([O.dequantize(O.Q8_0, w[r * 272:(r + 1) * 272], n) for r in range(rows)])
+    assert np.array_equal(got, G.q8_0_dequant(w, rows, n).reshape(-1))
+
+
+# ---------------------------------------------------------------- Q4_K / Q3_K
+def test_q4k_known_answer_block():
+    # d = 1, dmin = 0, every sub-scale 1 -> value == q
+    q = np.arange(256) % 16
+    blk = G.q4_k_pack(0x3C00, 0x0000, [1] * 8, [0] * 8, q)
+    assert np.array_equal(O.dequantize(O.Q4_K, blk, 256), q.astype(np.float32))
+    # d = 0.5, dmin = 2, sc = j+1, m = 63-j (exercises the 6-bit high parts)
+    sc, mn = [1, 17, 33, 49, 63, 5, 40, 62], [63, 2, 47, 16, 31, 60, 1, 33]
+    blk = G.q4_k_pack(0x3800, 0x4000, sc, mn, q)
+    d, dmin, sc2, mn2, q2 = G.q4_k_unpack(blk)
+    assert list(sc2) == sc and list(mn2) == mn and np.array_equal(q2, q)
+    exp = np.concatenate([np.float32(0.5 * sc[a]) * q[a * 32:(a + 1) * 32] - np.float32(2.0 * mn[a])
+                          for a in range(8)]).astype(np.float32)
+    assert np.array_equal(O.dequantize(O.Q4_K, blk, 256), exp)
+
+
+def test_q3k_known_answer_block():
+    q3 = np.arange(256) % 8
+    scales = [32 + 1] * 16                       # (sc - 32) == 1
+    blk = G.q3_k_pack(q3, scales, 0x3C00)        # d = 1 -> value == q3 - 4
+    assert np.array_equal(O.dequantize(O.Q3_K, blk, 256), (q3 - 4).astype(np.float32))
+    scales = list(range(0, 64, 4))               # 16 distinct 6-bit scales
+    blk = G.q3_k_pack(q3[::-1].copy(), scales, 0x4000)
+    vals, sc2, d = G.q3_k_unpack(blk)
+    assert list(sc2) == scales and np.array_equal(vals, q3[::-1] - 4)
+    exp = np.concatenate([np.float32(2.0 * (scales[k] - 32)) * (q3[::-1][16 * k:16 * (k + 1)] - 4)
+                          for k in range(16)]).astype(np.float32)
+    assert np.array_equal(O.dequantize(O.Q3_K, blk, 256), exp)
+
+
+@pytest.mark.parametrize("kind", [O.Q4_K, O.Q3_K])
+def test_kquant_dequant_matches_independent_layout(kind):
+    rng = np.random.default_rng(kind)
+    rows, n = 3, 512
+    rb = 144 if kind == O.Q4_K else 110
+    raw = rng.integers(0, 256, rows * (n // 256) * rb, dtype=np.int64).astype(np.uint8)
+    # keep the fp16 scales finite and moderate
+    blocks = raw.reshape(-1, rb)
+    for off in ((0, 2) if kind == O.Q4_K else (108,)):
+        blocks[:, off:off + 2] = np.float16(rng.uniform(0.001, 0.1, len(blocks))).view(np.uint8).reshape(-1, 2)
+    got = np.stack([O.dequantize(kind, raw[r * (n // 256) * rb:(r + 1) * (n // 256) * rb], n) for r in range(rows)])
+    ref = (G.q4_k_dequant if kind == O.Q4_K else G.q3_k_dequant)(raw, rows, n)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("kind", [O.Q4_K, O.Q3_K])
+def test_kquant_integer_path_matches_dequant(kind):
+    rng = np.random.default_rng(100 + kind)
+    rows, n = 16, 768
+    rb = 144 if kind == O.Q4_K else 110
+    raw = rng.integers(0, 256, rows * (n // 256) * rb, dtype=np.int64).astype(np.uint8)
+    blocks = raw.reshape(-1, rb)
+    for off in ((0, 2) if kind == O.Q4_K else (108,)):
+        blocks[:, off:off + 2] = np.float16(rng.uniform(0.001, 0.1, len(blocks))).view(np.uint8).reshape(-1, 2)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    qx, xs = O.quant_act(x)
+    y = O.matvec_q(kind, raw, n, rows, xs, qx)
+    W = (G.q4_k_dequant if kind == O.Q4_K else G.q3_k_dequant)(raw, rows, n).astype(np.float64)
+    xdq = (qx.reshape(-1, 32).astype(np.float64) * xs[:, None].astype(np.float64)).reshape(-1)
+    ref = W @ xdq
+    assert np.allclose(y, ref, rtol=2e-5, atol=2e-5 * np.abs(ref).max())
+    # integer sums brute force
+    dots = O.block_dots(kind, raw, n, rows, qx)
+    if kind == O.Q4_K:
+        qv = np.stack([G.q4_k_unpack(b)[4] for b in raw.reshape(-1, 144)]).reshape(rows, n)
+        ref_d = (qv.reshape(rows, -1, 32) * qx.reshape(-1, 32)[None].astype(np.int64)).sum(-1)
+    else:
+        qv = np.stack([G.q3_k_unpack(b)[0] for b in raw.reshape(-1, 110)]).reshape(rows, n)
+        ref_d = (qv.reshape(rows, -1, 16) * qx.reshape(-1, 16)[None].astype(np.int64)).sum(-1)
+    assert np.array_equal(dots, ref_d)
+
+
+# ---------------------------------------------------------------- prefill GEMM
+def test_prefill_gemm_integer_and_bound():
+    rows, n, batch = 48, 512, 9
+    w = rand_q8(rows, n, seed=5)
+    X = RNG.normal(0, 1, (batch, n)).astype(np.float32)
+    qs = [O.quant_act(x) for x in X]
+    qx = np.stack([a for a, _ in qs])
+    xs = np.stack([b for _, b in qs])
+    y = O.prefill_gemm(w, n, rows, xs, qx, batch)
+    d, q = G.q8_0_fields(w, rows, n)
+    c = np.einsum("rbk,tbk->trb", q.astype(np.int64), qx.reshape(batch, -1, 32).astype(np.int64))
+    s = (G.f16_to_f32(d)[None] * xs[:, None, :]).astype(np.float32)
+    ref = (c.astype(np.float64) * s.astype(np.float64)).sum(-1)
+    assert np.allclose(y, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    # sequential fmaf order: a token's row equals the decode form to within rounding
+    for t in range(batch):
+        yd = O.matvec_q(O.Q8_0, w, n, rows, xs[t], qx[t])
+        assert np.allclose(y[t], yd, rtol=1e-5, atol=1e-5 * np.abs(yd).max())
+    # rows and tokens are independent: permuting tokens permutes outputs exactly
+    perm = RNG.permutation(batch)
+    y2 = O.prefill_gemm(w, n, rows, xs[perm], qx[perm], batch)
+    assert np.array_equal(y2, y[perm])
+
+
+# ---------------------------------------------------------------- norm / rope / attention / greedy
+def test_rmsnorm_vs_float64():
+    x = RNG.normal(0, 30, 1536).astype(np.float32)
+    g = (1 + 0.1 * RNG.normal(0, 1, 1536)).astype(np.float32)
+    y = O.rmsnorm(x, g)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean() + 1e-6) * g
+    assert np.allclose(y, ref, rtol=3e-7 * 4, atol=0)
+    assert np.allclose(O.rmsnorm(np.zeros(64, np.float32), np.ones(64, np.float32)), 0)
+
+
+def test_rope_table_and_rotation():
+    T = O.rope_table(640, 128, 1e6)
+    assert np.array_equal(T[0, :64], np.ones(64, np.float32)) and np.array_equal(T[0, 64:], np.zeros(64, np.float32))
+    pos = np.arange(640)[:, None].astype(np.float64)
+    ang = pos * (1e6 ** (-(2 * np.arange(64)) / 128.0))[None]
+    assert np.abs(T[:, :64] - np.cos(ang)).max() < 2e-4 and np.abs(T[:, 64:] - np.sin(ang)).max() < 2e-4
+    v = RNG.normal(0, 5, 12 * 128).astype(np.float32)
+    b = RNG.normal(0, 0.02, 12 * 128).astype(np.float32)
+    assert np.array_equal(O.rope_bias(v, b, 12, 128, T[0]), (v + b).astype(np.float32))
+    out = O.rope_bias(v, b, 12, 128, T[300])
+    u = (v + b).astype(np.float64).reshape(12, 2, 64)
+    c, s = T[300, :64].astype(np.float64), T[300, 64:].astype(np.float64)
+    ref = np.stack([u[:, 0] * c - u[:, 1] * s, u[:, 0] * s + u[:, 1] * c], 1).reshape(-1)
+    assert np.allclose(out, ref, rtol=1e-6, atol=1e-5)
+    # rotation preserves each pair's norm
+    o = out.astype(np.float64).reshape(12, 2, 64)
+    assert np.allclose((o ** 2).sum(1), (u ** 2).sum(1), rtol=1e-5)
+
+
+def test_attention_vs_float64_softmax():
+    heads, kvh, hd, pos = 12, 2, 128, 200
+    q = RNG.normal(0, 3, heads * hd).astype(np.float32)
+    K = RNG.normal(0, 3, (pos + 1, kvh * hd)).astype(np.float16)
+    V = RNG.normal(0, 3, (pos + 1, kvh * hd)).astype(np.float16)
+    out = O.attention(q, K.view(np.uint16), V.view(np.uint16), pos, heads, kvh, hd)
+    ref = np.zeros(heads * hd)
+    for h in range(heads):
+        kh = h // (heads // kvh)
+        s = (K[:, kh * hd:(kh + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd]) / np.sqrt(hd)
+        pr = np.exp(s - s.max())
+        pr /= pr.sum()
+        ref[h * hd:(h + 1) * hd] = pr @ V[:, kh * hd:(kh + 1) * hd].astype(np.float64)
+    assert np.allclose(out, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    # a single position returns v exactly (softmax of one element is exactly 1)
+    out0 = O.attention(q, K.view(np.uint16), V.view(np.uint16), 0, heads, kvh, hd)
+    v0 = V[0].astype(np.float32)
+    assert np.array_equal(out0, np.concatenate([v0[(h // 6) * hd:(h // 6 + 1) * hd] for h in range(heads)]))
+
+
+def test_greedy_tie_and_nonfinite_rules():
+    x = RNG.normal(0, 1, 151936).astype(np.float32)
+    i, bad = O.greedy(x)
+    assert i == int(np.argmax(x)) and not bad
+    x[10] = x[500] = x.max() + 1
+    assert O.greedy(x) == (10, False)          # lowest id wins ties
+    x[7] = np.nan
+    assert O.greedy(x)[1]
+    y = np.full(16, -np.inf, np.float32)
+    assert O.greedy(y) == (0, True)
+
+
+def test_silu_mul_vs_float64():
+    g = np.concatenate([RNG.normal(0, 30, 2000), [0, -0.0, 100, -100, 88, -88]]).astype(np.float32)
+    u = RNG.normal(0, 30, g.size).astype(np.float32)
+    got = np.array([O.silu_mul(float(a), float(b)) for a, b in zip(g, u)], np.float32)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(got, ref, rtol=4e-7 * 4, atol=1e-30)
+
+
+# ---------------------------------------------------------------- MoE routing
+def test_moe_route_vs_stable_sort():
+    for seed in range(20):
+        lg = np.random.default_rng(seed).normal(0, 1, 128).astype(np.float32)
+        if seed == 3:
+            lg[5] = lg[77] = lg.max() + 0.5       # exact tie: lower id first
+        rc, ids, w = O.moe_route(lg, 8)
+        assert rc == 0
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = sorted(range(128), key=lambda e: (-np.float32(p[e]), e))
+        assert list(ids) == order[:8]
+        assert np.allclose(w, p[ids] / p[ids].sum(), rtol=1e-6)
+        assert abs(float(w.astype(np.float64).sum()) - 1) < 1e-6
+    _, ids, _ = O.moe_route(np.zeros(128, np.float32), 8)
+    assert list(ids) == list(range(8))

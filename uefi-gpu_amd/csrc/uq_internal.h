@@ -1,0 +1,61 @@
+// Internal host-side declarations shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+namespace uq {
+
+enum Status : int {
+    OK = 0,
+    ERR_SHAPE = -1,       // frontier_forward.rs:10 Error::Shape
+    ERR_QUANT_TYPE = -2,  // frontier_core.rs:37 Error::QuantType
+    ERR_NONFINITE = -3,   // Error::NonFinite
+    ERR_DEVICE = -4,      // Error::Backend (device call failed)
+    ERR_TIMEOUT = -5,     // llm.rs:267-269 bounded poll expired
+    ERR_CONTEXT = -6,     // Error::Context (position beyond the cache)
+    ERR_ARG = -7,         // null pointer / bad handle / wrong state
+};
+
+enum Kind : uint32_t { KIND_F32 = 0, KIND_Q8_0 = 8, KIND_Q3_K = 11, KIND_Q4_K = 12 };
+
+int set_error(int status, const std::string& msg);
+#define UQ_CHECK_HIP(call)                                                        \
+    do {                                                                          \
+        hipError_t e_ = (call);                                                   \
+        if (e_ != hipSuccess)                                                     \
+            return ::uq::set_error(::uq::ERR_DEVICE, std::string(#call) + ": " +  \
+                                                     hipGetErrorString(e_));      \
+    } while (0)
+
+int64_t row_bytes(uint32_t kind, int64_t n);  // GGUF bytes of one row, <0 if invalid
+
+// Device-resident weight. Q8_0 is split into an int8 plane qs[m][n] and an
+// fp16 scale plane d[m][n/32]; Q4_K keeps the 144-byte superblocks (16-byte
+// aligned already); Q3_K is split into quants q[m][n/256][96] (hmask 32 B +
+// qs 64 B), packed 6-bit scales sc[m][n/256][12] and fp16 d[m][n/256].
+struct Weight {
+    uint32_t kind = 0;
+    int64_t n = 0, m = 0;   // n = K (input length), m = N (output rows)
+    void* alloc = nullptr;  // single device allocation owning the planes
+    size_t alloc_bytes = 0;
+    const int8_t* qs = nullptr;    // Q8_0 quants / Q3_K quants / Q4_K superblocks
+    const uint16_t* d = nullptr;   // Q8_0 / Q3_K fp16 scales
+    const uint8_t* sc = nullptr;   // Q3_K packed scales
+    int64_t gguf_bytes = 0;        // bytes of the original GGUF tensor
+};
+
+// ---- kernel launchers (uq_matvec.hip) ----
+void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s);
+void launch_q8_repack(const uint8_t* gguf, int64_t rows, int64_t nb, int8_t* qs, uint16_t* d, hipStream_t s);
+void launch_q8_verify(const int8_t* qs, const uint16_t* d, const uint8_t* gguf, int64_t rows, int64_t nb,
+                      unsigned* mismatches, hipStream_t s);
+void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s);
+void launch_q3k_verify(const int8_t* q, const uint8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
+                       unsigned* mismatches, hipStream_t s);
+// y[m] = W x for any kind; gate/up fusion writes silu(gate)*up when w2 != null.
+int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s);
+int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s);
+
+}  // namespace uq

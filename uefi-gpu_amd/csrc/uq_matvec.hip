@@ -1,0 +1,412 @@
+// GGUF block-quant matvec for gfx950 (Q8_0, Q4_K, Q3_K) with int8 activations.
+//
+// Replaces linear_dp4a / qkv_dp4a / gateup_dp4a (driver/kernels/gpu_dp4a.cu:23-64)
+// and the fp32-activation frontier_matvec (driver/kernels/frontier_quant.cu:264-272).
+//
+// Design (bandwidth-bound, no MFMA):
+//  * weights are repacked once so every lane issues 16-byte global loads:
+//    Q8_0 -> int8 plane [rows][K] + fp16 scale plane; Q4_K superblocks are
+//    already 144 = 9*16 bytes; Q3_K -> 96-byte quant plane + 12-byte scale
+//    plane + fp16 d plane.
+//  * a row is owned by LPR consecutive lanes of a wave64; lane `sub` handles
+//    work units sub, sub+LPR, ... (Q8_0 unit = 32 values, Q4_K = 64, Q3_K = 128).
+//    The lane's activation units are loaded into registers once and reused for
+//    every row the wave visits (grid-stride over row sets).
+//  * int32 per-block dots with v_dot4_i32_i8; each block contributes an exact
+//    double term, lanes are combined by a butterfly in double, one f32 rounding.
+#include "uq_device.h"
+#include "uq_internal.h"
+
+namespace uq {
+namespace {
+
+constexpr int WG = 256;  // 4 waves
+
+// ---------------------------------------------------------------- activation quant
+__global__ __launch_bounds__(WG) void k_quant_act(const float* __restrict__ x, int64_t n,
+                                                  int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const float v = i < n ? x[i] : 0.0f;  // n % 32 == 0: a 32-lane block is all in or all out
+    float s;
+    const int8_t q = uq_quant_lane(v, &s);
+    if (i < n) {
+        xq[i] = q;
+        if ((threadIdx.x & 31) == 0) xs[i >> 5] = s;
+    }
+}
+
+// ---------------------------------------------------------------- repack / verify
+// Q8_0: 34-byte GGUF block (fp16 d, 32 x int8) -> qs[row][32b..] + d[row][b].
+__global__ __launch_bounds__(WG) void k_q8_repack(const uint8_t* __restrict__ src, int64_t rows, int64_t nb,
+                                                  int8_t* __restrict__ qs, uint16_t* __restrict__ d) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= rows * nb) return;
+    const uint8_t* p = src + blk * 34;
+    d[blk] = (uint16_t)(p[0] | (p[1] << 8));
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        w[k] = (uint32_t)p[2 + 4 * k] | ((uint32_t)p[3 + 4 * k] << 8) | ((uint32_t)p[4 + 4 * k] << 16) |
+               ((uint32_t)p[5 + 4 * k] << 24);
+    int4* dst = (int4*)(qs + blk * 32);
+    dst[0] = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    dst[1] = make_int4((int)w[4], (int)w[5], (int)w[6], (int)w[7]);
+}
+// Rebuilds each GGUF block from the planes and counts differing bytes
+// (the byte-for-byte check of gpu_prefill.rs:74-93).
+__global__ __launch_bounds__(WG) void k_q8_verify(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d,
+                                                  const uint8_t* __restrict__ src, int64_t rows, int64_t nb,
+                                                  unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= rows * nb) return;
+    const uint8_t* p = src + blk * 34;
+    unsigned miss = 0;
+    miss += (uint8_t)(d[blk] & 0xff) != p[0];
+    miss += (uint8_t)(d[blk] >> 8) != p[1];
+    for (int j = 0; j < 32; j++) miss += (uint8_t)qs[blk * 32 + j] != p[2 + j];
+    if (miss) atomicAdd(bad, miss);
+}
+// Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, scales 12, d 2) ->
+// q[blk][96] = hmask|qs, sc[blk][12], d[blk].
+__global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
+                                                   int8_t* __restrict__ q, uint8_t* __restrict__ sc,
+                                                   uint16_t* __restrict__ d) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint8_t* p = src + blk * 110;
+    uint8_t* dq = (uint8_t*)q + blk * 96;
+    for (int j = 0; j < 96; j++) dq[j] = p[j];
+    for (int j = 0; j < 12; j++) sc[blk * 12 + j] = p[96 + j];
+    d[blk] = (uint16_t)(p[108] | (p[109] << 8));
+}
+__global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const uint8_t* __restrict__ sc,
+                                                   const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
+                                                   int64_t blocks, unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint8_t* p = src + blk * 110;
+    unsigned miss = 0;
+    for (int j = 0; j < 96; j++) miss += (uint8_t)q[blk * 96 + j] != p[j];
+    for (int j = 0; j < 12; j++) miss += sc[blk * 12 + j] != p[96 + j];
+    miss += (uint8_t)(d[blk] & 0xff) != p[108];
+    miss += (uint8_t)(d[blk] >> 8) != p[109];
+    if (miss) atomicAdd(bad, miss);
+}
+
+// ---------------------------------------------------------------- per-kind units
+struct WArgs {
+    const int8_t* qs;
+    const uint16_t* d;
+    const uint8_t* sc;
+};
+
+// Q8_0 unit: one 32-value block.
+struct Q8 {
+    static constexpr int UNIT = 32;
+    struct X { int4 a, b; float s; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 32);
+        x.a = p[0];
+        x.b = p[1];
+        x.s = xs[u];
+    }
+    static UQ_DEV void zero_x(X& x) { x.a = x.b = make_int4(0, 0, 0, 0); x.s = 0.0f; }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        const int4* p = (const int4*)(w.qs + (row * nu + u) * 32);
+        const int4 wa = p[0], wb = p[1];
+        const int c = uq_dot32(wa, wb, x.a, x.b);
+        const float s = uq_half(w.d[row * nu + u]) * x.s;
+        return (double)c * (double)s;
+    }
+};
+
+// Q4_K unit: pair j of a superblock = 32 bytes of qs holding sub-blocks 2j (low
+// nibbles) and 2j+1 (high nibbles). ggml value = d*sc*q - dmin*m per sub-block.
+struct Q4K {
+    static constexpr int UNIT = 64;
+    struct X { int4 a0, a1, b0, b1; float s0, s1; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 64);
+        x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
+        x.s0 = xs[2 * u];
+        x.s1 = xs[2 * u + 1];
+    }
+    static UQ_DEV void zero_x(X& x) {
+        x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
+        x.s0 = x.s1 = 0.0f;
+    }
+    static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
+    static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        const int64_t sb = (row * nu + u) >> 2;  // nu = 4 * superblocks per row
+        const int j = u & 3;
+        const uint8_t* blk = (const uint8_t*)w.qs + sb * 144;
+        const int4 hdr = *(const int4*)blk;
+        const int4 q0 = *(const int4*)(blk + 16 + 32 * j);
+        const int4 q1 = *(const int4*)(blk + 32 + 32 * j);
+        int il = 0, ih = 0, xl = 0, xh = 0;
+        il = uq_dot4(lo4(q0.x), x.a0.x, il); il = uq_dot4(lo4(q0.y), x.a0.y, il);
+        il = uq_dot4(lo4(q0.z), x.a0.z, il); il = uq_dot4(lo4(q0.w), x.a0.w, il);
+        il = uq_dot4(lo4(q1.x), x.a1.x, il); il = uq_dot4(lo4(q1.y), x.a1.y, il);
+        il = uq_dot4(lo4(q1.z), x.a1.z, il); il = uq_dot4(lo4(q1.w), x.a1.w, il);
+        ih = uq_dot4(hi4(q0.x), x.b0.x, ih); ih = uq_dot4(hi4(q0.y), x.b0.y, ih);
+        ih = uq_dot4(hi4(q0.z), x.b0.z, ih); ih = uq_dot4(hi4(q0.w), x.b0.w, ih);
+        ih = uq_dot4(hi4(q1.x), x.b1.x, ih); ih = uq_dot4(hi4(q1.y), x.b1.y, ih);
+        ih = uq_dot4(hi4(q1.z), x.b1.z, ih); ih = uq_dot4(hi4(q1.w), x.b1.w, ih);
+        const int ones = 0x01010101;
+        xl = uq_dot4(ones, x.a0.x, xl); xl = uq_dot4(ones, x.a0.y, xl);
+        xl = uq_dot4(ones, x.a0.z, xl); xl = uq_dot4(ones, x.a0.w, xl);
+        xl = uq_dot4(ones, x.a1.x, xl); xl = uq_dot4(ones, x.a1.y, xl);
+        xl = uq_dot4(ones, x.a1.z, xl); xl = uq_dot4(ones, x.a1.w, xl);
+        xh = uq_dot4(ones, x.b0.x, xh); xh = uq_dot4(ones, x.b0.y, xh);
+        xh = uq_dot4(ones, x.b0.z, xh); xh = uq_dot4(ones, x.b0.w, xh);
+        xh = uq_dot4(ones, x.b1.x, xh); xh = uq_dot4(ones, x.b1.y, xh);
+        xh = uq_dot4(ones, x.b1.z, xh); xh = uq_dot4(ones, x.b1.w, xh);
+        // header: d (bytes 0-1), dmin (2-3), 12 scale bytes (4-15)
+        const float dd = uq_half((uint16_t)(hdr.x & 0xffff));
+        const float dm = uq_half((uint16_t)((unsigned)hdr.x >> 16));
+        const uint64_t slo = (uint64_t)(uint32_t)hdr.y | ((uint64_t)(uint32_t)hdr.z << 32);
+        const uint32_t shi = (uint32_t)hdr.w;
+        int sc0, m0, sc1, m1;
+        scale_min(2 * j, slo, shi, sc0, m0);
+        scale_min(2 * j + 1, slo, shi, sc1, m1);
+        const float d0 = dd * (float)sc0, n0 = dm * (float)m0;
+        const float d1 = dd * (float)sc1, n1 = dm * (float)m1;
+        const double t0 = (double)x.s0 * ((double)d0 * (double)il - (double)n0 * (double)xl);
+        const double t1 = (double)x.s1 * ((double)d1 * (double)ih - (double)n1 * (double)xh);
+        return t0 + t1;
+    }
+    static UQ_DEV int sbyte(int k, uint64_t lo, uint32_t hi) {
+        return k < 8 ? (int)((lo >> (8 * k)) & 0xff) : (int)((hi >> (8 * (k - 8))) & 0xff);
+    }
+    // ggml get_scale_min_k4 over the 12 scale bytes held in registers
+    static UQ_DEV void scale_min(int j, uint64_t lo, uint32_t hi, int& sc, int& m) {
+        if (j < 4) {
+            sc = sbyte(j, lo, hi) & 63;
+            m = sbyte(j + 4, lo, hi) & 63;
+        } else {
+            sc = (sbyte(j + 4, lo, hi) & 0xF) | ((sbyte(j - 4, lo, hi) >> 6) << 4);
+            m = (sbyte(j + 4, lo, hi) >> 4) | ((sbyte(j, lo, hi) >> 6) << 4);
+        }
+    }
+};
+
+// Q3_K unit: half n of a superblock = 128 values = 4 activation blocks j.
+// Block j's 32 values use qs[32n .. 32n+31] bits 2j..2j+1 and hmask[0..31]
+// bit 4n+j; value = low2 - 4*(1-hbit); sub-blocks of 16 carry 6-bit scales.
+struct Q3K {
+    static constexpr int UNIT = 128;
+    struct X { int4 v[8]; float s[4]; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 128);
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.s[k] = xs[4 * u + k];
+    }
+    static UQ_DEV void zero_x(X& x) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = make_int4(0, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.s[k] = 0.0f;
+    }
+    static UQ_DEV int dot16(const int4& w, const int4& xv, int c) {
+        c = uq_dot4(w.x, xv.x, c); c = uq_dot4(w.y, xv.y, c);
+        c = uq_dot4(w.z, xv.z, c); return uq_dot4(w.w, xv.w, c);
+    }
+    static UQ_DEV int4 extract(const int4& q, const int4& h, int shift, int hshift) {
+        int4 r;
+        r.x = (int)((((unsigned)q.x >> shift) & 0x03030303u) | ((((unsigned)h.x >> hshift) & 0x01010101u) << 2));
+        r.y = (int)((((unsigned)q.y >> shift) & 0x03030303u) | ((((unsigned)h.y >> hshift) & 0x01010101u) << 2));
+        r.z = (int)((((unsigned)q.z >> shift) & 0x03030303u) | ((((unsigned)h.z >> hshift) & 0x01010101u) << 2));
+        r.w = (int)((((unsigned)q.w >> shift) & 0x03030303u) | ((((unsigned)h.w >> hshift) & 0x01010101u) << 2));
+        return r;
+    }
+    // 6-bit scale s = 8n + k (k < 8) from the 12 packed bytes held as
+    // lo = bytes 0..7 and s2 = bytes 8..11 (ggml Q3_K scale packing).
+    static UQ_DEV int scale6(uint64_t lo, uint32_t s2, int n, int k) {
+        const int low = (int)((lo >> (8 * k + 4 * n)) & 0xF);
+        const int high = (int)((s2 >> (8 * (k & 3) + 2 * (2 * n + (k >> 2)))) & 3u);
+        return low | (high << 4);
+    }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        const int64_t sb = (row * nu + u) >> 1;  // nu = 2 * superblocks per row
+        const int n = u & 1;
+        const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
+        const int4 h0 = *(const int4*)blk, h1 = *(const int4*)(blk + 16);
+        const int4 q0 = *(const int4*)(blk + 32 + 32 * n), q1 = *(const int4*)(blk + 48 + 32 * n);
+        const uint32_t* sp = (const uint32_t*)(w.sc + sb * 12);
+        const uint64_t slo = (uint64_t)sp[0] | ((uint64_t)sp[1] << 32);
+        const uint32_t s2 = sp[2];
+        const float dd = uq_half(w.d[sb]);
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 w0 = extract(q0, h0, 2 * j, 4 * n + j), w1 = extract(q1, h1, 2 * j, 4 * n + j);
+            const int4 xa = x.v[2 * j], xb = x.v[2 * j + 1];
+            const int ones = 0x01010101;
+            int i0 = dot16(w0, xa, 0), i1 = dot16(w1, xb, 0);
+            const int s0x = dot16(make_int4(ones, ones, ones, ones), xa, 0);
+            const int s1x = dot16(make_int4(ones, ones, ones, ones), xb, 0);
+            i0 -= 4 * s0x;
+            i1 -= 4 * s1x;
+            const float dl0 = dd * (float)(scale6(slo, s2, n, 2 * j) - 32);
+            const float dl1 = dd * (float)(scale6(slo, s2, n, 2 * j + 1) - 32);
+            const double inner = (double)dl0 * (double)i0 + (double)dl1 * (double)i1;
+            acc += (double)x.s[j] * inner;
+        }
+        return acc;
+    }
+};
+
+// ---------------------------------------------------------------- matvec kernel
+template <class KQ, int LPR, int NBL, bool GATEUP>
+__global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
+                                               const float* __restrict__ xs, float* __restrict__ y,
+                                               int64_t rows, int64_t K) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int RPB = RPW * (WG / 64);
+    const int64_t nu = K / KQ::UNIT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    typename KQ::X xr[NBL];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i;
+        if (u < nu) KQ::load_x(xr[i], xq, xs, u);
+        else KQ::zero_x(xr[i]);
+    }
+    for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
+        const int64_t row = row0 + wave * RPW + grp;
+        if (row < rows) {
+            double acc = 0.0, acc2 = 0.0;
+#pragma unroll
+            for (int i = 0; i < NBL; i++) {
+                const int u = sub + LPR * i;
+                if (u < nu) {
+                    acc += KQ::term(w, row, nu, u, xr[i]);
+                    if (GATEUP) acc2 += KQ::term(w2, row, nu, u, xr[i]);
+                }
+            }
+            acc = uq_group_sum<LPR>(acc);
+            if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
+            if (sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+        }
+    }
+}
+
+// Integer per-block dots (test surface for the int32 work): Q8_0 per 32-block,
+// Q4_K per 32 sub-block (q 0..15), Q3_K per 16 sub-block (q3 -4..3); one thread
+// per (row, block), using the same int8 dot primitive as the matvec.
+__global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const int8_t* __restrict__ xq,
+                                                   int32_t* __restrict__ dots, int64_t rows, int64_t K) {
+    const int bsz = kind == KIND_Q3_K ? 16 : 32;
+    const int64_t nb = K / bsz;
+    const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (i >= rows * nb) return;
+    const int64_t row = i / nb, b = i % nb;
+    const int8_t* x = xq + b * bsz;
+    int c = 0;
+    if (kind == KIND_Q8_0) {
+        const int4* p = (const int4*)(w.qs + i * 32);
+        const int4* xp = (const int4*)x;
+        c = uq_dot32(p[0], p[1], xp[0], xp[1]);
+    } else if (kind == KIND_Q4_K) {
+        const int64_t sb = (row * (K / 256)) + b / 8;
+        const int a = (int)(b % 8), j = a >> 1, h = a & 1;
+        const uint8_t* qs = (const uint8_t*)w.qs + sb * 144 + 16 + 32 * j;
+        const int* xp = (const int*)x;
+        for (int k = 0; k < 8; k++) {
+            const int wq = *(const int*)(qs + 4 * k);
+            c = uq_dot4(h ? Q4K::hi4(wq) : Q4K::lo4(wq), xp[k], c);
+        }
+    } else {
+        const int64_t sb = (row * (K / 256)) + b / 16;
+        const int s = (int)(b % 16), n = s >> 3, j = (s >> 1) & 3, h = s & 1;
+        const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
+        const int* xp = (const int*)x;
+        for (int k = 0; k < 4; k++) {
+            const unsigned qv = *(const unsigned*)(blk + 32 + 32 * n + 16 * h + 4 * k);
+            const unsigned hv = *(const unsigned*)(blk + 16 * h + 4 * k);
+            const int v = (int)(((qv >> (2 * j)) & 0x03030303u) | (((hv >> (4 * n + j)) & 0x01010101u) << 2));
+            c = uq_dot4(v, xp[k], c);
+            c -= 4 * uq_dot4(0x01010101, xp[k], 0);
+        }
+    }
+    dots[i] = c;
+}
+
+inline unsigned grid_for(int64_t items, int per_block) {
+    return (unsigned)((items + per_block - 1) / per_block);
+}
+
+template <class KQ, int LPR, int NBL>
+void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
+    constexpr int RPB = (64 / LPR) * (WG / 64);
+    int64_t sets = (w.m + RPB - 1) / RPB;
+    const unsigned grid = (unsigned)(sets < 2048 ? sets : 2048);
+    WArgs a{w.qs, w.d, w.sc}, b{nullptr, nullptr, nullptr};
+    if (w2) {
+        b = WArgs{w2->qs, w2->d, w2->sc};
+        hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+    } else {
+        hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+    }
+}
+
+// Lane-group size per row from the number of units per row: small rows use
+// short groups (more rows per wave), long rows spread over a full wave.
+template <class KQ>
+int launch_kind(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
+    const int64_t nu = w.n / KQ::UNIT;
+#define UQ_TRY(L, B) \
+    if (nu <= (int64_t)(L) * (B)) { launch_t<KQ, L, B>(w, w2, xq, xs, y, s); return OK; }
+    UQ_TRY(4, 1) UQ_TRY(4, 2)
+    UQ_TRY(8, 1) UQ_TRY(8, 2) UQ_TRY(8, 3)
+    UQ_TRY(16, 2) UQ_TRY(16, 3) UQ_TRY(16, 4)
+    UQ_TRY(32, 3) UQ_TRY(32, 4)
+    UQ_TRY(64, 3) UQ_TRY(64, 4) UQ_TRY(64, 5) UQ_TRY(64, 6) UQ_TRY(64, 7) UQ_TRY(64, 8)
+#undef UQ_TRY
+    return set_error(ERR_SHAPE, "matvec: input length too large");
+}
+
+}  // namespace
+
+void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s) {
+    hipLaunchKernelGGL(k_quant_act, dim3(grid_for(n, WG)), dim3(WG), 0, s, x, n, xq, xs);
+}
+void launch_q8_repack(const uint8_t* gguf, int64_t rows, int64_t nb, int8_t* qs, uint16_t* d, hipStream_t s) {
+    hipLaunchKernelGGL(k_q8_repack, dim3(grid_for(rows * nb, WG)), dim3(WG), 0, s, gguf, rows, nb, qs, d);
+}
+void launch_q8_verify(const int8_t* qs, const uint16_t* d, const uint8_t* gguf, int64_t rows, int64_t nb,
+                      unsigned* bad, hipStream_t s) {
+    hipLaunchKernelGGL(k_q8_verify, dim3(grid_for(rows * nb, WG)), dim3(WG), 0, s, qs, d, gguf, rows, nb, bad);
+}
+void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s) {
+    hipLaunchKernelGGL(k_q3k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, sc, d);
+}
+void launch_q3k_verify(const int8_t* q, const uint8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
+                       unsigned* bad, hipStream_t s) {
+    hipLaunchKernelGGL(k_q3k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, sc, d, gguf, blocks, bad);
+}
+
+int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
+    if (w2 && (w2->kind != w.kind || w2->n != w.n || w2->m != w.m))
+        return set_error(ERR_SHAPE, "gate/up pair: shapes differ");
+    switch (w.kind) {
+    case KIND_Q8_0: return launch_kind<Q8>(w, w2, xq, xs, y, s);
+    case KIND_Q4_K: return launch_kind<Q4K>(w, w2, xq, xs, y, s);
+    case KIND_Q3_K: return launch_kind<Q3K>(w, w2, xq, xs, y, s);
+    default: return set_error(ERR_QUANT_TYPE, "matvec: unsupported kind");
+    }
+}
+
+int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s) {
+    const int bsz = w.kind == KIND_Q3_K ? 16 : 32;
+    const int64_t items = w.m * (w.n / bsz);
+    WArgs a{w.qs, w.d, w.sc};
+    hipLaunchKernelGGL(k_block_dots, dim3(grid_for(items, WG)), dim3(WG), 0, s, a, w.kind, xq, dots, w.m, w.n);
+    return OK;
+}
+
+}  // namespace uq

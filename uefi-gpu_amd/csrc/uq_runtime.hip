@@ -1,0 +1,417 @@
+// Host runtime of the library: process context, device-resident weights and
+// the synchronous linear calls of the reference's `Gpu` (driver/src/llm.rs:110-273).
+//
+// The reference submits hand-packed QMDs through a GPFIFO and polls sysmem
+// semaphores; here one HIP stream per process carries every launch and
+// hipStreamSynchronize is the completion poll.
+#include "uq_internal.h"
+#include "../../include/uq.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace uq {
+
+namespace {
+thread_local std::string g_error;
+
+struct Context {
+    bool ready = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    // staging for the host-pointer linears: x, quantized x, outputs
+    float* dx = nullptr;
+    int8_t* dxq = nullptr;
+    float* dxs = nullptr;
+    float* dy = nullptr;
+    size_t y_cap = 0;
+    unsigned* dcount = nullptr;
+};
+Context g_ctx;
+
+constexpr int64_t MAX_N = 16384;    // llm.rs:248 n<=16384
+constexpr int64_t MAX_M = 160000;   // llm.rs:248 m<=160000
+}  // namespace
+
+int set_error(int status, const std::string& msg) {
+    g_error = msg;
+    return status;
+}
+
+int64_t row_bytes(uint32_t kind, int64_t n) {
+    int64_t block, bytes;
+    switch (kind) {
+    case KIND_F32: block = 1; bytes = 4; break;
+    case KIND_Q8_0: block = 32; bytes = 34; break;
+    case KIND_Q4_K: block = 256; bytes = 144; break;
+    case KIND_Q3_K: block = 256; bytes = 110; break;
+    default: return ERR_QUANT_TYPE;
+    }
+    if (n <= 0 || n % block) return ERR_SHAPE;
+    return n / block * bytes;
+}
+
+static int require_ctx() {
+    if (!g_ctx.ready) return set_error(ERR_ARG, "uq_init has not been called");
+    return OK;
+}
+
+static int ensure_y(size_t m) {
+    if (m <= g_ctx.y_cap) return OK;
+    if (g_ctx.dy) UQ_CHECK_HIP(hipFree(g_ctx.dy));
+    g_ctx.dy = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&g_ctx.dy, sizeof(float) * 3 * m));
+    g_ctx.y_cap = m;
+    return OK;
+}
+
+static hipStream_t pick(void* s) { return s ? (hipStream_t)s : g_ctx.stream; }
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace uq
+
+using namespace uq;
+
+struct uq_weight {
+    Weight w;
+};
+
+extern "C" {
+
+const char* uq_last_error(void) { return uq::g_error.c_str(); }
+
+int uq_init(int device) {
+    if (g_ctx.ready) {
+        if (g_ctx.device == device) return OK;
+        return set_error(ERR_ARG, "uq_init: already initialised on another device");
+    }
+    int count = 0;
+    UQ_CHECK_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return set_error(ERR_ARG, "uq_init: no such device");
+    UQ_CHECK_HIP(hipSetDevice(device));
+    UQ_CHECK_HIP(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
+    UQ_CHECK_HIP(hipMalloc(&g_ctx.dx, sizeof(float) * MAX_N));
+    UQ_CHECK_HIP(hipMalloc(&g_ctx.dxq, MAX_N));
+    UQ_CHECK_HIP(hipMalloc(&g_ctx.dxs, sizeof(float) * (MAX_N / 32)));
+    UQ_CHECK_HIP(hipMalloc(&g_ctx.dcount, sizeof(unsigned) * 4));
+    g_ctx.device = device;
+    g_ctx.ready = true;
+    return OK;
+}
+
+int uq_shutdown(void) {
+    if (!g_ctx.ready) return OK;
+    hipStreamSynchronize(g_ctx.stream);
+    hipFree(g_ctx.dx);
+    hipFree(g_ctx.dxq);
+    hipFree(g_ctx.dxs);
+    hipFree(g_ctx.dy);
+    hipFree(g_ctx.dcount);
+    hipStreamDestroy(g_ctx.stream);
+    g_ctx = Context{};
+    return OK;
+}
+
+void* uq_stream(void) { return (void*)g_ctx.stream; }
+
+int uq_sync(void) {
+    if (int rc = require_ctx()) return rc;
+    UQ_CHECK_HIP(hipStreamSynchronize(g_ctx.stream));
+    return OK;
+}
+
+int64_t uq_row_bytes(uint32_t kind, int64_t n) { return uq::row_bytes(kind, n); }
+
+int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, uq_weight_t* out) {
+    if (int rc = require_ctx()) return rc;
+    if (!gguf || !out) return set_error(ERR_ARG, "weight_upload: null pointer");
+    if (kind != KIND_Q8_0 && kind != KIND_Q4_K && kind != KIND_Q3_K)
+        return set_error(ERR_QUANT_TYPE, "weight_upload: kind must be Q8_0, Q4_K or Q3_K");
+    const int64_t rb = uq::row_bytes(kind, n);
+    if (rb < 0 || m <= 0 || n > MAX_N || m > MAX_M)
+        return set_error(ERR_SHAPE, "weight_upload: bad shape");
+    if ((int64_t)bytes != rb * m) return set_error(ERR_SHAPE, "weight_upload: byte count != rows * row_bytes");
+    hipStream_t s = g_ctx.stream;
+    Weight w;
+    w.kind = kind;
+    w.n = n;
+    w.m = m;
+    w.gguf_bytes = rb * m;
+    size_t total = 0;
+    size_t off_q = 0, off_d = 0, off_sc = 0;
+    if (kind == KIND_Q8_0) {
+        off_q = 0;
+        off_d = align256((size_t)(n * m));
+        total = off_d + align256((size_t)(n / 32 * m) * 2);
+    } else if (kind == KIND_Q4_K) {
+        total = align256((size_t)(rb * m));
+    } else {
+        const size_t blocks = (size_t)(n / 256 * m);
+        off_q = 0;
+        off_sc = align256(blocks * 96);
+        off_d = off_sc + align256(blocks * 12);
+        total = off_d + align256(blocks * 2);
+    }
+    UQ_CHECK_HIP(hipMalloc(&w.alloc, total));
+    w.alloc_bytes = total;
+    uint8_t* base = (uint8_t*)w.alloc;
+    w.qs = (const int8_t*)(base + off_q);
+    if (kind != KIND_Q4_K) w.d = (const uint16_t*)(base + off_d);
+    if (kind == KIND_Q3_K) w.sc = base + off_sc;
+    int rc = OK;
+    if (kind == KIND_Q4_K) {
+        // superblocks are used as stored; the readback check is a plain compare
+        hipError_t e = hipMemcpyAsync(base, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) {
+            std::vector<uint8_t> back((size_t)w.gguf_bytes);
+            e = hipMemcpyAsync(back.data(), base, back.size(), hipMemcpyDeviceToHost, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e == hipSuccess && std::memcmp(back.data(), gguf, back.size()) != 0)
+                rc = set_error(ERR_DEVICE, "weight_upload: readback mismatch");
+        }
+        if (e != hipSuccess) rc = set_error(ERR_DEVICE, std::string("weight_upload: ") + hipGetErrorString(e));
+    } else {
+        void* staging = nullptr;
+        hipError_t e = hipMalloc(&staging, (size_t)w.gguf_bytes);
+        if (e == hipSuccess) e = hipMemcpyAsync(staging, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemsetAsync(g_ctx.dcount, 0, sizeof(unsigned), s);
+        if (e == hipSuccess) {
+            if (kind == KIND_Q8_0) {
+                launch_q8_repack((const uint8_t*)staging, m, n / 32, (int8_t*)w.qs, (uint16_t*)w.d, s);
+                launch_q8_verify(w.qs, w.d, (const uint8_t*)staging, m, n / 32, g_ctx.dcount, s);
+            } else {
+                const int64_t blocks = n / 256 * m;
+                launch_q3k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, (uint16_t*)w.d, s);
+                launch_q3k_verify(w.qs, w.sc, w.d, (const uint8_t*)staging, blocks, g_ctx.dcount, s);
+            }
+            e = hipGetLastError();
+        }
+        unsigned bad = 0;
+        if (e == hipSuccess) e = hipMemcpyAsync(&bad, g_ctx.dcount, sizeof(unsigned), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (staging) hipFree(staging);
+        if (e != hipSuccess) rc = set_error(ERR_DEVICE, std::string("weight_upload: ") + hipGetErrorString(e));
+        else if (bad) rc = set_error(ERR_DEVICE, "weight_upload: repack verify found " + std::to_string(bad) + " differing bytes");
+    }
+    if (rc != OK) {
+        hipFree(w.alloc);
+        return rc;
+    }
+    *out = new uq_weight{w};
+    return OK;
+}
+
+int uq_weight_free(uq_weight_t w) {
+    if (!w) return OK;
+    hipStreamSynchronize(g_ctx.stream);
+    hipFree(w->w.alloc);
+    delete w;
+    return OK;
+}
+
+int64_t uq_weight_bytes(uq_weight_t w) { return w ? (int64_t)w->w.alloc_bytes : ERR_ARG; }
+
+static int check_x(const float* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++)
+        if (!std::isfinite(x[i])) return set_error(ERR_NONFINITE, "input contains a non-finite value");
+    return OK;
+}
+
+int uq_quant_act_dev(const float* x, int64_t n, int8_t* xq, float* xs, void* stream) {
+    if (int rc = require_ctx()) return rc;
+    if (!x || !xq || !xs) return set_error(ERR_ARG, "quant_act_dev: null pointer");
+    if (n <= 0 || n % 32) return set_error(ERR_SHAPE, "quant_act_dev: n must be a positive multiple of 32");
+    launch_quant_act(x, n, xq, xs, pick(stream));
+    UQ_CHECK_HIP(hipGetLastError());
+    return OK;
+}
+
+int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, void* stream) {
+    if (int rc = require_ctx()) return rc;
+    if (!w || !xq || !xs || !y) return set_error(ERR_ARG, "matvec_q_dev: null pointer");
+    if (int rc = launch_matvec(w->w, nullptr, xq, xs, y, pick(stream))) return rc;
+    UQ_CHECK_HIP(hipGetLastError());
+    return OK;
+}
+
+int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream) {
+    if (int rc = require_ctx()) return rc;
+    if (!gate || !up || !xq || !xs || !out) return set_error(ERR_ARG, "gateup_q_dev: null pointer");
+    if (int rc = launch_matvec(gate->w, &up->w, xq, xs, out, pick(stream))) return rc;
+    UQ_CHECK_HIP(hipGetLastError());
+    return OK;
+}
+
+int uq_batch(const uq_weight_t* ws, int count, const float* x, int64_t n, float* const* ys, const int64_t* ms) {
+    if (int rc = require_ctx()) return rc;
+    if (!ws || !x || !ys || !ms || count < 1 || count > 3) return set_error(ERR_SHAPE, "batch: 1..3 tensors");
+    int64_t total = 0;
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !ys[i]) return set_error(ERR_ARG, "batch: null tensor or output");
+        if (ws[i]->w.n != n || ws[i]->w.m != ms[i]) return set_error(ERR_SHAPE, "batch: tensor shape != x/y lengths");
+        total += ms[i];
+    }
+    if (n > MAX_N) return set_error(ERR_SHAPE, "batch: n > 16384");
+    if (int rc = check_x(x, n)) return rc;
+    if (int rc = ensure_y((size_t)total)) return rc;
+    hipStream_t s = g_ctx.stream;
+    UQ_CHECK_HIP(hipMemcpyAsync(g_ctx.dx, x, sizeof(float) * n, hipMemcpyHostToDevice, s));
+    launch_quant_act(g_ctx.dx, n, g_ctx.dxq, g_ctx.dxs, s);
+    int64_t off = 0;
+    for (int i = 0; i < count; i++) {
+        if (int rc = launch_matvec(ws[i]->w, nullptr, g_ctx.dxq, g_ctx.dxs, g_ctx.dy + off, s)) return rc;
+        off += ms[i];
+    }
+    UQ_CHECK_HIP(hipGetLastError());
+    std::vector<float> host((size_t)total);
+    UQ_CHECK_HIP(hipMemcpyAsync(host.data(), g_ctx.dy, sizeof(float) * total, hipMemcpyDeviceToHost, s));
+    UQ_CHECK_HIP(hipStreamSynchronize(s));
+    off = 0;
+    for (int i = 0; i < count; i++) {
+        std::memcpy(ys[i], host.data() + off, sizeof(float) * ms[i]);
+        off += ms[i];
+    }
+    if (int rc = check_x(host.data(), total)) return set_error(rc, "batch: non-finite output");
+    return OK;
+}
+
+int uq_matvec(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m) {
+    float* ys[1] = {y};
+    int64_t ms[1] = {m};
+    return uq_batch(&w, 1, x, n, ys, ms);
+}
+
+int uq_quant_act(const float* x, int64_t n, int8_t* q, float* scale) {
+    if (int rc = require_ctx()) return rc;
+    if (!x || !q || !scale) return set_error(ERR_ARG, "quant_act: null pointer");
+    if (n <= 0 || n % 32 || n > MAX_N) return set_error(ERR_SHAPE, "quant_act: n must be a multiple of 32, <= 16384");
+    hipStream_t s = g_ctx.stream;
+    UQ_CHECK_HIP(hipMemcpyAsync(g_ctx.dx, x, sizeof(float) * n, hipMemcpyHostToDevice, s));
+    launch_quant_act(g_ctx.dx, n, g_ctx.dxq, g_ctx.dxs, s);
+    UQ_CHECK_HIP(hipGetLastError());
+    UQ_CHECK_HIP(hipMemcpyAsync(q, g_ctx.dxq, n, hipMemcpyDeviceToHost, s));
+    UQ_CHECK_HIP(hipMemcpyAsync(scale, g_ctx.dxs, sizeof(float) * (n / 32), hipMemcpyDeviceToHost, s));
+    UQ_CHECK_HIP(hipStreamSynchronize(s));
+    return OK;
+}
+
+int uq_block_dots(uq_weight_t w, const float* x, int64_t n, int32_t* dots, int64_t count) {
+    if (int rc = require_ctx()) return rc;
+    if (!w || !x || !dots) return set_error(ERR_ARG, "block_dots: null pointer");
+    if (w->w.n != n) return set_error(ERR_SHAPE, "block_dots: x length != tensor n");
+    const int bsz = w->w.kind == KIND_Q3_K ? 16 : 32;
+    if (count != w->w.m * (n / bsz)) return set_error(ERR_SHAPE, "block_dots: wrong output count");
+    hipStream_t s = g_ctx.stream;
+    int32_t* d = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&d, sizeof(int32_t) * count));
+    int rc = OK;
+    hipError_t e = hipMemcpyAsync(g_ctx.dx, x, sizeof(float) * n, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) {
+        launch_quant_act(g_ctx.dx, n, g_ctx.dxq, g_ctx.dxs, s);
+        rc = launch_block_dots(w->w, g_ctx.dxq, d, s);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess && rc == OK) e = hipMemcpyAsync(dots, d, sizeof(int32_t) * count, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    hipFree(d);
+    if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("block_dots: ") + hipGetErrorString(e));
+    return rc;
+}
+
+int uq_dev_alloc(size_t bytes, void** ptr) {
+    if (int rc = require_ctx()) return rc;
+    if (!ptr) return set_error(ERR_ARG, "dev_alloc: null pointer");
+    UQ_CHECK_HIP(hipMalloc(ptr, bytes ? bytes : 1));
+    return OK;
+}
+int uq_dev_free(void* ptr) {
+    if (ptr) {
+        hipStreamSynchronize(g_ctx.stream);
+        UQ_CHECK_HIP(hipFree(ptr));
+    }
+    return OK;
+}
+int uq_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (int rc = require_ctx()) return rc;
+    UQ_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(g_ctx.stream));
+    return OK;
+}
+int uq_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (int rc = require_ctx()) return rc;
+    UQ_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(g_ctx.stream));
+    return OK;
+}
+
+int uq_time_matvecs(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
+                    int probe, double* total_ms, double* probe_ms) {
+    if (int rc = require_ctx()) return rc;
+    if (!ws || count <= 0 || reps <= 0 || warmup < 0 || !total_ms) return set_error(ERR_ARG, "time_matvecs: bad args");
+    hipStream_t s = g_ctx.stream;
+    int64_t ymax = 0;
+    for (int i = 0; i < count; i++) {
+        if (!ws[i]) return set_error(ERR_ARG, "time_matvecs: null weight");
+        if (ws[i]->w.n > max_n) return set_error(ERR_SHAPE, "time_matvecs: weight n > max_n");
+        if (ws[i]->w.m > ymax) ymax = ws[i]->w.m;
+    }
+    // a seeded-constant activation: 0.5 everywhere except a ramp, quantized once
+    std::vector<float> hx((size_t)max_n);
+    for (int64_t i = 0; i < max_n; i++) hx[i] = (float)((i * 37) % 251) / 125.0f - 1.0f;
+    float *x = nullptr, *y = nullptr, *xs = nullptr;
+    int8_t* xq = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&x, sizeof(float) * max_n));
+    UQ_CHECK_HIP(hipMalloc(&xq, max_n));
+    UQ_CHECK_HIP(hipMalloc(&xs, sizeof(float) * (max_n / 32)));
+    UQ_CHECK_HIP(hipMalloc(&y, sizeof(float) * ymax));
+    UQ_CHECK_HIP(hipMemcpyAsync(x, hx.data(), sizeof(float) * max_n, hipMemcpyHostToDevice, s));
+    launch_quant_act(x, max_n, xq, xs, s);
+    std::vector<hipEvent_t> pev;
+    hipEvent_t t0, t1;
+    UQ_CHECK_HIP(hipEventCreate(&t0));
+    UQ_CHECK_HIP(hipEventCreate(&t1));
+    const int nprobe = probe >= 0 ? reps : 0;
+    pev.resize(2 * (size_t)nprobe);
+    for (auto& e : pev) UQ_CHECK_HIP(hipEventCreate(&e));
+    int rc = OK;
+    for (int r = 0; r < warmup + reps && rc == OK; r++) {
+        const bool timed = r >= warmup;
+        if (r == warmup) UQ_CHECK_HIP(hipEventRecord(t0, s));
+        for (int i = 0; i < count && rc == OK; i++) {
+            const bool pair = pairs && pairs[i] && i + 1 < count;
+            const bool rec = timed && i == probe;
+            if (rec) UQ_CHECK_HIP(hipEventRecord(pev[2 * (r - warmup)], s));
+            rc = launch_matvec(ws[i]->w, pair ? &ws[i + 1]->w : nullptr, xq, xs, y, s);
+            if (rec) UQ_CHECK_HIP(hipEventRecord(pev[2 * (r - warmup) + 1], s));
+            if (pair) i++;
+        }
+    }
+    UQ_CHECK_HIP(hipEventRecord(t1, s));
+    UQ_CHECK_HIP(hipEventSynchronize(t1));
+    float ms = 0;
+    UQ_CHECK_HIP(hipEventElapsedTime(&ms, t0, t1));
+    *total_ms = ms;
+    if (probe_ms) {
+        double sum = 0;
+        for (int r = 0; r < nprobe; r++) {
+            float p = 0;
+            UQ_CHECK_HIP(hipEventElapsedTime(&p, pev[2 * r], pev[2 * r + 1]));
+            sum += p;
+        }
+        *probe_ms = nprobe ? sum / nprobe : 0.0;
+    }
+    for (auto& e : pev) hipEventDestroy(e);
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    hipFree(x);
+    hipFree(xq);
+    hipFree(xs);
+    hipFree(y);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,262 @@
+"""Python binding of libuq.so (the C ABI declared in include/uq.h).
+
+A thin ctypes layer for tests and the benchmark, plus host-side helpers that
+mirror the reference runtime's call surface (driver/src/llm.rs:63 ``Tensor``,
+:226 ``Gpu::batch``, :246 ``Gpu::matvec``; frontier_forward.rs:10 ``Error``).
+
+The library must be built (``python uefi-gpu_amd/build_lib.py`` or
+``__graft_entry__.build()``); importing this module never falls back to any
+CPU path: a missing library raises ``UqError``.
+"""
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libuq.so")
+
+OK = 0
+KIND_F32, KIND_Q8_0, KIND_Q3_K, KIND_Q4_K = 0, 8, 11, 12
+
+
+class Error(enum.IntEnum):
+    """Status codes (frontier_forward.rs:10 Error, frontier_core.rs:37 QuantType)."""
+    SHAPE = -1
+    QUANT_TYPE = -2
+    NONFINITE = -3
+    DEVICE = -4
+    TIMEOUT = -5
+    CONTEXT = -6
+    ARG = -7
+
+
+class UqError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__("%s: %s" % (Error(status).name if status in Error._value2member_map_ else status, msg))
+        self.status = status
+
+
+_lib = None
+
+_c_f32p = ctypes.POINTER(ctypes.c_float)
+_c_i8p = ctypes.POINTER(ctypes.c_int8)
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_u8p = ctypes.POINTER(ctypes.c_uint8)
+_c_u32p = ctypes.POINTER(ctypes.c_uint32)
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "uq_init": (ctypes.c_int, [ctypes.c_int]),
+    "uq_shutdown": (ctypes.c_int, []),
+    "uq_last_error": (ctypes.c_char_p, []),
+    "uq_stream": (_vp, []),
+    "uq_sync": (ctypes.c_int, []),
+    "uq_row_bytes": (_i64, [ctypes.c_uint32, _i64]),
+    "uq_weight_upload": (ctypes.c_int, [ctypes.c_uint32, _i64, _i64, _vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "uq_weight_free": (ctypes.c_int, [_vp]),
+    "uq_weight_bytes": (_i64, [_vp]),
+    "uq_matvec": (ctypes.c_int, [_vp, _c_f32p, _i64, _c_f32p, _i64]),
+    "uq_batch": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _c_f32p, _i64, ctypes.POINTER(_c_f32p), _c_i64p]),
+    "uq_quant_act_dev": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
+    "uq_matvec_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "uq_gateup_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "uq_quant_act": (ctypes.c_int, [_c_f32p, _i64, _c_i8p, _c_f32p]),
+    "uq_block_dots": (ctypes.c_int, [_vp, _c_f32p, _i64, _c_i32p, _i64]),
+    "uq_dev_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "uq_dev_free": (ctypes.c_int, [_vp]),
+    "uq_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
+    "uq_memcpy_d2h": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
+    "uq_time_matvecs": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int), ctypes.c_int, _i64,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
+    "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
+    "uq_synth_tokens": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_uint32, _c_u32p]),
+}
+
+
+def declared_symbols():
+    return sorted(_SIGS)
+
+
+def lib():
+    """Load libuq.so (raises UqError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise UqError(Error.ARG, "libuq.so not built at %s (run __graft_entry__.build())" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != OK:
+        raise UqError(rc, lib().uq_last_error().decode(errors="replace"))
+    return rc
+
+
+def _p(a, ct):
+    return a.ctypes.data_as(ct)
+
+
+def init(device=0):
+    _check(lib().uq_init(device))
+
+
+def shutdown():
+    _check(lib().uq_shutdown())
+
+
+def row_bytes(kind, n):
+    return int(lib().uq_row_bytes(kind, n))
+
+
+# ---------------------------------------------------------------- synthetic data
+def synth_quant(kind, seed, rows, n):
+    out = np.empty(rows * row_bytes(kind, n), dtype=np.uint8)
+    _check(lib().uq_synth_quant(kind, seed & (2**64 - 1), rows, n, _p(out, _c_u8p)))
+    return out
+
+
+def synth_normal(seed, n, mean=0.0, std=1.0):
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().uq_synth_normal(seed & (2**64 - 1), n, mean, std, _p(out, _c_f32p)))
+    return out
+
+
+def synth_tokens(seed, n, vocab):
+    out = np.empty(n, dtype=np.uint32)
+    _check(lib().uq_synth_tokens(seed & (2**64 - 1), n, vocab, _p(out, _c_u32p)))
+    return out
+
+
+def fnv1a64(text):
+    h = 0xCBF29CE484222325
+    for b in text.encode():
+        h = ((h ^ b) * 0x100000001B3) & (2**64 - 1)
+    return h
+
+
+def tensor_seed(base, name):
+    """Per-tensor seed of a synthetic model: base mixed with FNV-1a of the GGUF name."""
+    return ((base * 0x9E3779B97F4A7C15) ^ fnv1a64(name)) & (2**64 - 1)
+
+
+# ---------------------------------------------------------------- weights / linears
+class Weight:
+    """A device-resident, verified, repacked GGUF tensor (uq_weight_t)."""
+
+    def __init__(self, kind, n, m, gguf_bytes):
+        self.kind, self.n, self.m = kind, int(n), int(m)
+        buf = np.ascontiguousarray(gguf_bytes, dtype=np.uint8)
+        h = _vp()
+        _check(lib().uq_weight_upload(kind, self.n, self.m, buf.ctypes.data, buf.nbytes, ctypes.byref(h)))
+        self.handle = h
+
+    def free(self):
+        if self.handle:
+            lib().uq_weight_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    @property
+    def device_bytes(self):
+        return int(lib().uq_weight_bytes(self.handle))
+
+
+def matvec(w, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(w.m, dtype=np.float32)
+    _check(lib().uq_matvec(w.handle, _p(x, _c_f32p), x.size, _p(y, _c_f32p), y.size))
+    return y
+
+
+def batch(ws, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ys = [np.empty(w.m, dtype=np.float32) for w in ws]
+    handles = (_vp * len(ws))(*[w.handle for w in ws])
+    yp = (_c_f32p * len(ws))(*[_p(y, _c_f32p) for y in ys])
+    ms = (ctypes.c_int64 * len(ws))(*[w.m for w in ws])
+    _check(lib().uq_batch(handles, len(ws), _p(x, _c_f32p), x.size, yp, ms))
+    return ys
+
+
+def quant_act(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.size, dtype=np.int8)
+    s = np.empty(x.size // 32, dtype=np.float32)
+    _check(lib().uq_quant_act(_p(x, _c_f32p), x.size, _p(q, _c_i8p), _p(s, _c_f32p)))
+    return q, s
+
+
+def block_dots(w, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    bsz = 16 if w.kind == KIND_Q3_K else 32
+    d = np.empty(w.m * (w.n // bsz), dtype=np.int32)
+    _check(lib().uq_block_dots(w.handle, _p(x, _c_f32p), x.size, _p(d, _c_i32p), d.size))
+    return d.reshape(w.m, w.n // bsz)
+
+
+def time_matvecs(weights, pairs, max_n, reps, warmup, probe):
+    hs = (_vp * len(weights))(*[w.handle for w in weights])
+    pr = (ctypes.c_int * len(weights))(*pairs)
+    tot, pm = ctypes.c_double(), ctypes.c_double()
+    _check(lib().uq_time_matvecs(hs, pr, len(weights), max_n, reps, warmup, probe, ctypes.byref(tot), ctypes.byref(pm)))
+    return tot.value, pm.value
+
+
+# ---------------------------------------------------------------- reference-shaped host API
+class Tensor:
+    """Tensor{name, n, m, typ, off} of driver/src/llm.rs:63 (n = columns, m = rows)."""
+
+    def __init__(self, name, n, m, typ, data):
+        self.name, self.n, self.m, self.typ, self.data = name, n, m, typ, data
+
+
+class Gpu:
+    """The reference's linear call surface (llm.rs:226-273) over libuq.
+
+    ``matvec``/``batch`` return False on any failure, as the reference does;
+    ``last_error`` keeps the message.
+    """
+
+    def __init__(self, device=0):
+        init(device)
+        self.weights = {}
+        self.last_error = ""
+
+    def upload(self, t):
+        self.weights[t.name] = Weight(t.typ, t.n, t.m, t.data)
+
+    def matvec(self, t, x, y):
+        return self.batch([t], x, [y])
+
+    def batch(self, tensors, x, ys):
+        if len(tensors) != len(ys) or not 1 <= len(tensors) <= 3:
+            return False
+        try:
+            for t, y in zip(tensors, ys):
+                if t.n != len(x) or t.m != len(y):
+                    return False
+            outs = batch([self.weights[t.name] for t in tensors], x)
+        except (UqError, KeyError) as e:
+            self.last_error = str(e)
+            return False
+        for y, o in zip(ys, outs):
+            y[:] = o
+        return True

@@ -80,6 +80,31 @@ def cpu_baseline(seconds=10.0):
                       % (passes, el, cpu_model(), os.cpu_count() or 0)}
 
 
+def decode_bench(prompt_len=512, steps=128):
+    """Qwen2.5-1.5B-architecture Q8_0 greedy decode, bs=1: the prompt of seeded
+    uniform ids fills the fp16 KV cache, then `steps` decode steps (one hipGraph
+    launch each, greedy id fed back on the device) are timed with HIP events."""
+    cfg = dict(uq.QWEN25_15B, max_seq=1024)
+    t0 = time.perf_counter()
+    model = uq.Qwen2Model(cfg, uq.synth_qwen2(cfg, 0x5EED0002))
+    t_load = time.perf_counter() - t0
+    prompt = uq.synth_tokens(0x5EED0002, prompt_len, cfg["vocab"])
+    t0 = time.perf_counter()
+    first = model.prompt(prompt, 0)
+    t_prompt = time.perf_counter() - t0
+    model.decode_run(first, prompt_len, 8)          # warm-up over the same positions
+    ids, ms = model.decode_run(first, prompt_len, steps)
+    weight_bytes = 28 * 49717248 + 247959552
+    kv_bytes = sum(28 * 2 * (prompt_len + i + 1) * 256 * 2 for i in range(steps))
+    tok_s = steps / (ms / 1e3)
+    model.free()
+    return {"tok_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "prompt": prompt_len,
+            "steps": steps, "model_upload_s": round(t_load, 1), "prompt_ingest_s": round(t_prompt, 2),
+            "weight_bytes_per_token": weight_bytes,
+            "effective_GBs": round((weight_bytes * steps + kv_bytes) / (ms / 1e3) / 1e9, 1),
+            "first_ids": [int(i) for i in ids[:8]]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +112,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus %d is not supported "
@@ -103,7 +129,8 @@ def main():
                 pairs.append(1 if (pair and i == 0) else 0)
                 shape_of.append((name, N, K, pair))
     per_copy = len(weights) // args.copies
-    step_bytes = sum(q8_bytes(N, K) * (2 if pair else 1) - (K + K // 32 * 4 if pair else 0)
+    # a fused pair reads two weight matrices and one activation, writes one output
+    step_bytes = sum(q8_bytes(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else q8_bytes(N, K)
                      for _, N, K, pair in SHAPES)
     lm_index = [i for i, s in enumerate(shape_of) if s[0] == "lm_head"][0]
     # one timed "round" in uq_time_matvecs = every copy once = `copies` steps
@@ -130,6 +157,13 @@ def main():
                      "kernel": "Q8_0 matvec, lm_head 151936x1536 (%d B per launch), mean of %d launches %.4f ms"
                                % (lm_bytes, rounds, lm_ms)},
     }
+    read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
+    result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
+                           "note": "plain int4 streaming read / copy of 1 GiB, same box"}
+    for w in weights:
+        w.free()
+    if not args.no_decode:
+        result["decode"] = decode_bench()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -106,6 +106,49 @@ int uq_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int uq_time_matvecs(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
                     int probe, double* total_ms, double* probe_ms);
 
+/* Achievable-bandwidth probe (no reference counterpart; measurement aid): a
+ * streaming read of `bytes` and a copy of `bytes` (read + write counted),
+ * `reps` launches each, GB/s from HIP events. */
+int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_gbs);
+
+/* ---------------------------------------------------------------- Qwen2 dense decoder */
+/* Model shape constants of driver/src/llm.rs:314-321 (DIM, HIDDEN, KV, HEAD,
+ * SEQ, LAYERS) as a runtime description. */
+typedef struct {
+    int32_t layers, dim, hidden, heads, kv_heads, head_dim, vocab, max_seq;
+    float eps, theta;
+} uq_qwen2_config;
+typedef struct uq_model* uq_model_t;
+
+/* Arena allocation of init_graph (gpu_graph.rs:81-87). Requires uq_init. */
+int uq_model_create(const uq_qwen2_config* cfg, uq_model_t* out);
+int uq_model_free(uq_model_t m);
+/* upload_weights (llm.rs:157-201) for one GGUF tensor by name
+ * ("token_embd.weight", "output.weight", "output_norm.weight",
+ * "blk.N.attn_{q,k,v,output}.weight", "blk.N.ffn_{gate,up,down}.weight",
+ * "blk.N.{attn,ffn}_norm.weight", "blk.N.attn_{q,k,v}.bias"): Q8_0 matrices
+ * (n columns, rows) or F32 vectors (rows == 1). Biases are optional. */
+int uq_model_set_tensor(uq_model_t m, const char* name, uint32_t kind, int64_t n, int64_t rows, const void* data,
+                        size_t bytes);
+/* init_graph (gpu_graph.rs:81-169): checks every tensor, builds the RoPE table
+ * (gpu_graph.rs:131-133) and captures one decode step into a hipGraph. */
+int uq_model_prepare(uq_model_t m);
+/* forward_gpu (gpu_graph.rs:170-197): one decode step of `token` at `pos`,
+ * writes the greedy next id; non-finite logits -> UQ_ERR_NONFINITE. */
+int uq_decode_step(uq_model_t m, uint32_t token, int pos, uint32_t* next);
+/* The decode loop of generate_one (llm.rs:422-428) with the greedy id fed back
+ * on the device: `steps` graph launches from (token, pos), tokens[i] = id
+ * produced at position pos+i; ms (optional) = hipEvent time of the launches. */
+int uq_decode_run(uq_model_t m, uint32_t token, int pos, int steps, uint32_t* tokens, double* ms);
+/* Prompt ingestion through the decode graph, one launch per prompt token at
+ * positions pos..pos+count-1 (the per-token forward of llm.rs:339-388); next =
+ * greedy id after the last prompt token. */
+int uq_prompt_tokens(uq_model_t m, const uint32_t* tokens, int count, int pos, uint32_t* next);
+/* LOGITS readback of verify_gpu_greedy (gpu_graph.rs:14-23). */
+int uq_model_logits(uq_model_t m, float* out, int64_t n);
+/* fp16 KV cache readback of positions [0, count) of one layer ([count][kv*hd]). */
+int uq_model_kv(uq_model_t m, int layer, int count, uint16_t* keys, uint16_t* values);
+
 #ifdef __cplusplus
 }
 #endif

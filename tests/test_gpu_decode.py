@@ -1,0 +1,102 @@
+"""GPU decode step (hipGraph) against the oracle decoder, through the C ABI.
+
+Every reduction on both sides accumulates exactly formed terms in double and
+rounds once, so logits, KV cache contents and greedy ids are expected to agree
+bit for bit; the assertions allow at most 1 ulp on logits (rounding of a sum
+that lands within 2^-29 of a tie) and require identical greedy ids."""
+import numpy as np
+import pytest
+
+import oracle as O
+import uq
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(layers=2, dim=256, hidden=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, max_seq=64,
+             eps=1e-6, theta=1e6)
+
+
+def ulps(a, b):
+    a = a.view(np.int32).astype(np.int64)
+    b = b.view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def build(cfg, seed):
+    t = uq.synth_qwen2(cfg, seed)
+    gpu = uq.Qwen2Model(cfg, t)
+    ora = O.Model(cfg, {k: v[3] for k, v in t.items()})
+    return gpu, ora
+
+
+@pytest.mark.parametrize("cfg,steps", [(SMALL, 24), (dict(SMALL, layers=3, dim=512, hidden=1024, heads=8,
+                                                          kv_heads=2, head_dim=64, vocab=3000), 12)])
+def test_decode_steps_teacher_forced(gpu, cfg, steps):
+    g, o = build(cfg, 0x5EED0002)
+    toks = uq.synth_tokens(0x5EED0002, steps, cfg["vocab"])
+    for pos in range(steps):
+        nxt = g.decode_step(int(toks[pos]), pos)
+        lg = g.logits()
+        rc, onxt, olg = o.decode(int(toks[pos]), pos, want_logits=True)
+        assert rc == 0
+        d = ulps(lg, olg)
+        assert d.max() <= 1, (pos, d.max(), (d > 0).sum())
+        assert nxt == onxt, pos
+    for layer in range(cfg["layers"]):
+        k, v = g.kv(layer, steps)
+        assert np.array_equal(k, o.keys(layer, steps)) and np.array_equal(v, o.values(layer, steps))
+
+
+def test_decode_run_free_running(gpu):
+    g, o = build(SMALL, 77)
+    first = 17
+    out, ms = g.decode_run(first, 0, 40)
+    tok, ref = first, []
+    for pos in range(40):
+        rc, tok, _ = o.decode(tok, pos)
+        assert rc == 0
+        ref.append(tok)
+    assert list(out) == ref
+    assert ms > 0
+
+
+def test_decode_rejects_bad_position_and_token(gpu):
+    g, _ = build(SMALL, 5)
+    with pytest.raises(uq.UqError) as e:
+        g.decode_step(3, SMALL["max_seq"])
+    assert e.value.status == uq.Error.CONTEXT
+    with pytest.raises(uq.UqError) as e:
+        g.decode_step(SMALL["vocab"], 0)
+    assert e.value.status == uq.Error.SHAPE
+    with pytest.raises(uq.UqError) as e:
+        g.decode_run(1, SMALL["max_seq"] - 4, 8)
+    assert e.value.status == uq.Error.CONTEXT
+
+
+def test_model_requires_every_tensor(gpu):
+    t = uq.synth_qwen2(SMALL, 3)
+    m = uq.Qwen2Model(SMALL)
+    for name, (kind, n, rows, arr) in t.items():
+        if name != "blk.1.ffn_down.weight":
+            m.set_tensor(name, kind, n, rows, arr)
+    with pytest.raises(uq.UqError) as e:
+        m.prepare()
+    assert "blk.1.ffn_down.weight" in str(e.value)
+    with pytest.raises(uq.UqError) as e:
+        m.set_tensor("blk.1.ffn_down.weight", uq.KIND_Q8_0, 256, 512, t["blk.1.ffn_down.weight"][3][:512 * 272])
+    assert e.value.status == uq.Error.SHAPE or "shape" in str(e.value)
+
+
+def test_decode_qwen25_shapes_two_layers(gpu):
+    """The real Qwen2.5-1.5B shapes (dim 1536, ffn 8960, 12/2 heads of 128,
+    vocab 151936) with two layers, against the oracle step by step."""
+    cfg = dict(uq.QWEN25_15B, layers=2, max_seq=64)
+    g, o = build(cfg, 0x5EED0002)
+    toks = uq.synth_tokens(9, 6, cfg["vocab"])
+    for pos in range(6):
+        nxt = g.decode_step(int(toks[pos]), pos)
+        rc, onxt, olg = o.decode(int(toks[pos]), pos, want_logits=True)
+        assert rc == 0 and nxt == onxt
+        assert ulps(g.logits(), olg).max() <= 1

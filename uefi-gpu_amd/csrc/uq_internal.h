@@ -59,3 +59,8 @@ int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const flo
 int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s);
 
 }  // namespace uq
+
+// The opaque handle of include/uq.h.
+struct uq_weight {
+    uq::Weight w;
+};

@@ -1,0 +1,53 @@
+// Host-side state of the Qwen2 dense decoder (uq_model.hip).
+#pragma once
+#include "uq_internal.h"
+#include "../../include/uq.h"
+
+#include <map>
+#include <string>
+#include <vector>
+
+namespace uq {
+
+struct LayerDev {
+    Weight qkv;  // q|k|v rows of one layer in one Q8_0 weight
+};
+
+struct Model {
+    uq_qwen2_config cfg{};
+    hipStream_t stream = nullptr;
+    bool prepared = false;
+    std::map<std::string, uq_weight_t> q8;
+    std::map<std::string, float*> f32;
+    std::map<std::string, int64_t> f32_len;
+    std::vector<LayerDev> layers;
+    std::vector<void*> owned;
+
+    float *X = nullptr, *TMP = nullptr, *XN = nullptr, *QKV = nullptr, *ATT = nullptr, *GATE = nullptr,
+          *LOGITS = nullptr, *XS = nullptr, *trig = nullptr;
+    int8_t* XQ = nullptr;
+    uint16_t *kcache = nullptr, *vcache = nullptr;
+    uint32_t *token = nullptr, *history = nullptr, *result = nullptr;
+    unsigned* ticket = nullptr;
+    int* pos = nullptr;
+    uint32_t* partial = nullptr;
+    uint32_t host_io[4] = {0, 0, 0, 0};
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+
+    ~Model();
+    int fail(int st, const std::string& msg);
+    const Weight* weight(const std::string& name) const;
+    const float* vec(const std::string& name) const;
+    int check_shapes();
+    int build_qkv(int l);
+    template <class T>
+    int alloc(T** p, size_t count);
+    int build_buffers();
+    int enqueue_step(hipStream_t s);
+    int prepare();
+    int set_position(uint32_t tok, int p);
+};
+
+}  // namespace uq

@@ -1,0 +1,413 @@
+// Qwen2 dense decoder on one GPU: device-resident GGUF tensors, activation and
+// fp16 KV arenas, and the decode step captured once into a hipGraph.
+//
+// Replaces the reference's decode graph (driver/src/gpu_graph.rs:81-197): its
+// 342 prebuilt QMD jobs in one GPFIFO entry, patched per token with `token`
+// and `pos`, become one hipGraphLaunch per token with `token`/`pos` read from
+// device memory and the greedy result fed back on the device.
+#include "uq_internal.h"
+#include "uq_decode.h"
+#include "uq_model.h"
+#include "../../include/uq.h"
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace uq;
+
+namespace uq {
+
+int Model::fail(int st, const std::string& msg) { return set_error(st, msg); }
+
+const Weight* Model::weight(const std::string& name) const {
+    auto it = q8.find(name);
+    return it == q8.end() ? nullptr : &it->second->w;
+}
+const float* Model::vec(const std::string& name) const {
+    auto it = f32.find(name);
+    return it == f32.end() ? nullptr : it->second;
+}
+
+Model::~Model() {
+    if (graph_exec) hipGraphExecDestroy(graph_exec);
+    if (graph) hipGraphDestroy(graph);
+    for (auto& kv : q8) uq_weight_free(kv.second);
+    for (auto& kv : f32) hipFree(kv.second);
+    for (auto* p : owned) hipFree(p);
+    for (auto& L : layers) hipFree(L.qkv.alloc);
+}
+
+}  // namespace uq
+
+static std::string lname(int l, const char* s) { return "blk." + std::to_string(l) + "." + s; }
+
+extern "C" {
+
+int uq_model_create(const uq_qwen2_config* cfg, uq_model_t* out) {
+    if (!cfg || !out) return set_error(ERR_ARG, "model_create: null pointer");
+    const auto& c = *cfg;
+    if (c.layers <= 0 || c.dim <= 0 || c.dim % 256 || c.dim > 4096 || c.hidden <= 0 || c.hidden % 256 ||
+        c.hidden > 16384 || c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 32 ||
+        c.heads * c.head_dim != c.dim || 1024 % c.head_dim || c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > 8192)
+        return set_error(ERR_SHAPE, "model_create: unsupported configuration");
+    void* stream = uq_stream();
+    if (!stream) return set_error(ERR_ARG, "uq_init has not been called");
+    Model* m = new Model();
+    m->cfg = c;
+    m->stream = (hipStream_t)stream;
+    *out = (uq_model_t)m;
+    return OK;
+}
+
+int uq_model_free(uq_model_t h) {
+    Model* m = (Model*)h;
+    if (!m) return OK;
+    hipStreamSynchronize(m->stream);
+    delete m;
+    return OK;
+}
+
+int uq_model_set_tensor(uq_model_t h, const char* name, uint32_t kind, int64_t n, int64_t rows, const void* data,
+                        size_t bytes) {
+    Model* m = (Model*)h;
+    if (!m || !name || !data) return set_error(ERR_ARG, "model_set_tensor: null pointer");
+    if (m->prepared) return set_error(ERR_ARG, "model_set_tensor: model already prepared");
+    const std::string nm(name);
+    if (kind == KIND_F32) {
+        if (rows != 1 || n <= 0 || (int64_t)bytes != 4 * n) return set_error(ERR_SHAPE, "model_set_tensor: bad F32 shape");
+        float* d = nullptr;
+        UQ_CHECK_HIP(hipMalloc(&d, bytes));
+        UQ_CHECK_HIP(hipMemcpy(d, data, bytes, hipMemcpyHostToDevice));
+        auto it = m->f32.find(nm);
+        if (it != m->f32.end()) hipFree(it->second);
+        m->f32[nm] = d;
+        m->f32_len[nm] = n;
+        return OK;
+    }
+    if (kind != KIND_Q8_0) return set_error(ERR_QUANT_TYPE, "model_set_tensor: dense decoder tensors are Q8_0 or F32");
+    uq_weight_t w = nullptr;
+    if (int rc = uq_weight_upload(kind, n, rows, data, bytes, &w)) return rc;
+    auto it = m->q8.find(nm);
+    if (it != m->q8.end()) uq_weight_free(it->second);
+    m->q8[nm] = w;
+    return OK;
+}
+
+}  // extern "C"
+
+namespace uq {
+
+int Model::check_shapes() {
+    const auto& c = cfg;
+    const int kvd = c.kv_heads * c.head_dim;
+    auto need_w = [&](const std::string& nm, int64_t n, int64_t rows) -> int {
+        const Weight* w = weight(nm);
+        if (!w) return fail(ERR_ARG, "missing tensor " + nm);
+        if (w->n != n || w->m != rows) return fail(ERR_SHAPE, "tensor " + nm + " has the wrong shape");
+        return OK;
+    };
+    auto need_v = [&](const std::string& nm, int64_t n, bool optional) -> int {
+        auto it = f32_len.find(nm);
+        if (it == f32_len.end()) return optional ? OK : fail(ERR_ARG, "missing tensor " + nm);
+        if (it->second != n) return fail(ERR_SHAPE, "tensor " + nm + " has the wrong length");
+        return OK;
+    };
+    if (int rc = need_w("token_embd.weight", c.dim, c.vocab)) return rc;
+    if (int rc = need_w("output.weight", c.dim, c.vocab)) return rc;
+    if (int rc = need_v("output_norm.weight", c.dim, false)) return rc;
+    for (int l = 0; l < c.layers; l++) {
+        if (int rc = need_w(lname(l, "attn_q.weight"), c.dim, c.dim)) return rc;
+        if (int rc = need_w(lname(l, "attn_k.weight"), c.dim, kvd)) return rc;
+        if (int rc = need_w(lname(l, "attn_v.weight"), c.dim, kvd)) return rc;
+        if (int rc = need_w(lname(l, "attn_output.weight"), c.dim, c.dim)) return rc;
+        if (int rc = need_w(lname(l, "ffn_gate.weight"), c.dim, c.hidden)) return rc;
+        if (int rc = need_w(lname(l, "ffn_up.weight"), c.dim, c.hidden)) return rc;
+        if (int rc = need_w(lname(l, "ffn_down.weight"), c.hidden, c.dim)) return rc;
+        if (int rc = need_v(lname(l, "attn_norm.weight"), c.dim, false)) return rc;
+        if (int rc = need_v(lname(l, "ffn_norm.weight"), c.dim, false)) return rc;
+        if (int rc = need_v(lname(l, "attn_q.bias"), c.dim, true)) return rc;
+        if (int rc = need_v(lname(l, "attn_k.bias"), kvd, true)) return rc;
+        if (int rc = need_v(lname(l, "attn_v.bias"), kvd, true)) return rc;
+    }
+    return OK;
+}
+
+// q, k and v of a layer become one Q8_0 weight of dim + 2*kvd rows (the
+// reference fuses them in one launch too, qkv_dp4a, gpu_dp4a.cu:53-59).
+int Model::build_qkv(int l) {
+    const Weight* ws[3] = {weight(lname(l, "attn_q.weight")), weight(lname(l, "attn_k.weight")),
+                           weight(lname(l, "attn_v.weight"))};
+    const int64_t n = cfg.dim, nb = n / 32;
+    int64_t rows = 0;
+    for (auto* w : ws) rows += w->m;
+    Weight& q = layers[l].qkv;
+    q.kind = KIND_Q8_0;
+    q.n = n;
+    q.m = rows;
+    const size_t off_d = ((size_t)(n * rows) + 255) & ~(size_t)255;
+    q.alloc_bytes = off_d + (((size_t)(nb * rows) * 2 + 255) & ~(size_t)255);
+    UQ_CHECK_HIP(hipMalloc(&q.alloc, q.alloc_bytes));
+    uint8_t* base = (uint8_t*)q.alloc;
+    q.qs = (const int8_t*)base;
+    q.d = (const uint16_t*)(base + off_d);
+    int64_t r0 = 0;
+    for (auto* w : ws) {
+        UQ_CHECK_HIP(hipMemcpyAsync(base + r0 * n, w->qs, (size_t)(w->m * n), hipMemcpyDeviceToDevice, stream));
+        UQ_CHECK_HIP(hipMemcpyAsync(base + off_d + r0 * nb * 2, w->d, (size_t)(w->m * nb * 2),
+                                    hipMemcpyDeviceToDevice, stream));
+        r0 += w->m;
+    }
+    UQ_CHECK_HIP(hipStreamSynchronize(stream));
+    return OK;
+}
+
+template <class T>
+int Model::alloc(T** p, size_t count) {
+    UQ_CHECK_HIP(hipMalloc((void**)p, sizeof(T) * (count ? count : 1)));
+    UQ_CHECK_HIP(hipMemset(*p, 0, sizeof(T) * (count ? count : 1)));
+    owned.push_back((void*)*p);
+    return OK;
+}
+
+int Model::build_buffers() {
+    const auto& c = cfg;
+    const int kvd = c.kv_heads * c.head_dim, big = c.hidden > c.dim ? c.hidden : c.dim;
+    if (int rc = alloc(&X, c.dim)) return rc;
+    if (int rc = alloc(&TMP, c.dim)) return rc;
+    if (int rc = alloc(&XN, c.dim)) return rc;
+    if (int rc = alloc(&QKV, c.dim + 2 * kvd)) return rc;
+    if (int rc = alloc(&ATT, c.dim)) return rc;
+    if (int rc = alloc(&GATE, c.hidden)) return rc;
+    if (int rc = alloc(&LOGITS, c.vocab)) return rc;
+    if (int rc = alloc(&XQ, big)) return rc;
+    if (int rc = alloc(&XS, big / 32)) return rc;
+    if (int rc = alloc(&kcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
+    if (int rc = alloc(&vcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
+    if (int rc = alloc(&trig, (size_t)c.max_seq * c.head_dim)) return rc;
+    if (int rc = alloc(&token, 1)) return rc;
+    if (int rc = alloc(&pos, 1)) return rc;
+    if (int rc = alloc(&history, c.max_seq)) return rc;
+    if (int rc = alloc(&partial, 4 * (size_t)greedy_partials(c.vocab))) return rc;
+    if (int rc = alloc(&ticket, 4)) return rc;
+    if (int rc = alloc(&result, 4)) return rc;
+    // RoPE table, gpu_graph.rs:131-133: angle = pos * powf(theta, -(2i)/hd), cos | sin
+    std::vector<float> t((size_t)c.max_seq * c.head_dim);
+    const int half = c.head_dim / 2;
+    for (int p = 0; p < c.max_seq; p++)
+        for (int i = 0; i < half; i++) {
+            const float e = -((float)(2 * i)) / (float)c.head_dim;
+            const float angle = (float)p * powf(c.theta, e);
+            float s, co;
+            sincosf(angle, &s, &co);
+            t[(size_t)p * c.head_dim + i] = co;
+            t[(size_t)p * c.head_dim + half + i] = s;
+        }
+    UQ_CHECK_HIP(hipMemcpy(trig, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice));
+    return OK;
+}
+
+int Model::enqueue_step(hipStream_t s) {
+    const auto& c = cfg;
+    const int kvd = c.kv_heads * c.head_dim;
+    const size_t kvl = (size_t)c.max_seq * kvd;
+    const Weight* emb = weight("token_embd.weight");
+    for (int l = 0; l < c.layers; l++) {
+        NormQuantArgs nq{};
+        nq.x = X;
+        nq.residual = TMP;
+        nq.gamma = vec(lname(l, "attn_norm.weight"));
+        nq.xq = XQ;
+        nq.xs = XS;
+        nq.dim = c.dim;
+        nq.add = l > 0;
+        nq.eps = c.eps;
+        if (l == 0) {
+            nq.embed_qs = emb->qs;
+            nq.embed_d = emb->d;
+            nq.token = token;
+        }
+        launch_resnorm_quant(nq, s);
+        if (int rc = launch_matvec(layers[l].qkv, nullptr, XQ, XS, QKV, s)) return rc;
+        RopeArgs ra{QKV, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")), vec(lname(l, "attn_v.bias")),
+                    trig, pos, kcache + l * kvl, vcache + l * kvl, c.heads, c.kv_heads, c.head_dim};
+        launch_rope_kv(ra, s);
+        AttnArgs aa{QKV, kcache + l * kvl, vcache + l * kvl, pos, ATT, XQ, XS, c.heads, c.kv_heads, c.head_dim,
+                    c.max_seq, (float)(1.0 / std::sqrt((double)c.head_dim))};
+        launch_attention(aa, s);
+        if (int rc = launch_matvec(*weight(lname(l, "attn_output.weight")), nullptr, XQ, XS, TMP, s)) return rc;
+        NormQuantArgs nf{};
+        nf.x = X;
+        nf.residual = TMP;
+        nf.gamma = vec(lname(l, "ffn_norm.weight"));
+        nf.xq = XQ;
+        nf.xs = XS;
+        nf.dim = c.dim;
+        nf.add = 1;
+        nf.eps = c.eps;
+        launch_resnorm_quant(nf, s);
+        if (int rc = launch_matvec(*weight(lname(l, "ffn_gate.weight")), weight(lname(l, "ffn_up.weight")), XQ, XS,
+                                   GATE, s))
+            return rc;
+        launch_quant_act(GATE, c.hidden, XQ, XS, s);
+        if (int rc = launch_matvec(*weight(lname(l, "ffn_down.weight")), nullptr, XQ, XS, TMP, s)) return rc;
+    }
+    NormQuantArgs no{};
+    no.x = X;
+    no.residual = TMP;
+    no.gamma = vec("output_norm.weight");
+    no.y = XN;
+    no.xq = XQ;
+    no.xs = XS;
+    no.dim = c.dim;
+    no.add = 1;
+    no.eps = c.eps;
+    launch_resnorm_quant(no, s);
+    if (int rc = launch_matvec(*weight("output.weight"), nullptr, XQ, XS, LOGITS, s)) return rc;
+    GreedyArgs ga{LOGITS, c.vocab, partial, ticket, result, token, pos, history, c.max_seq};
+    launch_greedy(ga, s);
+    return OK;
+}
+
+int Model::prepare() {
+    if (prepared) return OK;
+    if (int rc = check_shapes()) return rc;
+    layers.resize(cfg.layers);
+    for (int l = 0; l < cfg.layers; l++) {
+        if (int rc = build_qkv(l)) return rc;
+        for (const char* s : {"attn_q.weight", "attn_k.weight", "attn_v.weight"}) {
+            auto it = q8.find(lname(l, s));
+            uq_weight_free(it->second);
+            q8.erase(it);
+        }
+    }
+    if (int rc = build_buffers()) return rc;
+    UQ_CHECK_HIP(hipStreamSynchronize(stream));
+    UQ_CHECK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(stream);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (rc) {
+        if (g) hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(ERR_DEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+    graph = g;
+    UQ_CHECK_HIP(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
+    prepared = true;
+    return OK;
+}
+
+int Model::set_position(uint32_t tok, int p) {
+    if ((int64_t)tok >= cfg.vocab) return fail(ERR_SHAPE, "token id beyond the vocabulary");
+    if (p < 0 || p >= cfg.max_seq) return fail(ERR_CONTEXT, "position beyond the KV cache");
+    host_io[0] = tok;
+    host_io[1] = (uint32_t)p;
+    UQ_CHECK_HIP(hipMemcpyAsync(token, &host_io[0], 4, hipMemcpyHostToDevice, stream));
+    UQ_CHECK_HIP(hipMemcpyAsync(pos, &host_io[1], 4, hipMemcpyHostToDevice, stream));
+    return OK;
+}
+
+}  // namespace uq
+
+extern "C" {
+
+int uq_model_prepare(uq_model_t h) {
+    Model* m = (Model*)h;
+    if (!m) return set_error(ERR_ARG, "model_prepare: null model");
+    return m->prepare();
+}
+
+int uq_decode_step(uq_model_t h, uint32_t tok, int p, uint32_t* next) {
+    Model* m = (Model*)h;
+    if (!m || !next) return set_error(ERR_ARG, "decode_step: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "decode_step: model not prepared");
+    if (int rc = m->set_position(tok, p)) return rc;
+    UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+    uint32_t res[2] = {0, 0};
+    UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 8, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    if (res[1]) return set_error(ERR_NONFINITE, "decode_step: non-finite logits");
+    if ((int64_t)res[0] >= m->cfg.vocab) return set_error(ERR_DEVICE, "decode_step: invalid token id");
+    *next = res[0];
+    return OK;
+}
+
+int uq_decode_run(uq_model_t h, uint32_t tok, int p, int steps, uint32_t* tokens, double* ms) {
+    Model* m = (Model*)h;
+    if (!m || !tokens) return set_error(ERR_ARG, "decode_run: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "decode_run: model not prepared");
+    if (steps <= 0 || p < 0 || (int64_t)p + steps > m->cfg.max_seq)
+        return set_error(ERR_CONTEXT, "decode_run: positions beyond the KV cache");
+    if (int rc = m->set_position(tok, p)) return rc;
+    hipEvent_t e0, e1;
+    UQ_CHECK_HIP(hipEventCreate(&e0));
+    UQ_CHECK_HIP(hipEventCreate(&e1));
+    UQ_CHECK_HIP(hipEventRecord(e0, m->stream));
+    for (int i = 0; i < steps; i++) UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+    UQ_CHECK_HIP(hipEventRecord(e1, m->stream));
+    std::vector<uint32_t> out((size_t)steps);
+    uint32_t res[2] = {0, 0};
+    UQ_CHECK_HIP(hipMemcpyAsync(out.data(), m->history + p, 4 * (size_t)steps, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 8, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    float t = 0;
+    hipEventElapsedTime(&t, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (ms) *ms = t;
+    std::memcpy(tokens, out.data(), 4 * (size_t)steps);
+    if (res[1]) return set_error(ERR_NONFINITE, "decode_run: non-finite logits");
+    return OK;
+}
+
+int uq_prompt_tokens(uq_model_t h, const uint32_t* tokens, int count, int p, uint32_t* next) {
+    Model* m = (Model*)h;
+    if (!m || !tokens || !next) return set_error(ERR_ARG, "prompt_tokens: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "prompt_tokens: model not prepared");
+    if (count <= 0 || p < 0 || (int64_t)p + count > m->cfg.max_seq)
+        return set_error(ERR_CONTEXT, "prompt_tokens: positions beyond the KV cache");
+    for (int i = 0; i < count; i++)
+        if ((int64_t)tokens[i] >= m->cfg.vocab) return set_error(ERR_SHAPE, "prompt_tokens: token id beyond the vocabulary");
+    std::vector<uint32_t> staged(tokens, tokens + count);
+    for (int i = 0; i < count; i++) {
+        const int pp = p + i;
+        UQ_CHECK_HIP(hipMemcpyAsync(m->token, &staged[i], 4, hipMemcpyHostToDevice, m->stream));
+        UQ_CHECK_HIP(hipMemcpyAsync(m->pos, &pp, 4, hipMemcpyHostToDevice, m->stream));
+        UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+        UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    }
+    uint32_t res[2] = {0, 0};
+    UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 8, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    if (res[1]) return set_error(ERR_NONFINITE, "prompt_tokens: non-finite logits");
+    *next = res[0];
+    return OK;
+}
+
+int uq_model_logits(uq_model_t h, float* out, int64_t n) {
+    Model* m = (Model*)h;
+    if (!m || !out) return set_error(ERR_ARG, "model_logits: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "model_logits: model not prepared");
+    if (n != m->cfg.vocab) return set_error(ERR_SHAPE, "model_logits: n != vocab");
+    UQ_CHECK_HIP(hipMemcpyAsync(out, m->LOGITS, 4 * (size_t)n, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    return OK;
+}
+
+int uq_model_kv(uq_model_t h, int layer, int count, uint16_t* keys, uint16_t* values) {
+    Model* m = (Model*)h;
+    if (!m || !keys || !values) return set_error(ERR_ARG, "model_kv: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "model_kv: model not prepared");
+    if (layer < 0 || layer >= m->cfg.layers || count <= 0 || count > m->cfg.max_seq)
+        return set_error(ERR_SHAPE, "model_kv: bad layer or count");
+    const size_t kvd = (size_t)m->cfg.kv_heads * m->cfg.head_dim, kvl = kvd * m->cfg.max_seq;
+    UQ_CHECK_HIP(hipMemcpyAsync(keys, m->kcache + layer * kvl, 2 * kvd * count, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipMemcpyAsync(values, m->vcache + layer * kvl, 2 * kvd * count, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
+    return OK;
+}
+
+}  // extern "C"

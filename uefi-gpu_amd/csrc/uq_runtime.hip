@@ -76,10 +76,6 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 using namespace uq;
 
-struct uq_weight {
-    Weight w;
-};
-
 extern "C" {
 
 const char* uq_last_error(void) { return uq::g_error.c_str(); }

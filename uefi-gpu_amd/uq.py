@@ -74,6 +74,19 @@ _SIGS = {
     "uq_time_matvecs": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int), ctypes.c_int, _i64,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "uq_model_create": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
+    "uq_model_free": (ctypes.c_int, [_vp]),
+    "uq_model_set_tensor": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_uint32, _i64, _i64, _vp, ctypes.c_size_t]),
+    "uq_model_prepare": (ctypes.c_int, [_vp]),
+    "uq_decode_step": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_int, _c_u32p]),
+    "uq_decode_run": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, _c_u32p,
+                                     ctypes.POINTER(ctypes.c_double)]),
+    "uq_model_logits": (ctypes.c_int, [_vp, _c_f32p, _i64]),
+    "uq_prompt_tokens": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p]),
+    "uq_probe_bandwidth": (ctypes.c_int, [_i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_double)]),
+    "uq_model_kv": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint16),
+                                   ctypes.POINTER(ctypes.c_uint16)]),
     "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
     "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
     "uq_synth_tokens": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_uint32, _c_u32p]),
@@ -212,6 +225,12 @@ def block_dots(w, x):
     return d.reshape(w.m, w.n // bsz)
 
 
+def probe_bandwidth(nbytes=1 << 30, reps=10):
+    r, c = ctypes.c_double(), ctypes.c_double()
+    _check(lib().uq_probe_bandwidth(nbytes, reps, ctypes.byref(r), ctypes.byref(c)))
+    return r.value, c.value
+
+
 def time_matvecs(weights, pairs, max_n, reps, warmup, probe):
     hs = (_vp * len(weights))(*[w.handle for w in weights])
     pr = (ctypes.c_int * len(weights))(*pairs)
@@ -260,3 +279,112 @@ class Gpu:
         for y, o in zip(ys, outs):
             y[:] = o
         return True
+
+
+# ---------------------------------------------------------------- Qwen2 dense decoder
+class Qwen2Config(ctypes.Structure):
+    """uq_qwen2_config: the shape constants of driver/src/llm.rs:314-321."""
+    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "dim", "hidden", "heads", "kv_heads", "head_dim",
+                                             "vocab", "max_seq")] + [("eps", ctypes.c_float), ("theta", ctypes.c_float)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+QWEN25_15B = dict(layers=28, dim=1536, hidden=8960, heads=12, kv_heads=2, head_dim=128, vocab=151936,
+                  max_seq=1024, eps=1e-6, theta=1e6)
+
+
+def synth_qwen2(cfg, seed):
+    """Seeded random-init Qwen2 tensors in GGUF layout: name -> (kind, n, rows, array).
+    Q8_0 matrices from uq_synth_quant; norm weights 1 + 0.1 N(0,1); biases 0.02 N(0,1)."""
+    D, H, kvd = cfg["dim"], cfg["hidden"], cfg["kv_heads"] * cfg["head_dim"]
+    t = {}
+
+    def q8(name, n, rows):
+        t[name] = (KIND_Q8_0, n, rows, synth_quant(KIND_Q8_0, tensor_seed(seed, name), rows, n))
+
+    def f32(name, n, mean, std):
+        t[name] = (KIND_F32, n, 1, synth_normal(tensor_seed(seed, name), n, mean, std))
+
+    q8("token_embd.weight", D, cfg["vocab"])
+    q8("output.weight", D, cfg["vocab"])
+    f32("output_norm.weight", D, 1.0, 0.1)
+    for l in range(cfg["layers"]):
+        b = "blk.%d." % l
+        q8(b + "attn_q.weight", D, D)
+        q8(b + "attn_k.weight", D, kvd)
+        q8(b + "attn_v.weight", D, kvd)
+        q8(b + "attn_output.weight", D, D)
+        q8(b + "ffn_gate.weight", D, H)
+        q8(b + "ffn_up.weight", D, H)
+        q8(b + "ffn_down.weight", H, D)
+        f32(b + "attn_norm.weight", D, 1.0, 0.1)
+        f32(b + "ffn_norm.weight", D, 1.0, 0.1)
+        f32(b + "attn_q.bias", D, 0.0, 0.02)
+        f32(b + "attn_k.bias", kvd, 0.0, 0.02)
+        f32(b + "attn_v.bias", kvd, 0.0, 0.02)
+    return t
+
+
+class Qwen2Model:
+    """The decode graph of driver/src/gpu_graph.rs over libuq (uq_model_*)."""
+
+    def __init__(self, cfg, tensors=None):
+        self.cfg = dict(cfg)
+        c = Qwen2Config(**self.cfg)
+        h = _vp()
+        _check(lib().uq_model_create(ctypes.byref(c), ctypes.byref(h)))
+        self.handle = h
+        if tensors:
+            for name, (kind, n, rows, arr) in tensors.items():
+                self.set_tensor(name, kind, n, rows, arr)
+            self.prepare()
+
+    def set_tensor(self, name, kind, n, rows, arr):
+        a = np.ascontiguousarray(arr)
+        _check(lib().uq_model_set_tensor(self.handle, name.encode(), kind, n, rows, a.ctypes.data, a.nbytes))
+
+    def prepare(self):
+        _check(lib().uq_model_prepare(self.handle))
+
+    def decode_step(self, token, pos):
+        nxt = ctypes.c_uint32()
+        _check(lib().uq_decode_step(self.handle, token, pos, ctypes.byref(nxt)))
+        return nxt.value
+
+    def decode_run(self, token, pos, steps):
+        out = np.empty(steps, np.uint32)
+        ms = ctypes.c_double()
+        _check(lib().uq_decode_run(self.handle, token, pos, steps, _p(out, _c_u32p), ctypes.byref(ms)))
+        return out, ms.value
+
+    def prompt(self, tokens, pos=0):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        nxt = ctypes.c_uint32()
+        _check(lib().uq_prompt_tokens(self.handle, _p(t, _c_u32p), t.size, pos, ctypes.byref(nxt)))
+        return nxt.value
+
+    def logits(self):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        _check(lib().uq_model_logits(self.handle, _p(out, _c_f32p), out.size))
+        return out
+
+    def kv(self, layer, count):
+        kvd = self.cfg["kv_heads"] * self.cfg["head_dim"]
+        k = np.empty((count, kvd), np.uint16)
+        v = np.empty((count, kvd), np.uint16)
+        _check(lib().uq_model_kv(self.handle, layer, count, k.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                 v.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))))
+        return k, v
+
+    def free(self):
+        if getattr(self, "handle", None):
+            lib().uq_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -84,9 +84,17 @@ def test_model_requires_every_tensor(gpu):
     with pytest.raises(uq.UqError) as e:
         m.prepare()
     assert "blk.1.ffn_down.weight" in str(e.value)
+    raw = t["blk.1.ffn_down.weight"][3]
+    with pytest.raises(uq.UqError) as e:                       # byte count != rows * row_bytes
+        m.set_tensor("blk.1.ffn_down.weight", uq.KIND_Q8_0, 512, 256, raw[:-34])
+    assert e.value.status == uq.Error.SHAPE
+    m.set_tensor("blk.1.ffn_down.weight", uq.KIND_Q8_0, 256, 512, raw)   # transposed shape
     with pytest.raises(uq.UqError) as e:
-        m.set_tensor("blk.1.ffn_down.weight", uq.KIND_Q8_0, 256, 512, t["blk.1.ffn_down.weight"][3][:512 * 272])
-    assert e.value.status == uq.Error.SHAPE or "shape" in str(e.value)
+        m.prepare()
+    assert e.value.status == uq.Error.SHAPE and "ffn_down" in str(e.value)
+    m.set_tensor("blk.1.ffn_down.weight", uq.KIND_Q8_0, 512, 256, raw)
+    m.prepare()
+    assert m.decode_step(1, 0) < SMALL["vocab"]
 
 
 def test_decode_qwen25_shapes_two_layers(gpu):

@@ -1,0 +1,115 @@
+// Workgroup-level building blocks of the decode kernels: double sums and
+// float max over a workgroup, the residual + RMSNorm + block-32 quant of one
+// activation vector by one 256-thread workgroup, and the greedy candidate rule
+// (stable argmax: lowest id wins ties, any non-finite logit marks it bad).
+#pragma once
+#include "uq_device.h"
+#include "uq_decode.h"
+
+namespace uq {
+
+constexpr int NQ_WG = 256;
+
+// Sum of a double over the whole workgroup (WG threads, multiple of 64).
+template <int WG>
+__device__ inline double block_sum_d(double v, double* red) {
+    v = uq_group_sum<64>(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < WG / 64; w++) t += red[w];
+    return t;
+}
+template <int WG>
+__device__ inline float block_max_f(float v, float* red) {
+    v = uq_group_max<64>(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < WG / 64; w++) t = fmaxf(t, red[w]);
+    return t;
+}
+
+
+// Residual + RMSNorm + block-32 quant of a.dim values by one workgroup of WG
+// threads (element i = j*WG + t, so each 32-block sits in half a wave). The
+// quantized vector goes to q/s (LDS or global); write_x stores the summed
+// residual to a.x_out. Ends with a barrier.
+template <int WG>
+__device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red) {
+    constexpr int PER = (4096 + WG - 1) / WG;  // dim <= 4096
+    const int t = threadIdx.x, D = a.dim;
+    float xv[PER];
+    double ss = 0.0;
+    const uint32_t tok = a.embed_qs ? *a.token : 0u;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * WG + t;
+        if (i < D) {
+            float v;
+            if (a.embed_qs) {
+                const int64_t row = (int64_t)tok;
+                v = uq_half(a.embed_d[row * (D / 32) + i / 32]) * (float)a.embed_qs[row * D + i];
+            } else {
+                v = a.x[i];
+                if (a.residual) v = v + a.residual[i];
+            }
+            if (write_x && a.x_out) a.x_out[i] = v;
+            xv[j] = v;
+            const float sq = v * v;
+            ss += (double)sq;
+        }
+    }
+    ss = block_sum_d<WG>(ss, red);
+    const float mean = (float)(ss / (double)D);
+    const float scale = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * WG + t;
+        if (i < D) {
+            const float tmp = xv[j] * scale;
+            const float y = tmp * a.gamma[i];
+            float sc;
+            const int8_t qv = uq_quant_lane(y, &sc);
+            q[i] = qv;
+            if ((t & 31) == 0) s[i >> 5] = sc;
+        }
+    }
+    __syncthreads();
+}
+
+struct Cand {
+    float v;
+    int id;
+    unsigned bad;
+    unsigned pad;
+};
+__device__ __forceinline__ bool better(float a, int ai, float b, int bi) { return a > b || (a == b && ai < bi); }
+__device__ inline void cand_reduce(float& v, int& id, unsigned& bad, float* vs, int* ids, unsigned* bs) {
+    const int t = threadIdx.x;
+    vs[t] = v;
+    ids[t] = id;
+    bs[t] = bad;
+    __syncthreads();
+    for (int d = blockDim.x / 2; d; d >>= 1) {
+        if (t < d) {
+            if (better(vs[t + d], ids[t + d], vs[t], ids[t])) {
+                vs[t] = vs[t + d];
+                ids[t] = ids[t + d];
+            }
+            bs[t] |= bs[t + d];
+        }
+        __syncthreads();
+    }
+    v = vs[0];
+    id = ids[0];
+    bad = bs[0];
+}
+
+}  // namespace uq

@@ -54,6 +54,13 @@ UQ_DEV float uq_sigmoid(float x) {
     return 1.0f / d;
 }
 
+// 16-byte non-temporal load for weights that are streamed once per launch.
+typedef int uq_v4i __attribute__((ext_vector_type(4)));
+UQ_DEV int4 uq_ntload16(const void* p) {
+    const uq_v4i v = __builtin_nontemporal_load((const uq_v4i*)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
 // 4-way signed int8 dot with int32 accumulate (v_dot4_i32_i8).
 UQ_DEV int uq_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

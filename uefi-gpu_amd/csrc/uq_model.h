@@ -17,18 +17,19 @@ struct Model {
     uq_qwen2_config cfg{};
     hipStream_t stream = nullptr;
     bool prepared = false;
+    bool eager = false;
     std::map<std::string, uq_weight_t> q8;
     std::map<std::string, float*> f32;
     std::map<std::string, int64_t> f32_len;
     std::vector<LayerDev> layers;
     std::vector<void*> owned;
 
-    float *X = nullptr, *TMP = nullptr, *XN = nullptr, *QKV = nullptr, *ATT = nullptr, *GATE = nullptr,
+    float *R0 = nullptr, *R1 = nullptr, *TMP = nullptr, *XN = nullptr, *QKV = nullptr, *ATT = nullptr, *GATE = nullptr,
           *LOGITS = nullptr, *XS = nullptr, *trig = nullptr;
-    int8_t* XQ = nullptr;
+    int8_t *XQ = nullptr, *XQH = nullptr;  // quantized activations: dim-sized, hidden-sized
+    float* XSH = nullptr;
     uint16_t *kcache = nullptr, *vcache = nullptr;
     uint32_t *token = nullptr, *history = nullptr, *result = nullptr;
-    unsigned* ticket = nullptr;
     int* pos = nullptr;
     uint32_t* partial = nullptr;
     uint32_t host_io[4] = {0, 0, 0, 0};
@@ -48,6 +49,7 @@ struct Model {
     int enqueue_step(hipStream_t s);
     int prepare();
     int set_position(uint32_t tok, int p);
+    int launch_step();
 };
 
 }  // namespace uq

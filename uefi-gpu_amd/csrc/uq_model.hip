@@ -7,10 +7,12 @@
 // device memory and the greedy result fed back on the device.
 #include "uq_internal.h"
 #include "uq_decode.h"
+#include "uq_step.h"
 #include "uq_model.h"
 #include "../../include/uq.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -51,7 +53,7 @@ int uq_model_create(const uq_qwen2_config* cfg, uq_model_t* out) {
     const auto& c = *cfg;
     if (c.layers <= 0 || c.dim <= 0 || c.dim % 256 || c.dim > 4096 || c.hidden <= 0 || c.hidden % 256 ||
         c.hidden > 16384 || c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 32 ||
-        c.heads * c.head_dim != c.dim || 1024 % c.head_dim || c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > 8192)
+        c.heads * c.head_dim != c.dim || c.head_dim % 64 || c.head_dim > 256 || 1024 % c.head_dim || c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > 8192)
         return set_error(ERR_SHAPE, "model_create: unsupported configuration");
     void* stream = uq_stream();
     if (!stream) return set_error(ERR_ARG, "uq_init has not been called");
@@ -175,23 +177,25 @@ int Model::alloc(T** p, size_t count) {
 int Model::build_buffers() {
     const auto& c = cfg;
     const int kvd = c.kv_heads * c.head_dim, big = c.hidden > c.dim ? c.hidden : c.dim;
-    if (int rc = alloc(&X, c.dim)) return rc;
+    if (int rc = alloc(&R0, c.dim)) return rc;
+    if (int rc = alloc(&R1, c.dim)) return rc;
     if (int rc = alloc(&TMP, c.dim)) return rc;
     if (int rc = alloc(&XN, c.dim)) return rc;
     if (int rc = alloc(&QKV, c.dim + 2 * kvd)) return rc;
     if (int rc = alloc(&ATT, c.dim)) return rc;
     if (int rc = alloc(&GATE, c.hidden)) return rc;
     if (int rc = alloc(&LOGITS, c.vocab)) return rc;
-    if (int rc = alloc(&XQ, big)) return rc;
-    if (int rc = alloc(&XS, big / 32)) return rc;
+    if (int rc = alloc(&XQ, c.dim)) return rc;
+    if (int rc = alloc(&XS, c.dim / 32)) return rc;
+    if (int rc = alloc(&XQH, big)) return rc;
+    if (int rc = alloc(&XSH, big / 32)) return rc;
     if (int rc = alloc(&kcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
     if (int rc = alloc(&vcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
     if (int rc = alloc(&trig, (size_t)c.max_seq * c.head_dim)) return rc;
     if (int rc = alloc(&token, 1)) return rc;
     if (int rc = alloc(&pos, 1)) return rc;
     if (int rc = alloc(&history, c.max_seq)) return rc;
-    if (int rc = alloc(&partial, 4 * (size_t)greedy_partials(c.vocab))) return rc;
-    if (int rc = alloc(&ticket, 4)) return rc;
+    if (int rc = alloc(&partial, 4 * (size_t)LM_MAX_WG)) return rc;
     if (int rc = alloc(&result, 4)) return rc;
     // RoPE table, gpu_graph.rs:131-133: angle = pos * powf(theta, -(2i)/hd), cos | sin
     std::vector<float> t((size_t)c.max_seq * c.head_dim);
@@ -209,65 +213,54 @@ int Model::build_buffers() {
     return OK;
 }
 
+// One decode step, in the job order of gpu_graph.rs:137-162. The residual
+// stream ping-pongs between R0 and R1: the q|k|v kernel of a layer sums
+// R1 + TMP (the previous down projection) into R0, the gate/up kernel sums
+// R0 + TMP (the o projection) into R1.
 int Model::enqueue_step(hipStream_t s) {
     const auto& c = cfg;
     const int kvd = c.kv_heads * c.head_dim;
     const size_t kvl = (size_t)c.max_seq * kvd;
     const Weight* emb = weight("token_embd.weight");
-    for (int l = 0; l < c.layers; l++) {
+    auto nq_args = [&](const float* xin, const float* res, const float* gamma, float* xout) {
         NormQuantArgs nq{};
-        nq.x = X;
-        nq.residual = TMP;
-        nq.gamma = vec(lname(l, "attn_norm.weight"));
-        nq.xq = XQ;
-        nq.xs = XS;
+        nq.x = xin;
+        nq.residual = res;
+        nq.gamma = gamma;
+        nq.x_out = xout;
         nq.dim = c.dim;
-        nq.add = l > 0;
         nq.eps = c.eps;
+        return nq;
+    };
+    for (int l = 0; l < c.layers; l++) {
+        const Weight& qkv = layers[l].qkv;
+        NormQuantArgs na = nq_args(R1, TMP, vec(lname(l, "attn_norm.weight")), R0);
         if (l == 0) {
-            nq.embed_qs = emb->qs;
-            nq.embed_d = emb->d;
-            nq.token = token;
+            na.embed_qs = emb->qs;
+            na.embed_d = emb->d;
+            na.token = token;
         }
-        launch_resnorm_quant(nq, s);
-        if (int rc = launch_matvec(layers[l].qkv, nullptr, XQ, XS, QKV, s)) return rc;
-        RopeArgs ra{QKV, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")), vec(lname(l, "attn_v.bias")),
-                    trig, pos, kcache + l * kvl, vcache + l * kvl, c.heads, c.kv_heads, c.head_dim};
-        launch_rope_kv(ra, s);
-        AttnArgs aa{QKV, kcache + l * kvl, vcache + l * kvl, pos, ATT, XQ, XS, c.heads, c.kv_heads, c.head_dim,
+        QkvArgs qa{qkv.qs, qkv.d, na, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")),
+                   vec(lname(l, "attn_v.bias")), trig, pos, QKV, kcache + l * kvl, vcache + l * kvl,
+                   c.dim, c.heads, c.kv_heads, c.head_dim};
+        if (launch_qkv_rope(qa, s)) return fail(ERR_SHAPE, "qkv_rope: unsupported dim");
+        AttnArgs aa{QKV, kcache + l * kvl, vcache + l * kvl, pos, nullptr, XQ, XS, c.heads, c.kv_heads, c.head_dim,
                     c.max_seq, (float)(1.0 / std::sqrt((double)c.head_dim))};
-        launch_attention(aa, s);
+        if (launch_attention_q(aa, s)) return fail(ERR_SHAPE, "attention: head_dim / max_seq beyond the LDS budget");
         if (int rc = launch_matvec(*weight(lname(l, "attn_output.weight")), nullptr, XQ, XS, TMP, s)) return rc;
-        NormQuantArgs nf{};
-        nf.x = X;
-        nf.residual = TMP;
-        nf.gamma = vec(lname(l, "ffn_norm.weight"));
-        nf.xq = XQ;
-        nf.xs = XS;
-        nf.dim = c.dim;
-        nf.add = 1;
-        nf.eps = c.eps;
-        launch_resnorm_quant(nf, s);
-        if (int rc = launch_matvec(*weight(lname(l, "ffn_gate.weight")), weight(lname(l, "ffn_up.weight")), XQ, XS,
-                                   GATE, s))
-            return rc;
-        launch_quant_act(GATE, c.hidden, XQ, XS, s);
-        if (int rc = launch_matvec(*weight(lname(l, "ffn_down.weight")), nullptr, XQ, XS, TMP, s)) return rc;
+        const Weight *wg = weight(lname(l, "ffn_gate.weight")), *wu = weight(lname(l, "ffn_up.weight"));
+        GateArgs ga{wg->qs, wu->qs, wg->d, wu->d, nq_args(R0, TMP, vec(lname(l, "ffn_norm.weight")), R1),
+                    nullptr, XQH, XSH, c.hidden, c.dim};
+        if (launch_gateup_q(ga, s)) return fail(ERR_SHAPE, "gate/up: unsupported dim");
+        if (int rc = launch_matvec(*weight(lname(l, "ffn_down.weight")), nullptr, XQH, XSH, TMP, s)) return rc;
     }
-    NormQuantArgs no{};
-    no.x = X;
-    no.residual = TMP;
-    no.gamma = vec("output_norm.weight");
-    no.y = XN;
+    NormQuantArgs no = nq_args(R1, TMP, vec("output_norm.weight"), nullptr);
     no.xq = XQ;
     no.xs = XS;
-    no.dim = c.dim;
-    no.add = 1;
-    no.eps = c.eps;
     launch_resnorm_quant(no, s);
-    if (int rc = launch_matvec(*weight("output.weight"), nullptr, XQ, XS, LOGITS, s)) return rc;
-    GreedyArgs ga{LOGITS, c.vocab, partial, ticket, result, token, pos, history, c.max_seq};
-    launch_greedy(ga, s);
+    const Weight* out = weight("output.weight");
+    LmArgs la{out->qs, out->d, XQ, XS, LOGITS, c.vocab, c.dim, partial, result, token, pos, history, c.max_seq};
+    if (launch_lm_greedy(la, s)) return fail(ERR_SHAPE, "lm_head: unsupported dim");
     return OK;
 }
 
@@ -285,6 +278,14 @@ int Model::prepare() {
     }
     if (int rc = build_buffers()) return rc;
     UQ_CHECK_HIP(hipStreamSynchronize(stream));
+    // UQ_DECODE_EAGER=1 launches the step's kernels directly instead of through
+    // the captured graph (same kernels and order; used to profile per kernel).
+    const char* eager_env = getenv("UQ_DECODE_EAGER");
+    eager = eager_env && eager_env[0] == '1';
+    if (eager) {
+        prepared = true;
+        return OK;
+    }
     UQ_CHECK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     int rc = enqueue_step(stream);
     hipGraph_t g = nullptr;
@@ -297,6 +298,12 @@ int Model::prepare() {
     graph = g;
     UQ_CHECK_HIP(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
     prepared = true;
+    return OK;
+}
+
+int Model::launch_step() {
+    if (eager) return enqueue_step(stream);
+    UQ_CHECK_HIP(hipGraphLaunch(graph_exec, stream));
     return OK;
 }
 
@@ -325,7 +332,7 @@ int uq_decode_step(uq_model_t h, uint32_t tok, int p, uint32_t* next) {
     if (!m || !next) return set_error(ERR_ARG, "decode_step: null pointer");
     if (!m->prepared) return set_error(ERR_ARG, "decode_step: model not prepared");
     if (int rc = m->set_position(tok, p)) return rc;
-    UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+    if (int rc = m->launch_step()) return rc;
     uint32_t res[2] = {0, 0};
     UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 8, hipMemcpyDeviceToHost, m->stream));
     UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
@@ -342,16 +349,18 @@ int uq_decode_run(uq_model_t h, uint32_t tok, int p, int steps, uint32_t* tokens
     if (steps <= 0 || p < 0 || (int64_t)p + steps > m->cfg.max_seq)
         return set_error(ERR_CONTEXT, "decode_run: positions beyond the KV cache");
     if (int rc = m->set_position(tok, p)) return rc;
+    UQ_CHECK_HIP(hipMemsetAsync(m->result + 2, 0, 4, m->stream));
     hipEvent_t e0, e1;
     UQ_CHECK_HIP(hipEventCreate(&e0));
     UQ_CHECK_HIP(hipEventCreate(&e1));
     UQ_CHECK_HIP(hipEventRecord(e0, m->stream));
-    for (int i = 0; i < steps; i++) UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+    for (int i = 0; i < steps; i++)
+        if (int rc = m->launch_step()) return rc;
     UQ_CHECK_HIP(hipEventRecord(e1, m->stream));
     std::vector<uint32_t> out((size_t)steps);
-    uint32_t res[2] = {0, 0};
+    uint32_t res[3] = {0, 0, 0};
     UQ_CHECK_HIP(hipMemcpyAsync(out.data(), m->history + p, 4 * (size_t)steps, hipMemcpyDeviceToHost, m->stream));
-    UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 8, hipMemcpyDeviceToHost, m->stream));
+    UQ_CHECK_HIP(hipMemcpyAsync(res, m->result, 12, hipMemcpyDeviceToHost, m->stream));
     UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
     float t = 0;
     hipEventElapsedTime(&t, e0, e1);
@@ -359,7 +368,7 @@ int uq_decode_run(uq_model_t h, uint32_t tok, int p, int steps, uint32_t* tokens
     hipEventDestroy(e1);
     if (ms) *ms = t;
     std::memcpy(tokens, out.data(), 4 * (size_t)steps);
-    if (res[1]) return set_error(ERR_NONFINITE, "decode_run: non-finite logits");
+    if (res[2]) return set_error(ERR_NONFINITE, "decode_run: non-finite logits");
     return OK;
 }
 
@@ -376,7 +385,7 @@ int uq_prompt_tokens(uq_model_t h, const uint32_t* tokens, int count, int p, uin
         const int pp = p + i;
         UQ_CHECK_HIP(hipMemcpyAsync(m->token, &staged[i], 4, hipMemcpyHostToDevice, m->stream));
         UQ_CHECK_HIP(hipMemcpyAsync(m->pos, &pp, 4, hipMemcpyHostToDevice, m->stream));
-        UQ_CHECK_HIP(hipGraphLaunch(m->graph_exec, m->stream));
+        if (int rc = m->launch_step()) return rc;
         UQ_CHECK_HIP(hipStreamSynchronize(m->stream));
     }
     uint32_t res[2] = {0, 0};

@@ -1,0 +1,55 @@
+// Argument blocks and launchers of the fused decode-step kernels (uq_step.hip).
+// All matrices are Q8_0 planes (int8 quants [rows][k], fp16 scales [rows][k/32]).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "uq_decode.h"
+
+namespace uq {
+
+constexpr int LM_MAX_WG = 2048;  // lm_head grid cap == argmax partial slots
+
+struct QkvArgs {
+    const int8_t* w_qs;       // [heads*hd + 2*kv*hd][dim]
+    const uint16_t* w_d;
+    NormQuantArgs nq;         // prologue: residual sum, RMSNorm, quant of the input
+    const float *bq, *bk, *bv;
+    const float* trig;        // [max_seq][hd]
+    const int* pos;
+    float* q;                 // rotated q [heads*hd]
+    uint16_t* kcache;         // this layer [max_seq][kv*hd]
+    uint16_t* vcache;
+    int dim, heads, kv_heads, head_dim;
+};
+
+struct GateArgs {
+    const int8_t *g_qs, *u_qs;
+    const uint16_t *g_d, *u_d;
+    NormQuantArgs nq;         // prologue: residual sum, RMSNorm, quant of the input
+    float* out;               // optional silu(g)*u [rows]
+    int8_t* oq;               // quantized output [rows]
+    float* os;                // [rows/32]
+    int64_t rows, k;          // rows % 32 == 0
+};
+
+struct LmArgs {
+    const int8_t* w_qs;
+    const uint16_t* w_d;
+    const int8_t* xq;
+    const float* xs;
+    float* logits;
+    int64_t rows, k;
+    void* partial;            // [LM_MAX_WG] 16-byte candidates
+    uint32_t* result;         // [0] id, [1] bad, [2] sticky bad
+    uint32_t* token;          // optional next-step token feedback
+    int* pos;
+    uint32_t* history;
+    int max_seq;
+};
+
+int launch_qkv_rope(const QkvArgs& a, hipStream_t s);
+int launch_attention_q(const AttnArgs& a, hipStream_t s);
+int launch_gateup_q(const GateArgs& a, hipStream_t s);
+int launch_lm_greedy(const LmArgs& a, hipStream_t s);
+
+}  // namespace uq

@@ -1,0 +1,211 @@
+// Per-kind matvec work units shared by the generic matvec and the fused
+// decode-step kernels. A unit is the slice of one row that one lane consumes
+// per step: Q8_0 16 values (one 16-byte load), Q4_K 64 values (one 32-byte qs
+// pair + the superblock header), Q3_K 128 values (half a superblock).
+// term() returns the unit's exact double contribution to the row's dot.
+#pragma once
+#include "uq_device.h"
+
+namespace uq {
+
+struct WArgs {
+    const int8_t* qs;
+    const uint16_t* d;
+    const uint8_t* sc;
+};
+
+// Q8_0 unit: half a block (16 int8 = one 16-byte load). Lanes of a row group
+// read consecutive 16-byte pieces, so one wave instruction covers a contiguous
+// run of the row; weights are streamed with non-temporal loads. The two halves
+// of a block contribute exact double terms c_half * (dw*dx) whose sum equals
+// the block's c * (dw*dx) exactly.
+struct Q8 {
+    static constexpr int UNIT = 16;
+    struct X { int4 a; float s; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        x.a = *(const int4*)(xq + (size_t)u * 16);
+        x.s = xs[u >> 1];
+    }
+    static UQ_DEV void zero_x(X& x) { x.a = make_int4(0, 0, 0, 0); x.s = 0.0f; }
+    struct W { int4 q; uint16_t d; };
+    // weight part of a unit, loadable before the activations are known
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
+        const int64_t piece = row * nu + u;
+        return W{uq_ntload16(w.qs + piece * 16), w.d[piece >> 1]};
+    }
+    static UQ_DEV double dot(const W& wv, const X& x) {
+        int c = uq_dot4(wv.q.x, x.a.x, 0);
+        c = uq_dot4(wv.q.y, x.a.y, c);
+        c = uq_dot4(wv.q.z, x.a.z, c);
+        c = uq_dot4(wv.q.w, x.a.w, c);
+        const float s = uq_half(wv.d) * x.s;
+        return (double)c * (double)s;
+    }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        return dot(load_w(w, row, nu, u), x);
+    }
+};
+
+// Q4_K unit: pair j of a superblock = 32 bytes of qs holding sub-blocks 2j (low
+// nibbles) and 2j+1 (high nibbles). ggml value = d*sc*q - dmin*m per sub-block.
+struct Q4K {
+    static constexpr int UNIT = 64;
+    struct X { int4 a0, a1, b0, b1; float s0, s1; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 64);
+        x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
+        x.s0 = xs[2 * u];
+        x.s1 = xs[2 * u + 1];
+    }
+    static UQ_DEV void zero_x(X& x) {
+        x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
+        x.s0 = x.s1 = 0.0f;
+    }
+    static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
+    static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        const int64_t sb = (row * nu + u) >> 2;  // nu = 4 * superblocks per row
+        const int j = u & 3;
+        const uint8_t* blk = (const uint8_t*)w.qs + sb * 144;
+        const int4 hdr = uq_ntload16(blk);
+        const int4 q0 = uq_ntload16(blk + 16 + 32 * j);
+        const int4 q1 = uq_ntload16(blk + 32 + 32 * j);
+        int il = 0, ih = 0, xl = 0, xh = 0;
+        il = uq_dot4(lo4(q0.x), x.a0.x, il); il = uq_dot4(lo4(q0.y), x.a0.y, il);
+        il = uq_dot4(lo4(q0.z), x.a0.z, il); il = uq_dot4(lo4(q0.w), x.a0.w, il);
+        il = uq_dot4(lo4(q1.x), x.a1.x, il); il = uq_dot4(lo4(q1.y), x.a1.y, il);
+        il = uq_dot4(lo4(q1.z), x.a1.z, il); il = uq_dot4(lo4(q1.w), x.a1.w, il);
+        ih = uq_dot4(hi4(q0.x), x.b0.x, ih); ih = uq_dot4(hi4(q0.y), x.b0.y, ih);
+        ih = uq_dot4(hi4(q0.z), x.b0.z, ih); ih = uq_dot4(hi4(q0.w), x.b0.w, ih);
+        ih = uq_dot4(hi4(q1.x), x.b1.x, ih); ih = uq_dot4(hi4(q1.y), x.b1.y, ih);
+        ih = uq_dot4(hi4(q1.z), x.b1.z, ih); ih = uq_dot4(hi4(q1.w), x.b1.w, ih);
+        const int ones = 0x01010101;
+        xl = uq_dot4(ones, x.a0.x, xl); xl = uq_dot4(ones, x.a0.y, xl);
+        xl = uq_dot4(ones, x.a0.z, xl); xl = uq_dot4(ones, x.a0.w, xl);
+        xl = uq_dot4(ones, x.a1.x, xl); xl = uq_dot4(ones, x.a1.y, xl);
+        xl = uq_dot4(ones, x.a1.z, xl); xl = uq_dot4(ones, x.a1.w, xl);
+        xh = uq_dot4(ones, x.b0.x, xh); xh = uq_dot4(ones, x.b0.y, xh);
+        xh = uq_dot4(ones, x.b0.z, xh); xh = uq_dot4(ones, x.b0.w, xh);
+        xh = uq_dot4(ones, x.b1.x, xh); xh = uq_dot4(ones, x.b1.y, xh);
+        xh = uq_dot4(ones, x.b1.z, xh); xh = uq_dot4(ones, x.b1.w, xh);
+        // header: d (bytes 0-1), dmin (2-3), 12 scale bytes (4-15)
+        const float dd = uq_half((uint16_t)(hdr.x & 0xffff));
+        const float dm = uq_half((uint16_t)((unsigned)hdr.x >> 16));
+        const uint64_t slo = (uint64_t)(uint32_t)hdr.y | ((uint64_t)(uint32_t)hdr.z << 32);
+        const uint32_t shi = (uint32_t)hdr.w;
+        int sc0, m0, sc1, m1;
+        scale_min(2 * j, slo, shi, sc0, m0);
+        scale_min(2 * j + 1, slo, shi, sc1, m1);
+        const float d0 = dd * (float)sc0, n0 = dm * (float)m0;
+        const float d1 = dd * (float)sc1, n1 = dm * (float)m1;
+        const double t0 = (double)x.s0 * ((double)d0 * (double)il - (double)n0 * (double)xl);
+        const double t1 = (double)x.s1 * ((double)d1 * (double)ih - (double)n1 * (double)xh);
+        return t0 + t1;
+    }
+    static UQ_DEV int sbyte(int k, uint64_t lo, uint32_t hi) {
+        return k < 8 ? (int)((lo >> (8 * k)) & 0xff) : (int)((hi >> (8 * (k - 8))) & 0xff);
+    }
+    // ggml get_scale_min_k4 over the 12 scale bytes held in registers
+    static UQ_DEV void scale_min(int j, uint64_t lo, uint32_t hi, int& sc, int& m) {
+        if (j < 4) {
+            sc = sbyte(j, lo, hi) & 63;
+            m = sbyte(j + 4, lo, hi) & 63;
+        } else {
+            sc = (sbyte(j + 4, lo, hi) & 0xF) | ((sbyte(j - 4, lo, hi) >> 6) << 4);
+            m = (sbyte(j + 4, lo, hi) >> 4) | ((sbyte(j, lo, hi) >> 6) << 4);
+        }
+    }
+};
+
+// Q3_K unit: half n of a superblock = 128 values = 4 activation blocks j.
+// Block j's 32 values use qs[32n .. 32n+31] bits 2j..2j+1 and hmask[0..31]
+// bit 4n+j; value = low2 - 4*(1-hbit); sub-blocks of 16 carry 6-bit scales.
+struct Q3K {
+    static constexpr int UNIT = 128;
+    struct X { int4 v[8]; float s[4]; };
+    static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 128);
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.s[k] = xs[4 * u + k];
+    }
+    static UQ_DEV void zero_x(X& x) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = make_int4(0, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.s[k] = 0.0f;
+    }
+    static UQ_DEV int dot16(const int4& w, const int4& xv, int c) {
+        c = uq_dot4(w.x, xv.x, c); c = uq_dot4(w.y, xv.y, c);
+        c = uq_dot4(w.z, xv.z, c); return uq_dot4(w.w, xv.w, c);
+    }
+    static UQ_DEV int4 extract(const int4& q, const int4& h, int shift, int hshift) {
+        int4 r;
+        r.x = (int)((((unsigned)q.x >> shift) & 0x03030303u) | ((((unsigned)h.x >> hshift) & 0x01010101u) << 2));
+        r.y = (int)((((unsigned)q.y >> shift) & 0x03030303u) | ((((unsigned)h.y >> hshift) & 0x01010101u) << 2));
+        r.z = (int)((((unsigned)q.z >> shift) & 0x03030303u) | ((((unsigned)h.z >> hshift) & 0x01010101u) << 2));
+        r.w = (int)((((unsigned)q.w >> shift) & 0x03030303u) | ((((unsigned)h.w >> hshift) & 0x01010101u) << 2));
+        return r;
+    }
+    // 6-bit scale s = 8n + k (k < 8) from the 12 packed bytes held as
+    // lo = bytes 0..7 and s2 = bytes 8..11 (ggml Q3_K scale packing).
+    static UQ_DEV int scale6(uint64_t lo, uint32_t s2, int n, int k) {
+        const int low = (int)((lo >> (8 * k + 4 * n)) & 0xF);
+        const int high = (int)((s2 >> (8 * (k & 3) + 2 * (2 * n + (k >> 2)))) & 3u);
+        return low | (high << 4);
+    }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        const int64_t sb = (row * nu + u) >> 1;  // nu = 2 * superblocks per row
+        const int n = u & 1;
+        const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
+        const int4 h0 = uq_ntload16(blk), h1 = uq_ntload16(blk + 16);
+        const int4 q0 = uq_ntload16(blk + 32 + 32 * n), q1 = uq_ntload16(blk + 48 + 32 * n);
+        const uint32_t* sp = (const uint32_t*)(w.sc + sb * 12);
+        const uint64_t slo = (uint64_t)sp[0] | ((uint64_t)sp[1] << 32);
+        const uint32_t s2 = sp[2];
+        const float dd = uq_half(w.d[sb]);
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 w0 = extract(q0, h0, 2 * j, 4 * n + j), w1 = extract(q1, h1, 2 * j, 4 * n + j);
+            const int4 xa = x.v[2 * j], xb = x.v[2 * j + 1];
+            const int ones = 0x01010101;
+            int i0 = dot16(w0, xa, 0), i1 = dot16(w1, xb, 0);
+            const int s0x = dot16(make_int4(ones, ones, ones, ones), xa, 0);
+            const int s1x = dot16(make_int4(ones, ones, ones, ones), xb, 0);
+            i0 -= 4 * s0x;
+            i1 -= 4 * s1x;
+            const float dl0 = dd * (float)(scale6(slo, s2, n, 2 * j) - 32);
+            const float dl1 = dd * (float)(scale6(slo, s2, n, 2 * j + 1) - 32);
+            const double inner = (double)dl0 * (double)i0 + (double)dl1 * (double)i1;
+            acc += (double)x.s[j] * inner;
+        }
+        return acc;
+    }
+};
+
+
+// Activation units of one lane (units sub, sub+LPR, ...) kept in registers.
+template <class KQ, int LPR, int NBL>
+UQ_DEV void load_xr(typename KQ::X* xr, const int8_t* xq, const float* xs, int64_t nu, int sub) {
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i;
+        if (u < nu) KQ::load_x(xr[i], xq, xs, u);
+        else KQ::zero_x(xr[i]);
+    }
+}
+// This lane's share of row `row`, summed over the LPR lanes of its group.
+template <class KQ, int LPR, int NBL>
+UQ_DEV double row_dot(const WArgs& w, int64_t row, int64_t nu, int sub, const typename KQ::X* xr) {
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i;
+        if (u < nu) acc += KQ::term(w, row, nu, u, xr[i]);
+    }
+    return uq_group_sum<LPR>(acc);
+}
+
+}  // namespace uq

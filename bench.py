@@ -81,28 +81,54 @@ def cpu_baseline(seconds=10.0):
 
 
 def decode_bench(prompt_len=512, steps=128):
-    """Qwen2.5-1.5B-architecture Q8_0 greedy decode, bs=1: the prompt of seeded
-    uniform ids fills the fp16 KV cache, then `steps` decode steps (one hipGraph
-    launch each, greedy id fed back on the device) are timed with HIP events."""
+    """Qwen2.5-1.5B-architecture Q8_0 greedy run, bs=1, random-init weights: a
+    512-token prompt of seeded uniform ids through the int8-MFMA prefill, then
+    `steps` decode steps (one hipGraph launch each, greedy id fed back on the
+    device) timed with HIP events. Prefill is timed on the host clock around
+    the synchronous call."""
     cfg = dict(uq.QWEN25_15B, max_seq=1024)
     t0 = time.perf_counter()
     model = uq.Qwen2Model(cfg, uq.synth_qwen2(cfg, 0x5EED0002))
     t_load = time.perf_counter() - t0
     prompt = uq.synth_tokens(0x5EED0002, prompt_len, cfg["vocab"])
-    t0 = time.perf_counter()
-    first = model.prompt(prompt, 0)
-    t_prompt = time.perf_counter() - t0
-    model.decode_run(first, prompt_len, 8)          # warm-up over the same positions
+    model.prefill(prompt)                             # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        first = model.prefill(prompt)
+        times.append(time.perf_counter() - t0)
+    t_prefill = min(times)
+    model.decode_run(first, prompt_len, 8)            # warm-up over the same positions
     ids, ms = model.decode_run(first, prompt_len, steps)
     weight_bytes = 28 * 49717248 + 247959552
     kv_bytes = sum(28 * 2 * (prompt_len + i + 1) * 256 * 2 for i in range(steps))
-    tok_s = steps / (ms / 1e3)
     model.free()
-    return {"tok_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "prompt": prompt_len,
-            "steps": steps, "model_upload_s": round(t_load, 1), "prompt_ingest_s": round(t_prompt, 2),
-            "weight_bytes_per_token": weight_bytes,
+    return {"tok_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4), "prompt": prompt_len,
+            "steps": steps, "weight_bytes_per_token": weight_bytes,
             "effective_GBs": round((weight_bytes * steps + kv_bytes) / (ms / 1e3) / 1e9, 1),
-            "first_ids": [int(i) for i in ids[:8]]}
+            "prefill_tok_s": round(prompt_len / t_prefill, 1), "prefill_ms": round(t_prefill * 1e3, 3),
+            "model_upload_s": round(t_load, 1), "first_ids": [int(first)] + [int(i) for i in ids[:7]]}
+
+
+def prefill_gemm_bench(tokens=512, reps=20):
+    """512-token Q8_0 prefill GEMMs (N x K) 1536x1536, 256x1536, 8960x1536 gate+up
+    pair (one fused launch), 1536x8960 on int8 MFMA: TOPS = 2*M*N*K / time."""
+    out = {}
+    tot_ops, tot_ms = 0, 0.0
+    for name, N, K, pair in SHAPES[:4]:
+        w = uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0xABC + N + K, N, K))
+        w2 = uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0xABD + N + K, N, K)) if pair else None
+        ms = uq.time_prefill_gemm(w, w2, tokens, reps)
+        ops = 2 * tokens * N * K * (2 if pair else 1)
+        out[name] = {"ms": round(ms, 4), "TOPS": round(ops / (ms / 1e3) / 1e12, 2)}
+        tot_ops += ops
+        tot_ms += ms
+        w.free()
+        if w2:
+            w2.free()
+    out["aggregate_TOPS"] = round(tot_ops / (tot_ms / 1e3) / 1e12, 2)
+    out["int8_mfma_peak_TOPS"] = 5000.0
+    return out
 
 
 def main():
@@ -164,6 +190,7 @@ def main():
         w.free()
     if not args.no_decode:
         result["decode"] = decode_bench()
+        result["prefill_gemm"] = prefill_gemm_bench()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -91,6 +91,15 @@ int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const fl
 int uq_quant_act(const float* x, int64_t n, int8_t* q, float* scale);
 int uq_block_dots(uq_weight_t w, const float* x, int64_t n, int32_t* dots, int64_t count);
 
+/* The prefill GEMM alone (prefill_gemm, gpu_prefill.cu:74-100; CPU check
+ * gpu_prefill.rs:95-121): y[t][r] for `tokens` rows of pre-quantized
+ * activations xq[t][n] with scales xs[t][n/32], host memory. Q8_0, m % 64. */
+int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t tokens, float* y);
+
+/* Mean HIP-event time of the prefill GEMM on `tokens` synthetic activations
+ * (w2 non-null: the fused gate/up pair), `reps` launches. Measurement aid. */
+int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps, double* ms);
+
 /* ---------------------------------------------------------------- memory + timing
  * Small helpers so harnesses need no other GPU runtime binding. */
 int uq_dev_alloc(size_t bytes, void** ptr);
@@ -144,6 +153,11 @@ int uq_decode_run(uq_model_t m, uint32_t token, int pos, int steps, uint32_t* to
  * positions pos..pos+count-1 (the per-token forward of llm.rs:339-388); next =
  * greedy id after the last prompt token. */
 int uq_prompt_tokens(uq_model_t m, const uint32_t* tokens, int count, int pos, uint32_t* next);
+/* prepare_prefill + run_prefill (gpu_prefill.rs:122-157): the prompt at
+ * positions 0..count-1 through int8-MFMA GEMMs and causal attention, filling
+ * the fp16 KV cache; next = greedy id after the last prompt token. The decode
+ * step continues at pos = count. count <= min(max_seq, 1024). */
+int uq_prefill(uq_model_t m, const uint32_t* tokens, int count, uint32_t* next);
 /* LOGITS readback of verify_gpu_greedy (gpu_graph.rs:14-23). */
 int uq_model_logits(uq_model_t m, float* out, int64_t n);
 /* fp16 KV cache readback of positions [0, count) of one layer ([count][kv*hd]). */

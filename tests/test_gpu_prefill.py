@@ -1,0 +1,93 @@
+"""GPU prefill (int8 MFMA GEMM + batched norm/RoPE/attention) against the
+oracle, through the C ABI. The GEMM keeps the reference's sequential per-block
+fmaf update (gpu_prefill.cu:93-94), so outputs are compared bit for bit; the
+int32 block dots inside it are exact by construction of that comparison."""
+import numpy as np
+import pytest
+
+import oracle as O
+import uq
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(layers=2, dim=256, hidden=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, max_seq=128,
+             eps=1e-6, theta=1e6)
+
+
+def ulps(a, b):
+    a = a.view(np.int32).astype(np.int64)
+    b = b.view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
+
+
+def quant_rows(X):
+    qs = [O.quant_act(x) for x in X]
+    return np.stack([q for q, _ in qs]), np.stack([s for _, s in qs])
+
+
+@pytest.mark.parametrize("N,K,T", [(1536, 1536, 512), (256, 1536, 77), (8960, 1536, 64), (1536, 8960, 40),
+                                   (64, 32, 1), (128, 64, 130)])
+def test_prefill_gemm_bit_exact(gpu, N, K, T):
+    raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0003 + N, N, K)
+    X = np.stack([uq.synth_normal(0x5EED0003 + t, K) for t in range(T)])
+    qx, xs = quant_rows(X)
+    w = uq.Weight(uq.KIND_Q8_0, K, N, raw)
+    y = uq.prefill_gemm(w, qx, xs)
+    ref = O.prefill_gemm(raw, K, N, xs, qx, T)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), ulps(y, ref).max()
+
+
+def build(cfg, seed):
+    t = uq.synth_qwen2(cfg, seed)
+    return uq.Qwen2Model(cfg, t), O.Model(cfg, {k: v[3] for k, v in t.items()})
+
+
+@pytest.mark.parametrize("n", [1, 7, 64, 100])
+def test_prefill_matches_oracle(gpu, n):
+    g, o = build(SMALL, 21)
+    toks = uq.synth_tokens(21 + n, n, SMALL["vocab"])
+    nxt = g.prefill(toks)
+    rc, onxt, olg = o.prefill(toks, want_logits=True)
+    assert rc == 0
+    assert ulps(g.logits(), olg).max() <= 1
+    assert nxt == onxt
+    for layer in range(SMALL["layers"]):
+        k, v = g.kv(layer, n)
+        assert np.array_equal(k, o.keys(layer, n)) and np.array_equal(v, o.values(layer, n))
+
+
+def test_prefill_then_decode(gpu):
+    g, o = build(SMALL, 33)
+    toks = uq.synth_tokens(33, 50, SMALL["vocab"])
+    first = g.prefill(toks)
+    rc, ofirst, _ = o.prefill(toks)
+    assert rc == 0 and first == ofirst
+    ids, _ = g.decode_run(first, 50, 30)
+    tok, ref = ofirst, []
+    for pos in range(50, 80):
+        rc, tok, _ = o.decode(tok, pos)
+        assert rc == 0
+        ref.append(tok)
+    assert list(ids) == ref
+
+
+def test_prefill_qwen25_shapes_two_layers(gpu):
+    cfg = dict(uq.QWEN25_15B, layers=2, max_seq=256)
+    g, o = build(cfg, 0x5EED0002)
+    toks = uq.synth_tokens(0x5EED0002, 96, cfg["vocab"])
+    nxt = g.prefill(toks)
+    rc, onxt, olg = o.prefill(toks, want_logits=True)
+    assert rc == 0 and nxt == onxt
+    assert ulps(g.logits(), olg).max() <= 1
+
+
+def test_prefill_rejects_bad_input(gpu):
+    g, _ = build(SMALL, 4)
+    with pytest.raises(uq.UqError) as e:
+        g.prefill(np.array([SMALL["vocab"]], np.uint32))
+    assert e.value.status == uq.Error.SHAPE
+    with pytest.raises(uq.UqError) as e:
+        g.prefill(np.zeros(SMALL["max_seq"] + 1, np.uint32))
+    assert e.value.status == uq.Error.CONTEXT

@@ -39,10 +39,11 @@ __device__ inline float block_max_f(float v, float* red) {
 
 // Residual + RMSNorm + block-32 quant of a.dim values by one workgroup of WG
 // threads (element i = j*WG + t, so each 32-block sits in half a wave). The
-// quantized vector goes to q/s (LDS or global); write_x stores the summed
-// residual to a.x_out. Ends with a barrier.
+// quantized vector goes to q/s (LDS or global; scale b at s[b * sstride]);
+// write_x stores the summed residual to a.x_out. Ends with a barrier.
 template <int WG>
-__device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red) {
+__device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red,
+                                  int sstride = 1) {
     constexpr int PER = (4096 + WG - 1) / WG;  // dim <= 4096
     const int t = threadIdx.x, D = a.dim;
     float xv[PER];
@@ -78,7 +79,7 @@ __device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* 
             float sc;
             const int8_t qv = uq_quant_lane(y, &sc);
             q[i] = qv;
-            if ((t & 31) == 0) s[i >> 5] = sc;
+            if ((t & 31) == 0) s[(i >> 5) * sstride] = sc;
         }
     }
     __syncthreads();

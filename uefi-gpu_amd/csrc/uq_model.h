@@ -11,6 +11,8 @@ namespace uq {
 
 struct LayerDev {
     Weight qkv;  // q|k|v rows of one layer in one Q8_0 weight
+    // fp16 weight scales transposed to [k/32][rows] for the prefill GEMM
+    uint16_t *qkv_dt = nullptr, *o_dt = nullptr, *g_dt = nullptr, *u_dt = nullptr, *d_dt = nullptr;
 };
 
 struct Model {
@@ -34,6 +36,12 @@ struct Model {
     uint32_t* partial = nullptr;
     uint32_t host_io[4] = {0, 0, 0, 0};
 
+    // prefill arenas, sized for pcap tokens (padded to the GEMM tile)
+    int pcap = 0;
+    float *PX = nullptr, *PTMP = nullptr, *PY = nullptr, *PATT = nullptr, *PG = nullptr, *PXST = nullptr;
+    int8_t* PXQ = nullptr;
+    uint32_t* PTOK = nullptr;
+
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
 
@@ -50,6 +58,8 @@ struct Model {
     int prepare();
     int set_position(uint32_t tok, int p);
     int launch_step();
+    int build_prefill();
+    int prefill(const uint32_t* tokens, int n, uint32_t* next);
 };
 
 }  // namespace uq

@@ -8,6 +8,7 @@
 #include "uq_internal.h"
 #include "uq_decode.h"
 #include "uq_step.h"
+#include "uq_prefill.h"
 #include "uq_model.h"
 #include "../../include/uq.h"
 
@@ -277,6 +278,7 @@ int Model::prepare() {
         }
     }
     if (int rc = build_buffers()) return rc;
+    if (int rc = build_prefill()) return rc;
     UQ_CHECK_HIP(hipStreamSynchronize(stream));
     // UQ_DECODE_EAGER=1 launches the step's kernels directly instead of through
     // the captured graph (same kernels and order; used to profile per kernel).
@@ -298,6 +300,120 @@ int Model::prepare() {
     graph = g;
     UQ_CHECK_HIP(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0));
     prepared = true;
+    return OK;
+}
+
+// Prefill arenas and the transposed weight scales of every layer.
+int Model::build_prefill() {
+    const auto& c = cfg;
+    const int kvd = c.kv_heads * c.head_dim, nqkv = c.dim + 2 * kvd;
+    const int cap = c.max_seq < 1024 ? c.max_seq : 1024;
+    pcap = (cap + 63) / 64 * 64;
+    const int big = c.hidden > nqkv ? c.hidden : nqkv;
+    if (int rc = alloc(&PX, (size_t)pcap * c.dim)) return rc;
+    if (int rc = alloc(&PTMP, (size_t)pcap * c.dim)) return rc;
+    if (int rc = alloc(&PY, (size_t)pcap * nqkv)) return rc;
+    if (int rc = alloc(&PATT, (size_t)pcap * c.dim)) return rc;
+    if (int rc = alloc(&PG, (size_t)pcap * c.hidden)) return rc;
+    if (int rc = alloc(&PXQ, (size_t)pcap * big)) return rc;
+    if (int rc = alloc(&PXST, (size_t)pcap * big / 32)) return rc;
+    if (int rc = alloc(&PTOK, (size_t)pcap)) return rc;
+    auto tr = [&](const Weight& w, uint16_t** dt) -> int {
+        if (int rc = alloc(dt, (size_t)w.m * (w.n / 32))) return rc;
+        launch_transpose_scales(w.d, w.m, w.n / 32, *dt, stream);
+        return OK;
+    };
+    for (int l = 0; l < c.layers; l++) {
+        LayerDev& L = layers[l];
+        if (int rc = tr(L.qkv, &L.qkv_dt)) return rc;
+        if (int rc = tr(*weight(lname(l, "attn_output.weight")), &L.o_dt)) return rc;
+        if (int rc = tr(*weight(lname(l, "ffn_gate.weight")), &L.g_dt)) return rc;
+        if (int rc = tr(*weight(lname(l, "ffn_up.weight")), &L.u_dt)) return rc;
+        if (int rc = tr(*weight(lname(l, "ffn_down.weight")), &L.d_dt)) return rc;
+    }
+    UQ_CHECK_HIP(hipGetLastError());
+    UQ_CHECK_HIP(hipStreamSynchronize(stream));
+    return OK;
+}
+
+// Prompt prefill at positions 0..n-1 in the job order of prepare_prefill
+// (gpu_prefill.rs:122-150): per layer norm+quant, q|k|v GEMM, RoPE + KV,
+// causal attention, quant, o GEMM, norm+quant, gate/up GEMM with SiLU, quant,
+// down GEMM; then the last token's residual through the decode output head.
+int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
+    const auto& c = cfg;
+    if (n <= 0 || n > pcap || n > c.max_seq) return fail(ERR_CONTEXT, "prefill: prompt longer than the prefill window");
+    for (int i = 0; i < n; i++)
+        if ((int64_t)tokens[i] >= c.vocab) return fail(ERR_SHAPE, "prefill: token id beyond the vocabulary");
+    const int kvd = c.kv_heads * c.head_dim, nqkv = c.dim + 2 * kvd;
+    const int mp = (n + 63) / 64 * 64;
+    const size_t kvl = (size_t)c.max_seq * kvd;
+    const hipStream_t s = stream;
+    const Weight* emb = weight("token_embd.weight");
+    UQ_CHECK_HIP(hipMemcpyAsync(PTOK, tokens, 4 * (size_t)n, hipMemcpyHostToDevice, s));
+    auto norm = [&](int l, const float* gamma, bool first) {
+        PfNormArgs na{};
+        na.nq.gamma = gamma;
+        na.nq.dim = c.dim;
+        na.nq.eps = c.eps;
+        if (first) {
+            na.nq.embed_qs = emb->qs;
+            na.nq.embed_d = emb->d;
+            na.tokens = PTOK;
+        } else {
+            na.residual = PTMP;
+        }
+        na.x = PX;
+        na.xq = PXQ;
+        na.xst = PXST;
+        na.mp = mp;
+        launch_pf_norm(na, n, s);
+    };
+    auto gemm = [&](const Weight& w, const uint16_t* dt, const Weight* w2, const uint16_t* dt2, float* y) {
+        PfGemmArgs ga{w.qs, dt, w2 ? w2->qs : nullptr, dt2, PXQ, PXST, y, w.m, w.n, mp};
+        return launch_pf_gemm(ga, s);
+    };
+    for (int l = 0; l < c.layers; l++) {
+        const LayerDev& L = layers[l];
+        norm(l, vec(lname(l, "attn_norm.weight")), l == 0);
+        if (gemm(L.qkv, L.qkv_dt, nullptr, nullptr, PY)) return fail(ERR_SHAPE, "prefill: q|k|v rows not a multiple of 64");
+        PfRopeArgs ra{PY, nqkv, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")), vec(lname(l, "attn_v.bias")),
+                      trig, kcache + l * kvl, vcache + l * kvl, 0, c.heads, c.kv_heads, c.head_dim};
+        launch_pf_rope_kv(ra, n, s);
+        PfAttnArgs aa{PY, nqkv, kcache + l * kvl, vcache + l * kvl, PATT, n, 0, pcap, c.heads, c.kv_heads, c.head_dim,
+                      (float)(1.0 / std::sqrt((double)c.head_dim))};
+        if (launch_pf_attention(aa, s)) return fail(ERR_SHAPE, "prefill: attention head_dim unsupported");
+        launch_pf_quant(PATT, c.dim, n, mp, PXQ, PXST, s);
+        if (gemm(*weight(lname(l, "attn_output.weight")), L.o_dt, nullptr, nullptr, PTMP))
+            return fail(ERR_SHAPE, "prefill: o rows not a multiple of 64");
+        norm(l, vec(lname(l, "ffn_norm.weight")), false);
+        if (gemm(*weight(lname(l, "ffn_gate.weight")), L.g_dt, weight(lname(l, "ffn_up.weight")), L.u_dt, PG))
+            return fail(ERR_SHAPE, "prefill: ffn rows not a multiple of 64");
+        launch_pf_quant(PG, c.hidden, n, mp, PXQ, PXST, s);
+        if (gemm(*weight(lname(l, "ffn_down.weight")), L.d_dt, nullptr, nullptr, PTMP))
+            return fail(ERR_SHAPE, "prefill: down rows not a multiple of 64");
+    }
+    // the last prompt token through the decode output head (gpu_prefill.rs:138-148)
+    NormQuantArgs no{};
+    no.x = PX + (size_t)(n - 1) * c.dim;
+    no.residual = PTMP + (size_t)(n - 1) * c.dim;
+    no.gamma = vec("output_norm.weight");
+    no.xq = XQ;
+    no.xs = XS;
+    no.dim = c.dim;
+    no.eps = c.eps;
+    launch_resnorm_quant(no, s);
+    host_io[1] = (uint32_t)(n - 1);
+    UQ_CHECK_HIP(hipMemcpyAsync(pos, &host_io[1], 4, hipMemcpyHostToDevice, s));
+    const Weight* out = weight("output.weight");
+    LmArgs la{out->qs, out->d, XQ, XS, LOGITS, c.vocab, c.dim, partial, result, token, pos, history, c.max_seq};
+    if (launch_lm_greedy(la, s)) return fail(ERR_SHAPE, "lm_head: unsupported dim");
+    UQ_CHECK_HIP(hipGetLastError());
+    uint32_t res[2] = {0, 0};
+    UQ_CHECK_HIP(hipMemcpyAsync(res, result, 8, hipMemcpyDeviceToHost, s));
+    UQ_CHECK_HIP(hipStreamSynchronize(s));
+    if (res[1]) return fail(ERR_NONFINITE, "prefill: non-finite logits");
+    *next = res[0];
     return OK;
 }
 
@@ -394,6 +510,95 @@ int uq_prompt_tokens(uq_model_t h, const uint32_t* tokens, int count, int p, uin
     if (res[1]) return set_error(ERR_NONFINITE, "prompt_tokens: non-finite logits");
     *next = res[0];
     return OK;
+}
+
+int uq_prefill(uq_model_t h, const uint32_t* tokens, int count, uint32_t* next) {
+    Model* m = (Model*)h;
+    if (!m || !tokens || !next) return set_error(ERR_ARG, "prefill: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "prefill: model not prepared");
+    return m->prefill(tokens, count, next);
+}
+
+int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t tokens, float* y) {
+    if (!w || !xq || !xs || !y) return set_error(ERR_ARG, "prefill_gemm: null pointer");
+    const Weight& W = w->w;
+    if (W.kind != KIND_Q8_0) return set_error(ERR_QUANT_TYPE, "prefill_gemm: Q8_0 only");
+    if (W.m % 64 || tokens <= 0 || tokens > 4096) return set_error(ERR_SHAPE, "prefill_gemm: rows % 64, 1..4096 tokens");
+    hipStream_t s = (hipStream_t)uq_stream();
+    const int64_t k = W.n, nb = k / 32, mp = (tokens + 63) / 64 * 64;
+    std::vector<float> xst((size_t)(nb * mp), 0.0f);
+    for (int64_t t = 0; t < tokens; t++)
+        for (int64_t b = 0; b < nb; b++) xst[b * mp + t] = xs[t * nb + b];
+    uint16_t* dt = nullptr;
+    int8_t* dq = nullptr;
+    float *ds = nullptr, *dy = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&dt, 2 * (size_t)(nb * W.m)));
+    UQ_CHECK_HIP(hipMalloc(&dq, (size_t)(mp * k)));
+    UQ_CHECK_HIP(hipMalloc(&ds, 4 * xst.size()));
+    UQ_CHECK_HIP(hipMalloc(&dy, 4 * (size_t)(mp * W.m)));
+    UQ_CHECK_HIP(hipMemsetAsync(dq, 0, (size_t)(mp * k), s));
+    UQ_CHECK_HIP(hipMemcpyAsync(dq, xq, (size_t)(tokens * k), hipMemcpyHostToDevice, s));
+    UQ_CHECK_HIP(hipMemcpyAsync(ds, xst.data(), 4 * xst.size(), hipMemcpyHostToDevice, s));
+    launch_transpose_scales(W.d, W.m, nb, dt, s);
+    PfGemmArgs ga{W.qs, dt, nullptr, nullptr, dq, ds, dy, W.m, k, (int)mp};
+    int rc = launch_pf_gemm(ga, s) ? set_error(ERR_SHAPE, "prefill_gemm: shape") : OK;
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && rc == OK) e = hipMemcpyAsync(y, dy, 4 * (size_t)(tokens * W.m), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    hipFree(dt);
+    hipFree(dq);
+    hipFree(ds);
+    hipFree(dy);
+    if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("prefill_gemm: ") + hipGetErrorString(e));
+    return rc;
+}
+
+int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps, double* ms) {
+    if (!w || reps <= 0 || !ms) return set_error(ERR_ARG, "time_prefill_gemm: bad args");
+    const Weight& W = w->w;
+    if (W.kind != KIND_Q8_0 || W.m % 64 || tokens <= 0 || tokens > 4096)
+        return set_error(ERR_SHAPE, "time_prefill_gemm: Q8_0, rows % 64, 1..4096 tokens");
+    if (w2 && (w2->w.m != W.m || w2->w.n != W.n)) return set_error(ERR_SHAPE, "time_prefill_gemm: pair shapes differ");
+    hipStream_t s = (hipStream_t)uq_stream();
+    const int64_t k = W.n, nb = k / 32, mp = (tokens + 63) / 64 * 64;
+    std::vector<int8_t> hq((size_t)(mp * k));
+    std::vector<float> hs((size_t)(nb * mp));
+    for (size_t i = 0; i < hq.size(); i++) hq[i] = (int8_t)((int)((i * 2654435761u) >> 24) % 255 - 127);
+    for (size_t i = 0; i < hs.size(); i++) hs[i] = 0.01f + 0.001f * (float)(i % 7);
+    uint16_t *dt = nullptr, *dt2 = nullptr;
+    int8_t* dq = nullptr;
+    float *ds = nullptr, *dy = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&dt, 2 * (size_t)(nb * W.m)));
+    if (w2) UQ_CHECK_HIP(hipMalloc(&dt2, 2 * (size_t)(nb * W.m)));
+    UQ_CHECK_HIP(hipMalloc(&dq, hq.size()));
+    UQ_CHECK_HIP(hipMalloc(&ds, 4 * hs.size()));
+    UQ_CHECK_HIP(hipMalloc(&dy, 4 * (size_t)(mp * W.m)));
+    UQ_CHECK_HIP(hipMemcpyAsync(dq, hq.data(), hq.size(), hipMemcpyHostToDevice, s));
+    UQ_CHECK_HIP(hipMemcpyAsync(ds, hs.data(), 4 * hs.size(), hipMemcpyHostToDevice, s));
+    launch_transpose_scales(W.d, W.m, nb, dt, s);
+    if (w2) launch_transpose_scales(w2->w.d, W.m, nb, dt2, s);
+    PfGemmArgs ga{W.qs, dt, w2 ? w2->w.qs : nullptr, dt2, dq, ds, dy, W.m, k, (int)mp};
+    hipEvent_t e0, e1;
+    UQ_CHECK_HIP(hipEventCreate(&e0));
+    UQ_CHECK_HIP(hipEventCreate(&e1));
+    int rc = launch_pf_gemm(ga, s) ? set_error(ERR_SHAPE, "time_prefill_gemm: shape") : OK;
+    if (rc == OK) {
+        UQ_CHECK_HIP(hipEventRecord(e0, s));
+        for (int r = 0; r < reps; r++) launch_pf_gemm(ga, s);
+        UQ_CHECK_HIP(hipEventRecord(e1, s));
+        UQ_CHECK_HIP(hipEventSynchronize(e1));
+        float t = 0;
+        UQ_CHECK_HIP(hipEventElapsedTime(&t, e0, e1));
+        *ms = t / reps;
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipFree(dt);
+    if (dt2) hipFree(dt2);
+    hipFree(dq);
+    hipFree(ds);
+    hipFree(dy);
+    return rc;
 }
 
 int uq_model_logits(uq_model_t h, float* out, int64_t n) {

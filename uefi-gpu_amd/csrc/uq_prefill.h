@@ -1,0 +1,62 @@
+// Argument blocks and launchers of the prefill kernels (uq_prefill.hip).
+// Token-major activations: x[t][dim] f32, xq[t][k] int8, xst[k/32][mp] f32
+// (scales transposed so a GEMM lane reads its token's scale with one load);
+// mp = token count padded to the GEMM tile (64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "uq_decode.h"
+
+namespace uq {
+
+struct PfNormArgs {
+    NormQuantArgs nq;        // gamma, eps, dim, embedding planes (layer 0)
+    float* x;                // residual rows [n][dim], updated in place
+    const float* residual;   // added rows [n][dim] (null for the embedding)
+    const uint32_t* tokens;  // token ids [n] when embedding
+    int8_t* xq;              // [mp][dim]
+    float* xst;              // [dim/32][mp]
+    int mp;
+};
+
+struct PfGemmArgs {
+    const int8_t* w_qs;      // [n][k]
+    const uint16_t* w_dt;    // fp16 scales transposed [k/32][n]
+    const int8_t* w2_qs;     // second matrix (up) for the gate/up SiLU epilogue, or null
+    const uint16_t* w2_dt;
+    const int8_t* xq;        // [mp][k]
+    const float* xst;        // [k/32][mp]
+    float* y;                // [mp][n]
+    int64_t n, k;
+    int mp;
+};
+
+struct PfRopeArgs {
+    float* qkv;              // rows [n][stride]: q | k | v
+    int stride;
+    const float *bq, *bk, *bv;
+    const float* trig;
+    uint16_t* kcache;        // this layer
+    uint16_t* vcache;
+    int p0, heads, kv_heads, head_dim;
+};
+
+struct PfAttnArgs {
+    const float* qkv;        // rotated q rows [n][stride]
+    int stride;
+    const uint16_t* kcache;
+    const uint16_t* vcache;
+    float* out;              // [n][heads*hd]
+    int n, p0, kcap;         // queries, first position, key capacity (>= p0 + n)
+    int heads, kv_heads, head_dim;
+    float qscale;
+};
+
+void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, uint16_t* dt, hipStream_t s);
+void launch_pf_norm(const PfNormArgs& a, int tokens, hipStream_t s);
+void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, float* xst, hipStream_t s);
+int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s);
+void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s);
+int launch_pf_attention(const PfAttnArgs& a, hipStream_t s);
+
+}  // namespace uq

@@ -82,6 +82,9 @@ _SIGS = {
     "uq_decode_run": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, _c_u32p,
                                      ctypes.POINTER(ctypes.c_double)]),
     "uq_model_logits": (ctypes.c_int, [_vp, _c_f32p, _i64]),
+    "uq_prefill": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, _c_u32p]),
+    "uq_prefill_gemm": (ctypes.c_int, [_vp, _c_i8p, _c_f32p, _i64, _c_f32p]),
+    "uq_time_prefill_gemm": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "uq_prompt_tokens": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p]),
     "uq_probe_bandwidth": (ctypes.c_int, [_i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double)]),
@@ -225,6 +228,22 @@ def block_dots(w, x):
     return d.reshape(w.m, w.n // bsz)
 
 
+def prefill_gemm(w, xq, xs):
+    """The int8-MFMA prefill GEMM on pre-quantized activations xq [tokens][n], xs [tokens][n/32]."""
+    xq = np.ascontiguousarray(xq, np.int8)
+    xs = np.ascontiguousarray(xs, np.float32)
+    tokens = xq.shape[0]
+    y = np.empty((tokens, w.m), np.float32)
+    _check(lib().uq_prefill_gemm(w.handle, _p(xq, _c_i8p), _p(xs, _c_f32p), tokens, _p(y, _c_f32p)))
+    return y
+
+
+def time_prefill_gemm(w, w2, tokens, reps):
+    ms = ctypes.c_double()
+    _check(lib().uq_time_prefill_gemm(w.handle, w2.handle if w2 else None, tokens, reps, ctypes.byref(ms)))
+    return ms.value
+
+
 def probe_bandwidth(nbytes=1 << 30, reps=10):
     r, c = ctypes.c_double(), ctypes.c_double()
     _check(lib().uq_probe_bandwidth(nbytes, reps, ctypes.byref(r), ctypes.byref(c)))
@@ -358,6 +377,12 @@ class Qwen2Model:
         ms = ctypes.c_double()
         _check(lib().uq_decode_run(self.handle, token, pos, steps, _p(out, _c_u32p), ctypes.byref(ms)))
         return out, ms.value
+
+    def prefill(self, tokens):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        nxt = ctypes.c_uint32()
+        _check(lib().uq_prefill(self.handle, _p(t, _c_u32p), t.size, ctypes.byref(nxt)))
+        return nxt.value
 
     def prompt(self, tokens, pos=0):
         t = np.ascontiguousarray(tokens, np.uint32)

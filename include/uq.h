@@ -163,6 +163,29 @@ int uq_model_logits(uq_model_t m, float* out, int64_t n);
 /* fp16 KV cache readback of positions [0, count) of one layer ([count][kv*hd]). */
 int uq_model_kv(uq_model_t m, int layer, int count, uint16_t* keys, uint16_t* values);
 
+/* ---------------------------------------------------------------- MoE expert FFN */
+/* Forward::ffn (driver/src/frontier_forward.rs:164-199) for one token: softmax
+ * routing over `experts` router logits, stable top-k (score descending, id
+ * ascending), weights score/sum(top-k); per selected expert and for the shared
+ * expert down(silu(gate x) * (up x)) with int8 activations per 32; combine in
+ * rank order, shared expert weighted by sigmoid(gate_inp . x). The expert
+ * matrices live in one HBM-resident bank per projection; the routing result
+ * stays on the device (the FrontierJob table of frontier_quant.cu:277-299). */
+typedef struct uq_moe* uq_moe_t;
+int uq_moe_create(int32_t dim, int32_t ff, int32_t experts, int32_t top_k, uint32_t expert_kind, uq_moe_t* out);
+int uq_moe_free(uq_moe_t m);
+/* GGUF bytes of expert e: gate and up (ff rows x dim), down (dim rows x ff). */
+int uq_moe_set_expert(uq_moe_t m, int32_t e, const void* gate, const void* up, const void* down);
+/* Shared expert (ffn_{gate,up,down}_shexp) and its f32 gate vector
+ * ffn_gate_inp_shexp of dim values (NULL: weight 1). */
+int uq_moe_set_shared(uq_moe_t m, uint32_t kind, const void* gate, const void* up, const void* down,
+                      const float* gate_inp);
+/* Host-memory call: x (dim), router logits (experts) -> out (dim); optional
+ * ids/weights (top_k) of the routing. Non-finite input -> UQ_ERR_NONFINITE. */
+int uq_moe_ffn(uq_moe_t m, const float* x, const float* router_logits, float* out, int32_t* ids, float* weights);
+/* Device-pointer form on `stream` (NULL: library stream), no synchronization. */
+int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,8 @@ struct Weight {
     int64_t gguf_bytes = 0;        // bytes of the original GGUF tensor
 };
 
+int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank);
+
 // ---- kernel launchers (uq_matvec.hip) ----
 void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s);
 void launch_q8_repack(const uint8_t* gguf, int64_t rows, int64_t nb, int8_t* qs, uint16_t* d, hipStream_t s);

@@ -170,7 +170,9 @@ int Model::build_qkv(int l) {
 template <class T>
 int Model::alloc(T** p, size_t count) {
     UQ_CHECK_HIP(hipMalloc((void**)p, sizeof(T) * (count ? count : 1)));
-    UQ_CHECK_HIP(hipMemset(*p, 0, sizeof(T) * (count ? count : 1)));
+    // zeroed on the library stream: it is non-blocking, so work queued on it is
+    // not ordered after a null-stream memset
+    UQ_CHECK_HIP(hipMemsetAsync(*p, 0, sizeof(T) * (count ? count : 1), stream));
     owned.push_back((void*)*p);
     return OK;
 }
@@ -210,7 +212,8 @@ int Model::build_buffers() {
             t[(size_t)p * c.head_dim + i] = co;
             t[(size_t)p * c.head_dim + half + i] = s;
         }
-    UQ_CHECK_HIP(hipMemcpy(trig, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice));
+    UQ_CHECK_HIP(hipMemcpyAsync(trig, t.data(), sizeof(float) * t.size(), hipMemcpyHostToDevice, stream));
+    UQ_CHECK_HIP(hipStreamSynchronize(stream));
     return OK;
 }
 

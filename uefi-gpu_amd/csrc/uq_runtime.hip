@@ -122,13 +122,18 @@ int uq_sync(void) {
 
 int64_t uq_row_bytes(uint32_t kind, int64_t n) { return uq::row_bytes(kind, n); }
 
-int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, uq_weight_t* out) {
+}  // extern "C"
+
+namespace uq {
+// Uploads, repacks and byte-verifies one GGUF tensor into w. bank = true lifts
+// the per-tensor row limit of llm.rs:248 (expert banks stack many tensors).
+int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank) {
     if (int rc = require_ctx()) return rc;
-    if (!gguf || !out) return set_error(ERR_ARG, "weight_upload: null pointer");
+    if (!gguf) return set_error(ERR_ARG, "weight_upload: null pointer");
     if (kind != KIND_Q8_0 && kind != KIND_Q4_K && kind != KIND_Q3_K)
         return set_error(ERR_QUANT_TYPE, "weight_upload: kind must be Q8_0, Q4_K or Q3_K");
     const int64_t rb = uq::row_bytes(kind, n);
-    if (rb < 0 || m <= 0 || n > MAX_N || m > MAX_M)
+    if (rb < 0 || m <= 0 || n > MAX_N || (!bank && m > MAX_M) || m > (int64_t)1 << 26)
         return set_error(ERR_SHAPE, "weight_upload: bad shape");
     if ((int64_t)bytes != rb * m) return set_error(ERR_SHAPE, "weight_upload: byte count != rows * row_bytes");
     hipStream_t s = g_ctx.stream;
@@ -197,6 +202,17 @@ int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size
         hipFree(w.alloc);
         return rc;
     }
+    out = w;
+    return OK;
+}
+}  // namespace uq
+
+extern "C" {
+
+int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, uq_weight_t* out) {
+    if (!out) return set_error(ERR_ARG, "weight_upload: null pointer");
+    Weight w;
+    if (int rc = upload_weight(kind, n, m, gguf, bytes, w, false)) return rc;
     *out = new uq_weight{w};
     return OK;
 }

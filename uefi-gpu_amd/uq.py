@@ -90,6 +90,13 @@ _SIGS = {
                                           ctypes.POINTER(ctypes.c_double)]),
     "uq_model_kv": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint16),
                                    ctypes.POINTER(ctypes.c_uint16)]),
+    "uq_moe_create": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                                     ctypes.POINTER(_vp)]),
+    "uq_moe_free": (ctypes.c_int, [_vp]),
+    "uq_moe_set_expert": (ctypes.c_int, [_vp, ctypes.c_int32, _vp, _vp, _vp]),
+    "uq_moe_set_shared": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, _vp, _vp, _c_f32p]),
+    "uq_moe_ffn": (ctypes.c_int, [_vp, _c_f32p, _c_f32p, _c_f32p, _c_i32p, _c_f32p]),
+    "uq_moe_ffn_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
     "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
     "uq_synth_tokens": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_uint32, _c_u32p]),
@@ -406,6 +413,65 @@ class Qwen2Model:
     def free(self):
         if getattr(self, "handle", None):
             lib().uq_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- MoE expert FFN
+MOE_CONFIG = dict(dim=2048, ff=768, experts=128, top_k=8, expert_kind=KIND_Q3_K, shared_kind=KIND_Q8_0)
+
+
+def synth_moe(cfg, seed):
+    """Seeded MoE layer: per expert gate/up (ff x dim) and down (dim x ff) in the
+    expert kind; shared expert in the shared kind; shared gate vector 0.05 N(0,1)."""
+    D, F, k, sk = cfg["dim"], cfg["ff"], cfg["expert_kind"], cfg["shared_kind"]
+    ex = []
+    for e in range(cfg["experts"]):
+        ex.append(tuple(synth_quant(k, tensor_seed(seed, "blk.0.ffn_%s_exps.%d" % (p, e)), rows, n)
+                        for p, rows, n in (("gate", F, D), ("up", F, D), ("down", D, F))))
+    shared = tuple(synth_quant(sk, tensor_seed(seed, "blk.0.ffn_%s_shexp" % p), rows, n)
+                   for p, rows, n in (("gate", F, D), ("up", F, D), ("down", D, F)))
+    gate_inp = synth_normal(tensor_seed(seed, "blk.0.ffn_gate_inp_shexp"), D, 0.0, 0.05)
+    return ex, shared, gate_inp
+
+
+class MoeLayer:
+    """Forward::ffn (frontier_forward.rs:164-199) over libuq (uq_moe_*)."""
+
+    def __init__(self, cfg, experts, shared, gate_inp):
+        self.cfg = dict(cfg)
+        h = _vp()
+        _check(lib().uq_moe_create(cfg["dim"], cfg["ff"], cfg["experts"], cfg["top_k"], cfg["expert_kind"],
+                                   ctypes.byref(h)))
+        self.handle = h
+        for e, (g, u, d) in enumerate(experts):
+            _check(lib().uq_moe_set_expert(h, e, g.ctypes.data, u.ctypes.data, d.ctypes.data))
+        g, u, d = shared
+        gi = None if gate_inp is None else np.ascontiguousarray(gate_inp, np.float32)
+        _check(lib().uq_moe_set_shared(h, cfg["shared_kind"], g.ctypes.data, u.ctypes.data, d.ctypes.data,
+                                       None if gi is None else _p(gi, _c_f32p)))
+
+    def ffn(self, x, logits):
+        x = np.ascontiguousarray(x, np.float32)
+        lg = np.ascontiguousarray(logits, np.float32)
+        out = np.empty(self.cfg["dim"], np.float32)
+        ids = np.empty(self.cfg["top_k"], np.int32)
+        w = np.empty(self.cfg["top_k"], np.float32)
+        _check(lib().uq_moe_ffn(self.handle, _p(x, _c_f32p), _p(lg, _c_f32p), _p(out, _c_f32p), _p(ids, _c_i32p),
+                                _p(w, _c_f32p)))
+        return out, ids, w
+
+    def ffn_dev(self, x_dev, logits_dev, out_dev, stream=None):
+        _check(lib().uq_moe_ffn_dev(self.handle, x_dev, logits_dev, out_dev, stream))
+
+    def free(self):
+        if getattr(self, "handle", None):
+            lib().uq_moe_free(self.handle)
             self.handle = None
 
     def __del__(self):

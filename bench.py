@@ -26,6 +26,11 @@ import uq  # noqa: E402
 
 METRIC = "Q8_0 matvec HBM GB/s (% peak); bs=1 decode tok/s, Qwen2.5-1.5B shape"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per lm_head launch (151936x1536 Q8_0), from rocprofv3 PMC passes
+# over this script: FETCH_SIZE 121,102.1 KiB x 2.0 + WRITE_SIZE 594.1 KiB x 1.0,
+# factors from 1 GiB read/copy probe kernels in the same runs
+# (profiles/q8_matvec_lm_head_pmc.md).
+LM_HEAD_TRAFFIC_BYTES = 248_625_459
 
 # (name, N rows, K, fused pair)
 SHAPES = [("attn_q/o", 1536, 1536, False), ("attn_k/v", 256, 1536, False),
@@ -131,6 +136,44 @@ def prefill_gemm_bench(tokens=512, reps=20):
     return out
 
 
+def q4k_sweep(copies=3, reps=30):
+    """The same bs=1 sweep with Q4_K weights (144 B per 256 values)."""
+    weights, pairs, names = [], [], []
+    for c in range(copies):
+        for name, N, K, pair in SHAPES:
+            for i in range(2 if pair else 1):
+                raw = uq.synth_quant(uq.KIND_Q4_K, 0x5EED0011 + c * 16 + i * 4 + N, N, K)
+                weights.append(uq.Weight(uq.KIND_Q4_K, K, N, raw))
+                pairs.append(1 if (pair and i == 0) else 0)
+                names.append(name)
+    q4 = lambda N, K: N * (K // 256) * 144 + K + (K // 32) * 4 + 4 * N
+    step_bytes = sum(q4(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else q4(N, K) for _, N, K, pair in SHAPES)
+    lm = names.index("lm_head")
+    total_ms, lm_ms = uq.time_matvecs(weights, pairs, 8960, reps, 3, lm)
+    for w in weights:
+        w.free()
+    return {"GBs": round(step_bytes * reps * copies / (total_ms / 1e3) / 1e9, 1), "bytes_per_step": step_bytes,
+            "lm_head_GBs": round(q4(151936, 1536) / (lm_ms / 1e3) / 1e9, 1),
+            "lm_head_frac": round(q4(151936, 1536) / (lm_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def moe_bench(steps=64):
+    """MoE decode layer: 128 Q3_K experts (dim 2048, ff 768), top-8 softmax
+    routing from N(0,1) logits, one shared Q8_0 expert; 64 seeded steps back to
+    back. Bytes per step: 8 x 3 Q3_K expert matrices + 3 shared Q8_0 matrices."""
+    cfg = uq.MOE_CONFIG
+    ex, sh, gi = uq.synth_moe(cfg, 0x5EED0004)
+    layer = uq.MoeLayer(cfg, ex, sh, gi)
+    xs = np.stack([uq.synth_normal(0x5EED0004 + 1000 * s, cfg["dim"]) for s in range(steps)])
+    lg = np.stack([uq.synth_normal(0x5EED0004 + 1000 * s + 1, cfg["experts"]) for s in range(steps)])
+    layer.run(xs[:4], lg[:4])
+    _, ms = layer.run(xs, lg)
+    layer.free()
+    step_bytes = 8 * 2027520 + 5013504
+    return {"GBs": round(step_bytes * steps / (ms / 1e3) / 1e9, 1), "us_per_step": round(ms * 1e3 / steps, 2),
+            "steps": steps, "bytes_per_step": step_bytes}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,7 +222,7 @@ def main():
                    "bytes_per_step": step_bytes, "seed": 0x5EED0001, "fraction_of_hbm_peak":
                        round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES,
                      "kernel": "Q8_0 matvec, lm_head 151936x1536 (%d B per launch), mean of %d launches %.4f ms"
                                % (lm_bytes, rounds, lm_ms)},
     }
@@ -191,6 +234,8 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_bench()
         result["prefill_gemm"] = prefill_gemm_bench()
+        result["q4k_sweep"] = q4k_sweep()
+        result["moe"] = moe_bench()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -185,6 +185,9 @@ int uq_moe_set_shared(uq_moe_t m, uint32_t kind, const void* gate, const void* u
 int uq_moe_ffn(uq_moe_t m, const float* x, const float* router_logits, float* out, int32_t* ids, float* weights);
 /* Device-pointer form on `stream` (NULL: library stream), no synchronization. */
 int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float* out, void* stream);
+/* `steps` tokens back to back on the library stream, device arrays x[steps][dim],
+ * logits[steps][experts], out[steps][dim]; ms = HIP-event time of the launches. */
+int uq_moe_run(uq_moe_t m, const float* xs, const float* logits, float* outs, int steps, double* ms);
 
 #ifdef __cplusplus
 }

@@ -108,3 +108,55 @@ def test_oracle_prefill_matches_decode_chain():
     # a second prefill over the same prompt is deterministic
     c = O.Model(TINY, arrays)
     assert c.prefill(toks, want_logits=True)[1] == nxt_p
+
+
+def test_oracle_moe_matches_numpy_restatement():
+    """frontier_forward.rs:164-199 restated in numpy float64 around the shared
+    int8 activation rule: softmax, stable top-k, p/sum weights, SwiGLU experts,
+    rank-ordered combine, sigmoid-gated shared expert."""
+    cfg = dict(dim=256, ff=256, experts=8, top_k=2, expert_kind=uq.KIND_Q8_0, shared_kind=uq.KIND_Q8_0)
+    ex, sh, gi = uq.synth_moe(cfg, 3)
+    om = O.MoeLayer(cfg["dim"], cfg["ff"], cfg["experts"], cfg["top_k"], cfg["expert_kind"],
+                    [e[0] for e in ex], [e[1] for e in ex], [e[2] for e in ex], cfg["shared_kind"],
+                    sh[0], sh[1], sh[2], gi)
+    D, F = cfg["dim"], cfg["ff"]
+    deq = lambda raw, rows, n: G.q8_0_dequant(raw, rows, n).astype(np.float64)
+    for step in range(4):
+        x = uq.synth_normal(50 + step, D)
+        lg = uq.synth_normal(60 + step, cfg["experts"])
+        rc, out, ids, w = om.ffn(x, lg)
+        assert rc == 0
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        order = sorted(range(cfg["experts"]), key=lambda e: (-np.float32(p[e]), e))[:cfg["top_k"]]
+        assert list(ids) == order
+        wts = p[order] / p[order].sum()
+        xq = np_quant(x)
+        ref = np.zeros(D)
+
+        def expert(g, u, d):
+            gv, uv = deq(g, F, D) @ xq, deq(u, F, D) @ xq
+            mid = gv / (1 + np.exp(-gv)) * uv
+            return deq(d, D, F) @ np_quant(mid)
+        for r, e in enumerate(order):
+            ref += wts[r] * expert(*ex[e])
+        ref += 1 / (1 + np.exp(-(gi.astype(np.float64) @ x.astype(np.float64)))) * expert(*sh)
+        assert np.abs(out - ref).max() < 2e-3 * np.abs(ref).max()
+
+
+def test_oracle_reproduces_committed_fixtures():
+    """tests/golden/small.npz was written by tests/golden/make_golden.py; the
+    oracle must reproduce every output bit for bit."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "small.npz"))
+    q, s = O.quant_act(f["quant_x"])
+    assert np.array_equal(q, f["quant_q"]) and np.array_equal(s, f["quant_s"])
+    for kind, name, n, m in ((O.Q8_0, "q8", 256, 64), (O.Q4_K, "q4k", 512, 48), (O.Q3_K, "q3k", 512, 40)):
+        y = O.matvec(kind, f[name + "_w"], n, m, f[name + "_x"])
+        assert np.array_equal(y, f[name + "_y"])
+        qx, _ = O.quant_act(f[name + "_x"])
+        assert np.array_equal(O.block_dots(kind, f[name + "_w"], n, m, qx), f[name + "_dots"])
+    y = O.prefill_gemm(f["q8_w"], 256, 64, f["gemm_xs"], f["gemm_qx"], 70)
+    assert np.array_equal(y, f["gemm_y"])
+    out = O.attention(f["attn_q"], f["attn_k"], f["attn_v"], 39, 12, 2, 128)
+    assert np.array_equal(out, f["attn_out"])

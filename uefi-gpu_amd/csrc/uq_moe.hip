@@ -394,6 +394,30 @@ int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float
     return OK;
 }
 
+int uq_moe_run(uq_moe_t m, const float* xs, const float* logits, float* outs, int steps, double* ms) {
+    if (!m || !xs || !logits || !outs || steps <= 0) return set_error(ERR_ARG, "moe_run: bad args");
+    if (int rc = moe_finalize(m)) return rc;
+    hipStream_t s = (hipStream_t)uq_stream();
+    hipEvent_t e0, e1;
+    UQ_CHECK_HIP(hipEventCreate(&e0));
+    UQ_CHECK_HIP(hipEventCreate(&e1));
+    UQ_CHECK_HIP(hipEventRecord(e0, s));
+    for (int i = 0; i < steps; i++)
+        if (int rc = uq_moe_ffn_dev(m, xs + (size_t)i * m->D, logits + (size_t)i * m->E, outs + (size_t)i * m->D, s))
+            return rc;
+    UQ_CHECK_HIP(hipEventRecord(e1, s));
+    UQ_CHECK_HIP(hipEventSynchronize(e1));
+    float t = 0;
+    UQ_CHECK_HIP(hipEventElapsedTime(&t, e0, e1));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (ms) *ms = t;
+    unsigned status = 0;
+    UQ_CHECK_HIP(hipMemcpy(&status, m->status, 4, hipMemcpyDeviceToHost));
+    if (status) return set_error(ERR_NONFINITE, "moe_run: non-finite input in the last step");
+    return OK;
+}
+
 int uq_moe_ffn(uq_moe_t m, const float* x, const float* router_logits, float* out, int32_t* ids, float* weights) {
     if (!m || !x || !router_logits || !out) return set_error(ERR_ARG, "moe_ffn: null pointer");
     if (int rc = moe_finalize(m)) return rc;

@@ -97,6 +97,7 @@ _SIGS = {
     "uq_moe_set_shared": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, _vp, _vp, _c_f32p]),
     "uq_moe_ffn": (ctypes.c_int, [_vp, _c_f32p, _c_f32p, _c_f32p, _c_i32p, _c_f32p]),
     "uq_moe_ffn_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "uq_moe_run": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
     "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
     "uq_synth_tokens": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_uint32, _c_u32p]),
@@ -468,6 +469,29 @@ class MoeLayer:
 
     def ffn_dev(self, x_dev, logits_dev, out_dev, stream=None):
         _check(lib().uq_moe_ffn_dev(self.handle, x_dev, logits_dev, out_dev, stream))
+
+    def run(self, xs, logits):
+        """Timed back-to-back steps over host arrays xs [steps][dim], logits [steps][experts]."""
+        xs = np.ascontiguousarray(xs, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        steps = xs.shape[0]
+        L = lib()
+        bufs = []
+        for a in (xs, logits, np.empty_like(xs)):
+            p = _vp()
+            _check(L.uq_dev_alloc(a.nbytes, ctypes.byref(p)))
+            bufs.append(p)
+        try:
+            _check(L.uq_memcpy_h2d(bufs[0], xs.ctypes.data, xs.nbytes))
+            _check(L.uq_memcpy_h2d(bufs[1], logits.ctypes.data, logits.nbytes))
+            ms = ctypes.c_double()
+            _check(L.uq_moe_run(self.handle, bufs[0], bufs[1], bufs[2], steps, ctypes.byref(ms)))
+            out = np.empty_like(xs)
+            _check(L.uq_memcpy_d2h(out.ctypes.data, bufs[2], out.nbytes))
+        finally:
+            for p in bufs:
+                L.uq_dev_free(p)
+        return out, ms.value
 
     def free(self):
         if getattr(self, "handle", None):

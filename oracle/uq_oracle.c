@@ -10,7 +10,10 @@
  * Parity pins (tests/test_oracle_*.py):
  *   uqo_half            exhaustive 65536 patterns vs numpy float16 (IEEE)
  *   uqo_f16_rne         vs numpy float32->float16 on specials + 4M samples
- *   uqo_expf            vs glibc/numpy expf: <=1 ulp everywhere sampled
+ *   uqo_expf            libm 0.2.16 expf algorithm (frontier_cpu_expf.rs:80-170):
+ *                       polynomial bits of :182-183, every reduction boundary
+ *                       of :189-199 against float64 exp, <1 ulp vs float64
+ *                       exp on dense and bit-pattern samples
  *   uqo_quant_act       closed form: zero block, ties-to-even, amax -> +-127,
  *                       |q*scale - x| <= scale/2, vs integer brute force
  *   block dots (Q8_0)   int64 numpy brute force
@@ -87,33 +90,55 @@ uint16_t uqo_f16_rne(float f) {
     return (uint16_t)(sign | h);
 }
 
-/* exp for softmax / SiLU / sigmoid. Replaces libm expf (frontier_cpu_expf.rs)
- * and CUDA expf (gpu_dp4a.cu:63, gpu_attention.cu:218) with one published
- * method evaluated identically on CPU and GPU: Cody-Waite reduction by ln2 in
- * double, degree-12 Taylor polynomial (Horner, fused multiply-add), scaling by
- * 2^k, one rounding to f32. */
+/* exp for softmax / SiLU / sigmoid: the expf of the reference's Rust path
+ * (libm 0.2.16, derived from FreeBSD e_expf.c), called at llm.rs:365,374 and
+ * restated instruction by instruction at frontier_cpu_expf.rs:80-170 (whose
+ * tests pin the polynomial bits at :182-183). f32 arithmetic throughout:
+ *   k = nearest integer to x/ln2 (|x| > 0.5 ln2; +-1 below 1.5 ln2),
+ *   hi = x - k*ln2_hi (exact), lo = k*ln2_lo, r = hi - lo,
+ *   c = r - r^2 (P1 + r^2 P2),  y = 1 + (r c / (2 - c) - lo + hi),
+ *   result = y * 2^k (scalbnf steps for k outside the normal exponent range).
+ * The kernels evaluate the same f32 operations (uq_device.h). */
+static float scalbnf_steps(float y, int k) {
+    if (k > 127) {
+        y = y * 0x1p127f; k -= 127;
+        if (k > 127) { y = y * 0x1p127f; k -= 127; if (k > 127) k = 127; }
+    } else if (k < -126) {
+        y = y * 0x1p-102f; k += 102;
+        if (k < -126) { y = y * 0x1p-102f; k += 102; if (k < -126) k = -126; }
+    }
+    return y * f_from_bits((uint32_t)(127 + k) << 23);
+}
+
 float uqo_expf(float x) {
-    if (x != x) return x;
-    if (x > 100.0f) return INFINITY;
-    if (x < -110.0f) return 0.0f;
-    const double xd = (double)x;
-    const double kd = rint(xd * 0x1.71547652b82fep+0);
-    double r = fma(-kd, 0x1.62e42fefa39efp-1, xd);
-    r = fma(-kd, 0x1.abc9e3b39803fp-56, r);
-    double p = 0x1.1eed8eff8d898p-29;
-    p = fma(p, r, 0x1.ae64567f544e4p-26);
-    p = fma(p, r, 0x1.27e4fb7789f5cp-22);
-    p = fma(p, r, 0x1.71de3a556c734p-19);
-    p = fma(p, r, 0x1.a01a01a01a01ap-16);
-    p = fma(p, r, 0x1.a01a01a01a01ap-13);
-    p = fma(p, r, 0x1.6c16c16c16c17p-10);
-    p = fma(p, r, 0x1.1111111111111p-7);
-    p = fma(p, r, 0x1.5555555555555p-5);
-    p = fma(p, r, 0x1.5555555555555p-3);
-    p = fma(p, r, 0x1.0000000000000p-1);
-    p = fma(p, r, 1.0);
-    p = fma(p, r, 1.0);
-    return (float)ldexp(p, (int)kd);
+    const uint32_t ax = bits_from_f(x) & 0x7fffffffu;
+    const int neg = (int)(bits_from_f(x) >> 31);
+    if (ax >= 0x42aeac50u) {                       /* |x| >= 87.3365 or NaN */
+        if (ax > 0x7f800000u) return x;            /* NaN */
+        if (!neg && ax >= 0x42b17218u) return x * 0x1p127f;  /* overflow */
+        if (neg && ax >= 0x42cff1b5u) return 0.0f; /* x <= -103.972 */
+    }
+    if (ax <= 0x39000000u) return 1.0f + x;        /* |x| <= 2^-14 */
+    float hi = x, lo = 0.0f;
+    int k = 0;
+    if (ax > 0x3eb17218u) {                        /* |x| > 0.5 ln2 */
+        if (ax > 0x3f851592u) {                    /* |x| > 1.5 ln2 */
+            const float t = x * f_from_bits(0x3fb8aa3bu);
+            k = (int)(t + (neg ? -0.5f : 0.5f));   /* truncation */
+        } else {
+            k = neg ? -1 : 1;
+        }
+        const float kf = (float)k;
+        hi = x - kf * f_from_bits(0x3f317200u);
+        lo = kf * f_from_bits(0x35bfbe8eu);
+        x = hi - lo;
+    }
+    const float r2 = x * x;
+    const float poly = r2 * (f_from_bits(0x3e2aaa8fu) + r2 * f_from_bits(0xbb355215u));
+    const float c = x - poly;
+    const float q = (x * c) / (2.0f - c);
+    const float y = 1.0f + ((q - lo) + hi);
+    return k == 0 ? y : scalbnf_steps(y, k);
 }
 
 /* driver/src/frontier_core.rs:53-58 row sizes, extended with the two K-quant

@@ -17,8 +17,8 @@
  *     in any order and still agree bit for bit (see uqo_* docstrings);
  *   - the Q8_0 prefill GEMM keeps the reference's sequential per-32-block f32
  *     fmaf update (driver/kernels/gpu_prefill.cu:93-94), mirrored exactly;
- *   - exp is uqo_expf: Cody-Waite reduction + degree-12 Taylor in double,
- *     rounded once (replaces libm/CUDA expf; within 1 ulp of glibc expf).
+ *   - exp is uqo_expf, the libm 0.2.16 expf of the reference's Rust path
+ *     (FreeBSD e_expf.c; driver/src/frontier_cpu_expf.rs:80-170), in f32.
  *
  * Parity status per function is listed in the header of uq_oracle.c.
  */

@@ -55,18 +55,59 @@ def test_f16_rne_matches_numpy():
 
 
 # ---------------------------------------------------------------- exp
-def test_expf_within_one_ulp_of_correctly_rounded():
-    xs = np.concatenate([np.linspace(-104, 88.7, 200001, dtype=np.float32),
-                         RNG.uniform(-20, 20, 100000).astype(np.float32),
-                         np.array([0.0, -0.0, 1.0, -1.0, 1e-8, -1e-8], np.float32)])
+def lcg_samples(count):
+    """The input stream of frontier_cpu_expf.rs:185-189: alternating dense
+    decimal points in [-80, 80) and raw bit patterns with exponents < 133."""
+    r, out = 17, []
+    for i in range(count):
+        r = (r * 1664525 + 1013904223) & 0xFFFFFFFF
+        if i % 2 == 0:
+            out.append(np.float32(((r % 160000) - 80000) / 1000.0))
+        else:
+            out.append(np.uint32((r & 0x807FFFFF) | (((r >> 24) % 133) << 23)).view(np.float32))
+    return np.array(out, np.float32)
+
+
+def test_expf_libm_algorithm_within_one_ulp():
+    """uqo_expf restates libm 0.2.16 expf (frontier_cpu_expf.rs:80-170). It is
+    not correctly rounded, so the check against float64 exp is <= 1 ulp; a
+    dropped low-order reduction term or a wrong polynomial constant exceeds it
+    (the lo term alone is k * 1.43e-6 relative, many ulps for k >= 1)."""
+    xs = np.concatenate([np.linspace(-103.9, 88.7, 200001, dtype=np.float32),
+                         RNG.uniform(-20, 20, 100000).astype(np.float32), lcg_samples(100000)])
     got = np.array([O.expf(float(x)) for x in xs], np.float32)
     ref = np.exp(xs.astype(np.float64)).astype(np.float32)
     d = ulp_diff(got, ref)
     assert d.max() <= 1
-    assert (d == 0).mean() > 0.9999
-    assert O.expf(0.0) == 1.0
+    assert (d == 0).mean() > 0.85
+
+
+def test_expf_reduction_boundaries_and_specials():
+    """Every branch boundary of the reduction (frontier_cpu_expf.rs:191-199):
+    tiny |x| <= 2^-14 returns 1 + x, the +-1 reduction below 1.5 ln2, the
+    multiple reduction, subnormal results below -87.34, zero from -103.97,
+    overflow from 88.72."""
+    for base in (0, 0x39000000, 0x3EB17218, 0x3F851592, 0x42A00000, 0x42AEAC50, 0x42B17218, 0x42CFF1B5):
+        for dlt in range(-2, 3):
+            for sign in (0, 0x80000000):
+                bits = max(0, base + dlt) | sign
+                x = np.uint32(bits).view(np.float32)
+                got = np.float32(O.expf(float(x)))
+                ref = np.float32(np.exp(np.float64(x)))
+                if np.isinf(ref):
+                    assert np.isinf(got) and got > 0, hex(bits)
+                else:
+                    assert ulp_diff(got, ref) <= 1, (hex(bits), got, ref)
+    tiny = np.float32(2.0 ** -15)
+    assert O.expf(float(tiny)) == np.float32(1) + tiny
+    assert O.expf(0.0) == 1.0 and O.expf(-0.0) == 1.0
+    assert O.expf(float(np.uint32(0x42CFF1B5 | 0x80000000).view(np.float32))) == 0.0
     assert O.expf(-200.0) == 0.0 and O.expf(200.0) == np.inf
+    assert O.expf(float("inf")) == np.inf and O.expf(float("-inf")) == 0.0
     assert np.isnan(O.expf(float("nan")))
+    sub = np.float32(O.expf(-95.0))                  # subnormal result
+    assert 0 < sub < np.finfo(np.float32).tiny
+    assert ulp_diff(sub, np.float32(np.exp(-95.0))) <= 1
 
 
 # ---------------------------------------------------------------- activation quant

@@ -5,7 +5,7 @@
 //    written op by op in the reference's order;
 //  * reductions accumulate exactly formed double terms and round to f32 once,
 //    so the result does not depend on the lane/wave summation order;
-//  * exp is uq_expf below (double Cody-Waite + degree-12 Taylor, one rounding),
+//  * exp is uq_expf below, the reference Rust path's libm expf in f32,
 //    bit-identical to the oracle's restatement.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -16,28 +16,54 @@
 UQ_DEV float uq_half(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 UQ_DEV uint16_t uq_f16_rne(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+UQ_DEV float uq_bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// y * 2^k with the pre-scaling steps of scalbnf for k outside [-126, 127]
+// (only the final multiply can round, into the subnormal range).
+UQ_DEV float uq_scalbnf_steps(float y, int k) {
+    if (k > 127) {
+        y = y * 0x1p127f; k -= 127;
+        if (k > 127) { y = y * 0x1p127f; k -= 127; if (k > 127) k = 127; }
+    } else if (k < -126) {
+        y = y * 0x1p-102f; k += 102;
+        if (k < -126) { y = y * 0x1p-102f; k += 102; if (k < -126) k = -126; }
+    }
+    return y * uq_bits_f((uint32_t)(127 + k) << 23);
+}
+
+// expf of the reference's Rust path: libm 0.2.16 (FreeBSD e_expf.c), as
+// restated at driver/src/frontier_cpu_expf.rs:80-170. Same f32 operations as
+// the oracle's uqo_expf; division is IEEE (HIP's correctly rounded f32 '/').
 UQ_DEV float uq_expf(float x) {
-    if (x != x) return x;
-    if (x > 100.0f) return __builtin_inff();
-    if (x < -110.0f) return 0.0f;
-    const double xd = (double)x;
-    const double kd = __builtin_rint(xd * 0x1.71547652b82fep+0);
-    double r = __builtin_fma(-kd, 0x1.62e42fefa39efp-1, xd);
-    r = __builtin_fma(-kd, 0x1.abc9e3b39803fp-56, r);
-    double p = 0x1.1eed8eff8d898p-29;
-    p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
-    p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
-    p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
-    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
-    p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
-    p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
-    p = __builtin_fma(p, r, 0x1.1111111111111p-7);
-    p = __builtin_fma(p, r, 0x1.5555555555555p-5);
-    p = __builtin_fma(p, r, 0x1.5555555555555p-3);
-    p = __builtin_fma(p, r, 0x1.0000000000000p-1);
-    p = __builtin_fma(p, r, 1.0);
-    p = __builtin_fma(p, r, 1.0);
-    return (float)__builtin_ldexp(p, (int)kd);
+    const uint32_t bx = __builtin_bit_cast(uint32_t, x);
+    const uint32_t ax = bx & 0x7fffffffu;
+    const bool neg = (bx >> 31) != 0;
+    if (ax >= 0x42aeac50u) {
+        if (ax > 0x7f800000u) return x;
+        if (!neg && ax >= 0x42b17218u) return x * 0x1p127f;
+        if (neg && ax >= 0x42cff1b5u) return 0.0f;
+    }
+    if (ax <= 0x39000000u) return 1.0f + x;
+    float hi = x, lo = 0.0f;
+    int k = 0;
+    if (ax > 0x3eb17218u) {
+        if (ax > 0x3f851592u) {
+            const float t = x * uq_bits_f(0x3fb8aa3bu);
+            k = (int)(t + (neg ? -0.5f : 0.5f));
+        } else {
+            k = neg ? -1 : 1;
+        }
+        const float kf = (float)k;
+        hi = x - kf * uq_bits_f(0x3f317200u);
+        lo = kf * uq_bits_f(0x35bfbe8eu);
+        x = hi - lo;
+    }
+    const float r2 = x * x;
+    const float poly = r2 * (uq_bits_f(0x3e2aaa8fu) + r2 * uq_bits_f(0xbb355215u));
+    const float c = x - poly;
+    const float q = (x * c) / (2.0f - c);
+    const float y = 1.0f + ((q - lo) + hi);
+    return k == 0 ? y : uq_scalbnf_steps(y, k);
 }
 
 // (g / (1 + exp(-g))) * u  -- gateup_dp4a / silu_mul form

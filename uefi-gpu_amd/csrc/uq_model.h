@@ -12,7 +12,7 @@ namespace uq {
 struct LayerDev {
     Weight qkv;  // q|k|v rows of one layer in one Q8_0 weight
     // fp16 weight scales transposed to [k/32][rows] for the prefill GEMM
-    uint16_t *qkv_dt = nullptr, *o_dt = nullptr, *g_dt = nullptr, *u_dt = nullptr, *d_dt = nullptr;
+    float *qkv_dt = nullptr, *o_dt = nullptr, *g_dt = nullptr, *u_dt = nullptr, *d_dt = nullptr;
 };
 
 struct Model {

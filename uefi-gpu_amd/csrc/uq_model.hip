@@ -321,7 +321,7 @@ int Model::build_prefill() {
     if (int rc = alloc(&PXQ, (size_t)pcap * big)) return rc;
     if (int rc = alloc(&PXST, (size_t)pcap * big / 32)) return rc;
     if (int rc = alloc(&PTOK, (size_t)pcap)) return rc;
-    auto tr = [&](const Weight& w, uint16_t** dt) -> int {
+    auto tr = [&](const Weight& w, float** dt) -> int {
         if (int rc = alloc(dt, (size_t)w.m * (w.n / 32))) return rc;
         launch_transpose_scales(w.d, w.m, w.n / 32, *dt, stream);
         return OK;
@@ -372,7 +372,7 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
         na.mp = mp;
         launch_pf_norm(na, n, s);
     };
-    auto gemm = [&](const Weight& w, const uint16_t* dt, const Weight* w2, const uint16_t* dt2, float* y) {
+    auto gemm = [&](const Weight& w, const float* dt, const Weight* w2, const float* dt2, float* y) {
         PfGemmArgs ga{w.qs, dt, w2 ? w2->qs : nullptr, dt2, PXQ, PXST, y, w.m, w.n, mp};
         return launch_pf_gemm(ga, s);
     };
@@ -532,10 +532,10 @@ int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t to
     std::vector<float> xst((size_t)(nb * mp), 0.0f);
     for (int64_t t = 0; t < tokens; t++)
         for (int64_t b = 0; b < nb; b++) xst[b * mp + t] = xs[t * nb + b];
-    uint16_t* dt = nullptr;
+    float* dt = nullptr;
     int8_t* dq = nullptr;
     float *ds = nullptr, *dy = nullptr;
-    UQ_CHECK_HIP(hipMalloc(&dt, 2 * (size_t)(nb * W.m)));
+    UQ_CHECK_HIP(hipMalloc(&dt, 4 * (size_t)(nb * W.m)));
     UQ_CHECK_HIP(hipMalloc(&dq, (size_t)(mp * k)));
     UQ_CHECK_HIP(hipMalloc(&ds, 4 * xst.size()));
     UQ_CHECK_HIP(hipMalloc(&dy, 4 * (size_t)(mp * W.m)));
@@ -568,11 +568,11 @@ int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps
     std::vector<float> hs((size_t)(nb * mp));
     for (size_t i = 0; i < hq.size(); i++) hq[i] = (int8_t)((int)((i * 2654435761u) >> 24) % 255 - 127);
     for (size_t i = 0; i < hs.size(); i++) hs[i] = 0.01f + 0.001f * (float)(i % 7);
-    uint16_t *dt = nullptr, *dt2 = nullptr;
+    float *dt = nullptr, *dt2 = nullptr;
     int8_t* dq = nullptr;
     float *ds = nullptr, *dy = nullptr;
-    UQ_CHECK_HIP(hipMalloc(&dt, 2 * (size_t)(nb * W.m)));
-    if (w2) UQ_CHECK_HIP(hipMalloc(&dt2, 2 * (size_t)(nb * W.m)));
+    UQ_CHECK_HIP(hipMalloc(&dt, 4 * (size_t)(nb * W.m)));
+    if (w2) UQ_CHECK_HIP(hipMalloc(&dt2, 4 * (size_t)(nb * W.m)));
     UQ_CHECK_HIP(hipMalloc(&dq, hq.size()));
     UQ_CHECK_HIP(hipMalloc(&ds, 4 * hs.size()));
     UQ_CHECK_HIP(hipMalloc(&dy, 4 * (size_t)(mp * W.m)));

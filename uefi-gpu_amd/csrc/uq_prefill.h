@@ -21,9 +21,9 @@ struct PfNormArgs {
 
 struct PfGemmArgs {
     const int8_t* w_qs;      // [n][k]
-    const uint16_t* w_dt;    // fp16 scales transposed [k/32][n]
+    const float* w_ds;       // weight scales widened to f32, transposed [k/32][n]
     const int8_t* w2_qs;     // second matrix (up) for the gate/up SiLU epilogue, or null
-    const uint16_t* w2_dt;
+    const float* w2_ds;
     const int8_t* xq;        // [mp][k]
     const float* xst;        // [k/32][mp]
     float* y;                // [mp][n]
@@ -52,7 +52,7 @@ struct PfAttnArgs {
     float qscale;
 };
 
-void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, uint16_t* dt, hipStream_t s);
+void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float* dt, hipStream_t s);
 void launch_pf_norm(const PfNormArgs& a, int tokens, hipStream_t s);
 void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, float* xst, hipStream_t s);
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s);

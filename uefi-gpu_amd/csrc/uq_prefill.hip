@@ -11,9 +11,9 @@
 // (gpu_prefill.cu:93-94). c_b is one v_mfma_i32_16x16x32_i8 per block with a
 // zero accumulator; the f32 rescale runs on the VALU in the same order as the
 // reference, so results match the oracle bit for bit.
-// Operands come straight from the row-major planes used by decode (no second
-// weight copy); only the fp16 weight scales get a [block][row] transpose so a
-// lane reads its four rows' scales with one 8-byte load.
+// Operands come from the row-major planes used by decode (no second weight
+// copy), staged through LDS; the fp16 weight scales get a [block][row]
+// transpose widened to f32, so a stage's scales are contiguous float4 loads.
 #include "uq_device.h"
 #include "uq_blockops.h"
 #include "uq_prefill.h"
@@ -24,12 +24,13 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ scale transpose
+// fp16 d[row][block] -> f32 dt[block][row] (exact widening).
 __global__ __launch_bounds__(256) void k_transpose_scales(const uint16_t* __restrict__ d, int64_t rows, int64_t nb,
-                                                          uint16_t* __restrict__ dt) {
+                                                          float* __restrict__ dt) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= rows * nb) return;
     const int64_t r = i / nb, b = i % nb;
-    dt[b * rows + r] = d[i];
+    dt[b * rows + r] = uq_half(d[i]);
 }
 
 // ------------------------------------------------------------------ per-token norm + quant
@@ -61,86 +62,214 @@ __global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, i
 }
 
 // ------------------------------------------------------------------ GEMM
-// Workgroup tile 64 rows x 64 tokens, four waves of 32 x 32 (2 x 2 MFMA tiles).
+// Workgroup tile 32 rows x 64 tokens, 4 waves of 32 rows x 16 tokens (2 MFMA
+// tiles, 4 with the gate/up pair). K runs in stages of four 32-blocks (128
+// values) through a ring of GR stages in LDS, filled by direct global->LDS
+// loads (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), so
+// GR-1 stages are in flight while one is computed, with no register staging.
+// LDS rows are 128 bytes; 16-byte chunk c of row r sits in slot c ^ swz(r),
+// which makes the 16 lanes of an MFMA fragment read hit 16 distinct bank pairs.
 // MFMA 16x16x32 i8 lane layout: A lane l = row l%16, k (l/16)*8..+7; B lane l =
 // token l%16, same k; D lane l = rows (l/16)*4..+3, token l%16.
+// Per output and block the VALU does (float)c, dw*dx and the fmaf in the
+// reference's order; that work, not the MFMA, bounds this kernel.
+constexpr int GK_BLK = 4;                  // 32-blocks per stage
+constexpr int GBM = 32, GBN = 64;          // rows, tokens per workgroup tile
+constexpr int GR = 4;                      // ring depth (stages)
+
 template <bool GU>
-__global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * 64 + (wave >> 1) * 32;
-    const int64_t t0 = (int64_t)blockIdx.y * 64 + (wave & 1) * 32;
-    const int li = lane & 15, lk = (lane >> 4) * 8, lm = (lane >> 4) * 4;
-    const int64_t K = a.k, N = a.n, nb = K / 32;
-    const int8_t* A0 = a.w_qs + (r0 + li) * K + lk;
-    const int8_t* A1 = A0 + 16 * K;
-    const int8_t* G0 = GU ? a.w2_qs + (r0 + li) * K + lk : nullptr;
-    const int8_t* G1 = GU ? G0 + 16 * K : nullptr;
-    const int8_t* B0 = a.xq + (t0 + li) * K + lk;
-    const int8_t* B1 = B0 + 16 * K;
-    float f[2][2][4], g[2][2][4];
-#pragma unroll
-    for (int x = 0; x < 2; x++)
-#pragma unroll
-        for (int y = 0; y < 2; y++)
-#pragma unroll
-            for (int m = 0; m < 4; m++) f[x][y][m] = g[x][y][m] = 0.0f;
+struct GemmStageLds {
+    int8_t a[GBM * 128];
+    int8_t a2[GU ? GBM * 128 : 16];
+    int8_t b[GBN * 128];
+    float sw[GK_BLK * GBM];
+    float sw2[GU ? GK_BLK * GBM : 4];
+    float sx[GK_BLK * GBN];
+};
+// loads per wave per stage: A (1), A2 (1), B (2), scales sw, sw2, sx
+template <bool GU>
+constexpr int gemm_lps() { return GU ? 7 : 5; }
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 16, 0, 0);
+}
+// rows r and r+16 (read by one ds_read2 of the two MFMA row tiles) get different slots
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
+
+// Per-lane source pointers of the stage loads at k = 0 (a full stage adds
+// kb * 32 bytes to the quantized planes and kb block rows to the scale planes).
+struct GemmSrc {
+    const int8_t *a, *a2, *b0, *b1;
+    const float *sw, *sw2, *sx;
+};
+template <bool GU>
+__device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int64_t r0, int64_t t0, int wave, int lane) {
+    const int64_t K = p.k, N = p.n;
+    const int slot = lane & 7, row = 8 * wave + (lane >> 3);
+    const int tk0 = 16 * wave + (lane >> 3), tk1 = tk0 + 8;
+    GemmSrc g;
+    g.a = p.w_qs + (r0 + row) * K + 16 * (slot ^ swz(row));
+    g.a2 = GU ? p.w2_qs + (r0 + row) * K + 16 * (slot ^ swz(row)) : nullptr;
+    g.b0 = p.xq + (t0 + tk0) * K + 16 * (slot ^ swz(tk0));
+    g.b1 = p.xq + (t0 + tk1) * K + 16 * (slot ^ swz(tk1));
+    g.sw = p.w_ds + (int64_t)wave * N + r0 + 4 * (lane & 7);
+    g.sw2 = GU ? p.w2_ds + (int64_t)wave * N + r0 + 4 * (lane & 7) : nullptr;
+    g.sx = p.xst + (int64_t)wave * p.mp + t0 + 4 * (lane & 15);
+    return g;
+}
+
+// Issue the global->LDS loads of one stage (first block kb). A full stage
+// offsets the precomputed pointers; a partial last stage (nblk < 4) re-reads
+// its last valid block in place of the missing ones (values unused).
+template <bool GU>
+__device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g, GemmStageLds<GU>& S,
+                                           int64_t kb, int nblk, int wave, int lane) {
+    const int slot = lane & 7;
+    int64_t da = kb * 32, db0 = da, db1 = da, dsw = kb * p.n, dsx = kb * (int64_t)p.mp;
+    if (nblk < GK_BLK) {
+        // chunk c = slot ^ swz(row) of block c/2; clamp the block, keep the half
+        const int row = 8 * wave + (lane >> 3), tk0 = 16 * wave + (lane >> 3), tk1 = tk0 + 8;
+        auto shift = [&](int r) {
+            const int c = slot ^ swz(r), blk = c >> 1, cb = blk < nblk ? blk : nblk - 1;
+            return (int64_t)(cb - blk) * 32;
+        };
+        da += shift(row);
+        db0 += shift(tk0);
+        db1 += shift(tk1);
+        const int j = wave < nblk ? wave : nblk - 1;
+        dsw += (int64_t)(j - wave) * p.n;
+        dsx += (int64_t)(j - wave) * p.mp;
+    }
+    lds_load16(g.a + da, S.a + wave * 1024);
+    if (GU) lds_load16(g.a2 + da, S.a2 + wave * 1024);
+    lds_load16(g.b0 + db0, S.b + (2 * wave) * 1024);
+    lds_load16(g.b1 + db1, S.b + (2 * wave + 1) * 1024);
+    if (lane < GBM / 4) {
+        lds_load16(g.sw + dsw, S.sw + wave * GBM);
+        if (GU) lds_load16(g.sw2 + dsw, S.sw2 + wave * GBM);
+    }
+    if (lane < GBN / 4) lds_load16(g.sx + dsx, S.sx + wave * GBN);
+}
+
+// Wait until at most `n` vector-memory ops of this wave are outstanding
+// (s_waitcnt vmcnt(n); expcnt and lgkmcnt left at their maxima).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// Workgroup barrier without the release fence of __syncthreads: that fence
+// waits for every outstanding vector-memory op, including the LDS-DMA loads
+// of the later stages. Visibility of a stage is ensured by wait_vm before it;
+// the empty asm statements keep the compiler from moving memory ops across.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// NB consecutive 32-blocks (from j0) of a stage: every MFMA of the group is
+// issued first, then the f32 rescale runs block by block in order.
+template <bool GU, int NB>
+__device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU>& S, int j0, int wc, int lane,
+                                            float (&f)[2][4], float (&g)[2][4]) {
+    const int li = lane & 15, lm = (lane >> 4) * 4, sub = ((lane >> 4) & 1) * 8, hi = lane >> 5;
     const v4i z = {0, 0, 0, 0};
-    for (int64_t b = 0; b < nb; b++) {
-        const long a0 = *(const long*)(A0 + 32 * b), a1 = *(const long*)(A1 + 32 * b);
-        const long b0 = *(const long*)(B0 + 32 * b), b1 = *(const long*)(B1 + 32 * b);
-        const uint2 d0 = *(const uint2*)(a.w_dt + b * N + r0 + lm);
-        const uint2 d1 = *(const uint2*)(a.w_dt + b * N + r0 + 16 + lm);
-        const float x0 = a.xst[b * a.mp + t0 + li], x1 = a.xst[b * a.mp + t0 + 16 + li];
-        const v4i c00 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, z, 0, 0, 0);
-        const v4i c01 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b1, z, 0, 0, 0);
-        const v4i c10 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b0, z, 0, 0, 0);
-        const v4i c11 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, z, 0, 0, 0);
-        const float w0[4] = {uq_half((uint16_t)(d0.x & 0xffff)), uq_half((uint16_t)(d0.x >> 16)),
-                             uq_half((uint16_t)(d0.y & 0xffff)), uq_half((uint16_t)(d0.y >> 16))};
-        const float w1[4] = {uq_half((uint16_t)(d1.x & 0xffff)), uq_half((uint16_t)(d1.x >> 16)),
-                             uq_half((uint16_t)(d1.y & 0xffff)), uq_half((uint16_t)(d1.y >> 16))};
+    v4i c[NB][2], c2[NB][2];
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            f[0][0][m] = fmaf((float)c00[m], w0[m] * x0, f[0][0][m]);
-            f[0][1][m] = fmaf((float)c01[m], w0[m] * x1, f[0][1][m]);
-            f[1][0][m] = fmaf((float)c10[m], w1[m] * x0, f[1][0][m]);
-            f[1][1][m] = fmaf((float)c11[m], w1[m] * x1, f[1][1][m]);
+    for (int jj = 0; jj < NB; jj++) {
+        const int j = j0 + jj, gc = 2 * j + hi;
+        long av[2], a2v[2], bv;
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            const int row = 16 * m + li;
+            const int off = row * 128 + ((gc ^ swz(row)) << 4) + sub;
+            av[m] = *(const long*)(S.a + off);
+            if (GU) a2v[m] = *(const long*)(S.a2 + off);
         }
-        if (GU) {
-            const long g0 = *(const long*)(G0 + 32 * b), g1 = *(const long*)(G1 + 32 * b);
-            const uint2 e0 = *(const uint2*)(a.w2_dt + b * N + r0 + lm);
-            const uint2 e1 = *(const uint2*)(a.w2_dt + b * N + r0 + 16 + lm);
-            const v4i h00 = __builtin_amdgcn_mfma_i32_16x16x32_i8(g0, b0, z, 0, 0, 0);
-            const v4i h01 = __builtin_amdgcn_mfma_i32_16x16x32_i8(g0, b1, z, 0, 0, 0);
-            const v4i h10 = __builtin_amdgcn_mfma_i32_16x16x32_i8(g1, b0, z, 0, 0, 0);
-            const v4i h11 = __builtin_amdgcn_mfma_i32_16x16x32_i8(g1, b1, z, 0, 0, 0);
-            const float u0[4] = {uq_half((uint16_t)(e0.x & 0xffff)), uq_half((uint16_t)(e0.x >> 16)),
-                                 uq_half((uint16_t)(e0.y & 0xffff)), uq_half((uint16_t)(e0.y >> 16))};
-            const float u1[4] = {uq_half((uint16_t)(e1.x & 0xffff)), uq_half((uint16_t)(e1.x >> 16)),
-                                 uq_half((uint16_t)(e1.y & 0xffff)), uq_half((uint16_t)(e1.y >> 16))};
+        {
+            const int tok = wc + li;
+            bv = *(const long*)(S.b + tok * 128 + ((gc ^ swz(tok)) << 4) + sub);
+        }
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                g[0][0][m] = fmaf((float)h00[m], u0[m] * x0, g[0][0][m]);
-                g[0][1][m] = fmaf((float)h01[m], u0[m] * x1, g[0][1][m]);
-                g[1][0][m] = fmaf((float)h10[m], u1[m] * x0, g[1][0][m]);
-                g[1][1][m] = fmaf((float)h11[m], u1[m] * x1, g[1][1][m]);
-            }
+        for (int m = 0; m < 2; m++) {
+            c[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[m], bv, z, 0, 0, 0);
+            if (GU) c2[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2v[m], bv, z, 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int x = 0; x < 2; x++)
+    for (int jj = 0; jj < NB; jj++) {
+        const int j = j0 + jj;
+        const float x = S.sx[j * GBN + wc + li];
 #pragma unroll
-        for (int y = 0; y < 2; y++) {
-            const int64_t t = t0 + 16 * y + li, r = r0 + 16 * x + lm;
-            float4 o;
-            if (GU) {
-                o = make_float4(uq_silu_mul(f[x][y][0], g[x][y][0]), uq_silu_mul(f[x][y][1], g[x][y][1]),
-                                uq_silu_mul(f[x][y][2], g[x][y][2]), uq_silu_mul(f[x][y][3], g[x][y][3]));
-            } else {
-                o = make_float4(f[x][y][0], f[x][y][1], f[x][y][2], f[x][y][3]);
+        for (int m = 0; m < 2; m++) {
+            const v4f w = *(const v4f*)(S.sw + j * GBM + 16 * m + lm);
+            v4f w2;
+            if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + 16 * m + lm);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                f[m][q] = fmaf((float)c[jj][m][q], w[q] * x, f[m][q]);
+                if (GU) g[m][q] = fmaf((float)c2[jj][m][q], w2[q] * x, g[m][q]);
             }
-            *(float4*)(a.y + t * N + r) = o;
         }
+    }
+}
+
+template <bool GU>
+__global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) GemmStageLds<GU> ring[GR];
+    constexpr int LPS = gemm_lps<GU>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wc = wave * 16;
+    const int64_t r0 = (int64_t)blockIdx.x * GBM, t0 = (int64_t)blockIdx.y * GBN;
+    const int64_t nb = a.k / 32, nst = (nb + GK_BLK - 1) / GK_BLK;
+    auto nblk_of = [&](int64_t s) { return (int)(nb - s * GK_BLK < GK_BLK ? nb - s * GK_BLK : GK_BLK); };
+    float f[2][4], g[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) f[m][q] = g[m][q] = 0.0f;
+    const GemmSrc src = gemm_src<GU>(a, r0, t0, wave, lane);
+    // prologue: stages 0 .. GR-2 in flight
+#pragma unroll
+    for (int s = 0; s < GR - 1; s++)
+        if (s < nst) gemm_issue<GU>(a, src, ring[s], (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
+    for (int64_t s = 0; s < nst; s++) {
+        // stage s landed for this wave: the stages issued after it may stay in flight
+        const int64_t later = (nst - 1 - s < GR - 2) ? nst - 1 - s : GR - 2;
+        if (later >= 2) wait_vm<2 * LPS>();
+        else if (later == 1) wait_vm<LPS>();
+        else wait_vm<0>();
+        stage_barrier();  // every wave's loads of stage s landed; stage s-1 fully consumed
+        const int64_t sn = s + GR - 1;
+        if (sn < nst) gemm_issue<GU>(a, src, ring[sn % GR], sn * GK_BLK, nblk_of(sn), wave, lane);
+        const GemmStageLds<GU>& S = ring[s % GR];
+        const int nblk = nblk_of(s);
+        if (nblk == GK_BLK) {
+            gemm_blocks<GU, GU ? 2 : 4>(S, 0, wc, lane, f, g);
+            if (GU) gemm_blocks<GU, 2>(S, 2, wc, lane, f, g);
+        } else {
+            for (int j = 0; j < nblk; j++) gemm_blocks<GU, 1>(S, j, wc, lane, f, g);
+        }
+    }
+    const int li = lane & 15, lm = (lane >> 4) * 4;
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int64_t t = t0 + wc + li, r = r0 + 16 * m + lm;
+        float4 o;
+        if (GU) {
+            o = make_float4(uq_silu_mul(f[m][0], g[m][0]), uq_silu_mul(f[m][1], g[m][1]),
+                            uq_silu_mul(f[m][2], g[m][2]), uq_silu_mul(f[m][3], g[m][3]));
+        } else {
+            o = make_float4(f[m][0], f[m][1], f[m][2], f[m][3]);
+        }
+        *(float4*)(a.y + t * a.n + r) = o;
+    }
 }
 
 // ------------------------------------------------------------------ RoPE + KV
@@ -246,11 +375,35 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
     double acc[DPT];
 #pragma unroll
     for (int i = 0; i < DPT; i++) acc[i] = 0.0;
+    // one 8-byte (HD 128) or 4-byte (HD 64) load per position, 4 positions in flight
+    typedef uint32_t vw_t __attribute__((ext_vector_type(DPT / 2)));
     const uint16_t* vb = a.vcache + kh * HD + kj * DPT;
-    for (int t = 0; t < T; t++) {
-        const double p = (double)sc[t];
+    constexpr int PU = 4;
+    int t = 0;
+    for (; t + PU <= T; t += PU) {
+        vw_t vv[PU];
+        double pp[PU];
 #pragma unroll
-        for (int i = 0; i < DPT; i++) acc[i] = __builtin_fma(p, (double)uq_half(vb[(size_t)t * kvd + i]), acc[i]);
+        for (int u = 0; u < PU; u++) {
+            vv[u] = *(const vw_t*)(vb + (size_t)(t + u) * kvd);
+            pp[u] = (double)sc[t + u];
+        }
+#pragma unroll
+        for (int u = 0; u < PU; u++)
+#pragma unroll
+            for (int i = 0; i < DPT / 2; i++) {
+                acc[2 * i] = __builtin_fma(pp[u], (double)uq_half((uint16_t)(vv[u][i] & 0xffff)), acc[2 * i]);
+                acc[2 * i + 1] = __builtin_fma(pp[u], (double)uq_half((uint16_t)(vv[u][i] >> 16)), acc[2 * i + 1]);
+            }
+    }
+    for (; t < T; t++) {
+        const double p = (double)sc[t];
+        const vw_t v = *(const vw_t*)(vb + (size_t)t * kvd);
+#pragma unroll
+        for (int i = 0; i < DPT / 2; i++) {
+            acc[2 * i] = __builtin_fma(p, (double)uq_half((uint16_t)(v[i] & 0xffff)), acc[2 * i]);
+            acc[2 * i + 1] = __builtin_fma(p, (double)uq_half((uint16_t)(v[i] >> 16)), acc[2 * i + 1]);
+        }
     }
     float* out = a.out + (size_t)tq * (a.heads * HD) + h * HD + kj * DPT;
 #pragma unroll
@@ -259,7 +412,7 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
 
 }  // namespace
 
-void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, uint16_t* dt, hipStream_t s) {
+void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float* dt, hipStream_t s) {
     hipLaunchKernelGGL(k_transpose_scales, dim3((unsigned)((rows * nb + 255) / 256)), dim3(256), 0, s, d, rows, nb, dt);
 }
 void launch_pf_norm(const PfNormArgs& a, int tokens, hipStream_t s) {
@@ -269,8 +422,8 @@ void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, 
     hipLaunchKernelGGL(k_pf_quant, dim3((unsigned)((k + 255) / 256), tokens), dim3(256), 0, s, x, k, mp, xq, xst);
 }
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s) {
-    if (a.n % 64 || a.mp % 64 || a.k % 32) return -1;
-    const dim3 grid((unsigned)(a.n / 64), (unsigned)(a.mp / 64));
+    if (a.n % 64 || a.mp % GBN || a.k % 32 || a.k <= 0) return -1;
+    const dim3 grid((unsigned)(a.n / GBM), (unsigned)(a.mp / GBN));
     if (a.w2_qs) hipLaunchKernelGGL(k_pf_gemm<true>, grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(k_pf_gemm<false>, grid, dim3(256), 0, s, a);
     return 0;

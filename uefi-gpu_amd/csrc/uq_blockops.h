@@ -38,32 +38,61 @@ __device__ inline float block_max_f(float v, float* red) {
 
 
 // Residual + RMSNorm + block-32 quant of a.dim values by one workgroup of WG
-// threads (element i = j*WG + t, so each 32-block sits in half a wave). The
-// quantized vector goes to q/s (LDS or global; scale b at s[b * sstride]);
-// write_x stores the summed residual to a.x_out. Ends with a barrier.
-template <int WG>
-__device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red,
-                                  int sstride = 1) {
-    constexpr int PER = (4096 + WG - 1) / WG;  // dim <= 4096
+// threads (element i = j*WG + t, so each 32-block sits in half a wave), in two
+// halves: norm_quant_load issues the raw loads (activations, residual, gamma
+// or the embedding row) and nothing else, so a kernel can issue its weight
+// loads after it and still have the prologue wait only for the activations
+// (vector-memory counters drain in issue order); norm_quant_finish does the
+// arithmetic. The quantized vector goes to q/s (LDS or global; scale b at
+// s[b * sstride]); write_x stores the summed residual to a.x_out. Ends with a
+// barrier.
+// PER elements per thread: dim <= PER * WG.
+template <int PER>
+struct NqRegs {
+    float x[PER], r[PER], g[PER];
+    int e[PER];
+    uint16_t d[PER];
+};
+template <int WG, int MAXD>
+using NqRegsFor = NqRegs<(MAXD + WG - 1) / WG>;
+
+template <int WG, int PER>
+__device__ __forceinline__ void norm_quant_load(const NormQuantArgs& a, NqRegs<PER>& v) {
     const int t = threadIdx.x, D = a.dim;
-    float xv[PER];
-    double ss = 0.0;
     const uint32_t tok = a.embed_qs ? *a.token : 0u;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int i = j * WG + t;
         if (i < D) {
-            float v;
             if (a.embed_qs) {
                 const int64_t row = (int64_t)tok;
-                v = uq_half(a.embed_d[row * (D / 32) + i / 32]) * (float)a.embed_qs[row * D + i];
+                v.d[j] = a.embed_d[row * (D / 32) + i / 32];
+                v.e[j] = a.embed_qs[row * D + i];
             } else {
-                v = a.x[i];
-                if (a.residual) v = v + a.residual[i];
+                v.x[j] = a.x[i];
+                v.r[j] = a.residual ? a.residual[i] : 0.0f;
             }
-            if (write_x && a.x_out) a.x_out[i] = v;
-            xv[j] = v;
-            const float sq = v * v;
+            v.g[j] = a.gamma[i];
+        }
+    }
+}
+
+template <int WG, int PER>
+__device__ __forceinline__ void norm_quant_finish(const NormQuantArgs& a, const NqRegs<PER>& v, bool write_x,
+                                                  int8_t* q, float* s, double* red, int sstride = 1) {
+    const int t = threadIdx.x, D = a.dim;
+    float xv[PER];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * WG + t;
+        if (i < D) {
+            float x;
+            if (a.embed_qs) x = uq_half(v.d[j]) * (float)v.e[j];
+            else x = a.residual ? v.x[j] + v.r[j] : v.x[j];
+            if (write_x && a.x_out) a.x_out[i] = x;
+            xv[j] = x;
+            const float sq = x * x;
             ss += (double)sq;
         }
     }
@@ -75,7 +104,7 @@ __device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* 
         const int i = j * WG + t;
         if (i < D) {
             const float tmp = xv[j] * scale;
-            const float y = tmp * a.gamma[i];
+            const float y = tmp * v.g[j];
             float sc;
             const int8_t qv = uq_quant_lane(y, &sc);
             q[i] = qv;
@@ -83,6 +112,14 @@ __device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* 
         }
     }
     __syncthreads();
+}
+
+template <int WG>
+__device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red,
+                                  int sstride = 1) {
+    NqRegsFor<WG, 4096> v;
+    norm_quant_load<WG>(a, v);
+    norm_quant_finish<WG>(a, v, write_x, q, s, red, sstride);
 }
 
 struct Cand {

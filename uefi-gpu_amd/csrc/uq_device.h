@@ -99,25 +99,75 @@ UQ_DEV int uq_dot32(const int4& wa, const int4& wb, const int4& xa, const int4& 
     return c;
 }
 
-UQ_DEV double uq_shfl_xor_d(double v, int mask) {
+// Cross-lane reductions without LDS traffic: DPP lane moves inside rows of 16
+// lanes (quad_perm xor 1 and xor 2, row_half_mirror, row_mirror, row_ror:8)
+// and the gfx950 permlane16/32 swaps across rows. Every lane of a group ends
+// with the same bits (each step adds a value and its partner's, commutatively).
+constexpr int UQ_DPP_XOR1 = 0xB1, UQ_DPP_XOR2 = 0x4E, UQ_DPP_MIRROR = 0x140, UQ_DPP_HALF_MIRROR = 0x141,
+              UQ_DPP_ROR8 = 0x128;
+template <int CTRL>
+UQ_DEV int uq_dpp(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+UQ_DEV double uq_dpp_d(double v) {
     int2 p = __builtin_bit_cast(int2, v);
-    p.x = __shfl_xor(p.x, mask, 64);
-    p.y = __shfl_xor(p.y, mask, 64);
+    p.x = uq_dpp<CTRL>(p.x);
+    p.y = uq_dpp<CTRL>(p.y);
     return __builtin_bit_cast(double, p);
+}
+template <int CTRL>
+UQ_DEV float uq_dpp_f(float v) { return __builtin_bit_cast(float, uq_dpp<CTRL>(__builtin_bit_cast(int, v))); }
+// rows (0,1) and (2,3) of 16 lanes, or halves of 32 lanes, summed / maxed
+UQ_DEV double uq_swap16_sum(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(p.x, p.x, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(p.y, p.y, false, false);
+    return __builtin_bit_cast(double, make_int2(a[0], b[0])) + __builtin_bit_cast(double, make_int2(a[1], b[1]));
+}
+UQ_DEV double uq_swap32_sum(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    const auto a = __builtin_amdgcn_permlane32_swap(p.x, p.x, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(p.y, p.y, false, false);
+    return __builtin_bit_cast(double, make_int2(a[0], b[0])) + __builtin_bit_cast(double, make_int2(a[1], b[1]));
+}
+UQ_DEV float uq_swap16_max(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
+}
+UQ_DEV float uq_swap32_max(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    const auto a = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)a[0]), __builtin_bit_cast(float, (int)a[1]));
 }
 
 // Sum of a double over groups of G consecutive lanes (G a power of two <= 64);
 // every lane of the group receives the total.
 template <int G>
 UQ_DEV double uq_group_sum(double v) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v += uq_shfl_xor_d(v, off);
+    if (G >= 2) v = v + uq_dpp_d<UQ_DPP_XOR1>(v);
+    if (G >= 4) v = v + uq_dpp_d<UQ_DPP_XOR2>(v);
+    if (G >= 8) v = v + uq_dpp_d<UQ_DPP_HALF_MIRROR>(v);
+    if (G >= 16) v = v + uq_dpp_d<UQ_DPP_MIRROR>(v);
+    if (G >= 32) v = uq_swap16_sum(v);
+    if (G >= 64) v = uq_swap32_sum(v);
     return v;
 }
 template <int G>
 UQ_DEV float uq_group_max(float v) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if (G >= 2) v = fmaxf(v, uq_dpp_f<UQ_DPP_XOR1>(v));
+    if (G >= 4) v = fmaxf(v, uq_dpp_f<UQ_DPP_XOR2>(v));
+    if (G >= 8) v = fmaxf(v, uq_dpp_f<UQ_DPP_HALF_MIRROR>(v));
+    if (G >= 16) v = fmaxf(v, uq_dpp_f<UQ_DPP_MIRROR>(v));
+    if (G >= 32) v = uq_swap16_max(v);
+    if (G >= 64) v = uq_swap32_max(v);
+    return v;
+}
+// Sum over the lanes of a wave with equal lane % LP (LP in 8, 16, 32, 64).
+template <int LP>
+UQ_DEV double uq_rows_sum(double v) {
+    if (LP <= 8) v = v + uq_dpp_d<UQ_DPP_ROR8>(v);
+    if (LP <= 16) v = uq_swap16_sum(v);
+    if (LP <= 32) v = uq_swap32_sum(v);
     return v;
 }
 

@@ -5,11 +5,12 @@
 //
 // Design (bandwidth-bound, no MFMA):
 //  * weights are repacked once so every lane issues 16-byte global loads:
-//    Q8_0 -> int8 plane [rows][K] + fp16 scale plane; Q4_K superblocks are
-//    already 144 = 9*16 bytes; Q3_K -> 96-byte quant plane + 12-byte scale
-//    plane + fp16 d plane.
+//    Q8_0 -> int8 plane [rows][K] + fp16 scale plane; Q4_K -> 128-byte nibble
+//    plane + 16-byte header plane (d, dmin, scales); Q3_K -> 96-byte quant
+//    plane + 12-byte scale plane + fp16 d plane. Each repack is checked by
+//    rebuilding the GGUF bytes on the device.
 //  * a row is owned by LPR consecutive lanes of a wave64; lane `sub` handles
-//    work units sub, sub+LPR, ... (Q8_0 unit = 32 values, Q4_K = 64, Q3_K = 128).
+//    work units sub, sub+LPR, ... (Q8_0 unit = 16 values, Q4_K = 64, Q3_K = 128).
 //    The lane's activation units are loaded into registers once and reused for
 //    every row the wave visits (grid-stride over row sets).
 //  * int32 per-block dots with v_dot4_i32_i8; each block contributes an exact
@@ -67,6 +68,28 @@ __global__ __launch_bounds__(WG) void k_q8_verify(const int8_t* __restrict__ qs,
     for (int j = 0; j < 32; j++) miss += (uint8_t)qs[blk * 32 + j] != p[2 + j];
     if (miss) atomicAdd(bad, miss);
 }
+// Q4_K: 144-byte GGUF superblock (d, dmin, 12 scale bytes, qs 128) ->
+// qs[blk][128] and hdr[blk][16] = d | dmin | scales.
+__global__ __launch_bounds__(WG) void k_q4k_repack(const uint8_t* __restrict__ src, int64_t blocks,
+                                                   int8_t* __restrict__ q, uint8_t* __restrict__ hdr) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint8_t* p = src + blk * 144;
+    uint8_t* dq = (uint8_t*)q + blk * 128;
+    for (int j = 0; j < 16; j++) hdr[blk * 16 + j] = p[j];
+    for (int j = 0; j < 128; j++) dq[j] = p[16 + j];
+}
+__global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q, const uint8_t* __restrict__ hdr,
+                                                   const uint8_t* __restrict__ src, int64_t blocks,
+                                                   unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint8_t* p = src + blk * 144;
+    unsigned miss = 0;
+    for (int j = 0; j < 16; j++) miss += hdr[blk * 16 + j] != p[j];
+    for (int j = 0; j < 128; j++) miss += (uint8_t)q[blk * 128 + j] != p[16 + j];
+    if (miss) atomicAdd(bad, miss);
+}
 // Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, scales 12, d 2) ->
 // q[blk][96] = hmask|qs, sc[blk][12], d[blk].
 __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
@@ -105,28 +128,32 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
     typename KQ::X xr[NBL];
-#pragma unroll
-    for (int i = 0; i < NBL; i++) {
-        const int u = sub + LPR * i;
-        if (u < nu) KQ::load_x(xr[i], xq, xs, u);
-        else KQ::zero_x(xr[i]);
-    }
+    load_xr<KQ, LPR, NBL>(xr, xq, xs, nu, sub);
     for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
         const int64_t row = row0 + wave * RPW + grp;
-        if (row < rows) {
-            double acc = 0.0, acc2 = 0.0;
+        // rows past the end load the last row; every lane takes part in the reductions
+        const int64_t rr = row < rows ? row : rows - 1;
+        typename KQ::W wv[NBL], wv2[NBL];
 #pragma unroll
-            for (int i = 0; i < NBL; i++) {
-                const int u = sub + LPR * i;
-                if (u < nu) {
-                    acc += KQ::term(w, row, nu, u, xr[i]);
-                    if (GATEUP) acc2 += KQ::term(w2, row, nu, u, xr[i]);
-                }
-            }
-            acc = uq_group_sum<LPR>(acc);
-            if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
-            if (sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = KQ::load_w(w, rr, nu, uc);
+            if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
         }
+        double acc = 0.0, acc2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            const double t = KQ::dot(wv[i], xr[i], uc);
+            acc += u < nu ? t : 0.0;
+            if (GATEUP) {
+                const double t2 = KQ::dot(wv2[i], xr[i], uc);
+                acc2 += u < nu ? t2 : 0.0;
+            }
+        }
+        acc = uq_group_sum<LPR>(acc);
+        if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
+        if (row < rows && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
     }
 }
 
@@ -149,7 +176,7 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
     } else if (kind == KIND_Q4_K) {
         const int64_t sb = (row * (K / 256)) + b / 8;
         const int a = (int)(b % 8), j = a >> 1, h = a & 1;
-        const uint8_t* qs = (const uint8_t*)w.qs + sb * 144 + 16 + 32 * j;
+        const uint8_t* qs = (const uint8_t*)w.qs + sb * 128 + 32 * j;
         const int* xp = (const int*)x;
         for (int k = 0; k < 8; k++) {
             const int wq = *(const int*)(qs + 4 * k);
@@ -217,6 +244,13 @@ void launch_q8_repack(const uint8_t* gguf, int64_t rows, int64_t nb, int8_t* qs,
 void launch_q8_verify(const int8_t* qs, const uint16_t* d, const uint8_t* gguf, int64_t rows, int64_t nb,
                       unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q8_verify, dim3(grid_for(rows * nb, WG)), dim3(WG), 0, s, qs, d, gguf, rows, nb, bad);
+}
+void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* hdr, hipStream_t s) {
+    hipLaunchKernelGGL(k_q4k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, hdr);
+}
+void launch_q4k_verify(const int8_t* q, const uint8_t* hdr, const uint8_t* gguf, int64_t blocks, unsigned* bad,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(k_q4k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, hdr, gguf, blocks, bad);
 }
 void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, sc, d);

@@ -149,7 +149,10 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
         off_d = align256((size_t)(n * m));
         total = off_d + align256((size_t)(n / 32 * m) * 2);
     } else if (kind == KIND_Q4_K) {
-        total = align256((size_t)(rb * m));
+        const size_t blocks = (size_t)(n / 256 * m);
+        off_q = 0;
+        off_sc = align256(blocks * 128);
+        total = off_sc + align256(blocks * 16);
     } else {
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
@@ -162,20 +165,9 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
     uint8_t* base = (uint8_t*)w.alloc;
     w.qs = (const int8_t*)(base + off_q);
     if (kind != KIND_Q4_K) w.d = (const uint16_t*)(base + off_d);
-    if (kind == KIND_Q3_K) w.sc = base + off_sc;
+    if (kind != KIND_Q8_0) w.sc = base + off_sc;
     int rc = OK;
-    if (kind == KIND_Q4_K) {
-        // superblocks are used as stored; the readback check is a plain compare
-        hipError_t e = hipMemcpyAsync(base, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
-        if (e == hipSuccess) {
-            std::vector<uint8_t> back((size_t)w.gguf_bytes);
-            e = hipMemcpyAsync(back.data(), base, back.size(), hipMemcpyDeviceToHost, s);
-            if (e == hipSuccess) e = hipStreamSynchronize(s);
-            if (e == hipSuccess && std::memcmp(back.data(), gguf, back.size()) != 0)
-                rc = set_error(ERR_DEVICE, "weight_upload: readback mismatch");
-        }
-        if (e != hipSuccess) rc = set_error(ERR_DEVICE, std::string("weight_upload: ") + hipGetErrorString(e));
-    } else {
+    {
         void* staging = nullptr;
         hipError_t e = hipMalloc(&staging, (size_t)w.gguf_bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(staging, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
@@ -184,6 +176,10 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
             if (kind == KIND_Q8_0) {
                 launch_q8_repack((const uint8_t*)staging, m, n / 32, (int8_t*)w.qs, (uint16_t*)w.d, s);
                 launch_q8_verify(w.qs, w.d, (const uint8_t*)staging, m, n / 32, g_ctx.dcount, s);
+            } else if (kind == KIND_Q4_K) {
+                const int64_t blocks = n / 256 * m;
+                launch_q4k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, s);
+                launch_q4k_verify(w.qs, w.sc, (const uint8_t*)staging, blocks, g_ctx.dcount, s);
             } else {
                 const int64_t blocks = n / 256 * m;
                 launch_q3k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, (uint16_t*)w.d, s);

@@ -50,6 +50,8 @@ __global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
     const int rbase = region == 0 ? 0 : (region == 1 ? a.heads * hd : a.heads * hd + kvd);
     const int64_t nu = a.dim / Q8::UNIT;
     const WArgs w{a.w_qs, a.w_d, nullptr};
+    NqRegsFor<256, NBL * 32 * Q8::UNIT> nqv;  // dim <= 32 lanes x NBL units x 16
+    norm_quant_load<256>(a.nq, nqv);  // activations first: the prologue waits only for them
     Q8::W wv[NBL];
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
@@ -70,7 +72,7 @@ __global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
             sn = a.trig[(size_t)pos * hd + half + j];
         }
     }
-    norm_quant<256>(a.nq, blockIdx.x == 0, sq, ssc, red);
+    norm_quant_finish<256>(a.nq, nqv, blockIdx.x == 0, sq, ssc, red);
     if (!live) return;  // whole wave; no barrier follows
     double acc = 0.0;
 #pragma unroll
@@ -194,11 +196,9 @@ __global__ __launch_bounds__(AT_WG) void k_attention(AttnArgs a) {
             }
         }
     }
-    // lanes with the same chunk in a wave: c = lane % LP; combine over lane bits >= LP
+    // lanes with the same chunk in a wave: c = lane % LP
 #pragma unroll
-    for (int off = LP; off < 64; off <<= 1)
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[i] += uq_shfl_xor_d(acc[i], off);
+    for (int i = 0; i < 8; i++) acc[i] = uq_rows_sum<LP>(acc[i]);
     const int wave = tid >> 6, lane = tid & 63;
     if (lane < LP)
 #pragma unroll
@@ -229,6 +229,8 @@ __global__ __launch_bounds__(1024) void k_gateup_q(GateArgs a) {
     const int64_t nu = a.k / Q8::UNIT;
     const int64_t row = (int64_t)blockIdx.x * 32 + wave * 2 + grp;
     const WArgs wg{a.g_qs, a.g_d, nullptr}, wu{a.u_qs, a.u_d, nullptr};
+    NqRegsFor<1024, NBL * 32 * Q8::UNIT> nqv;  // dim <= 32 lanes x NBL units x 16
+    norm_quant_load<1024>(a.nq, nqv);  // activations first: the prologue waits only for them
     Q8::W gw[NBL], uw[NBL];
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(1024) void k_gateup_q(GateArgs a) {
             uw[i] = Q8::load_w(wu, row, nu, u);
         }
     }
-    norm_quant<1024>(a.nq, blockIdx.x == 0, sq, ssc, red);
+    norm_quant_finish<1024>(a.nq, nqv, blockIdx.x == 0, sq, ssc, red);
     double g = 0.0, uacc = 0.0;
 #pragma unroll
     for (int i = 0; i < NBL; i++) {

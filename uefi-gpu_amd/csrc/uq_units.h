@@ -2,7 +2,10 @@
 // decode-step kernels. A unit is the slice of one row that one lane consumes
 // per step: Q8_0 16 values (one 16-byte load), Q4_K 64 values (one 32-byte qs
 // pair + the superblock header), Q3_K 128 values (half a superblock).
-// term() returns the unit's exact double contribution to the row's dot.
+// load_w(w, row, nu, u) issues the unit's weight loads and nothing else;
+// dot(W, X, u) returns the unit's double contribution to the row's dot;
+// term() = dot(load_w()). Kernels issue every unit's load_w of a row before
+// the first dot, so a row costs one memory round trip.
 #pragma once
 #include "uq_device.h"
 
@@ -33,7 +36,7 @@ struct Q8 {
         const int64_t piece = row * nu + u;
         return W{uq_ntload16(w.qs + piece * 16), w.d[piece >> 1]};
     }
-    static UQ_DEV double dot(const W& wv, const X& x) {
+    static UQ_DEV double dot(const W& wv, const X& x, int = 0) {
         int c = uq_dot4(wv.q.x, x.a.x, 0);
         c = uq_dot4(wv.q.y, x.a.y, c);
         c = uq_dot4(wv.q.z, x.a.z, c);
@@ -48,29 +51,44 @@ struct Q8 {
 
 // Q4_K unit: pair j of a superblock = 32 bytes of qs holding sub-blocks 2j (low
 // nibbles) and 2j+1 (high nibbles). ggml value = d*sc*q - dmin*m per sub-block.
+// Planes (repacked at upload, byte-verified): qs[sb][128] streamed with
+// non-temporal loads, so a row's lanes read contiguous 32-byte pieces, and
+// the 16-byte headers hdr[sb] = d | dmin | 12 scale bytes, read through the
+// cache (the four lanes of a superblock share one). The activation sums of a
+// unit (for the min term) are formed once when the activation is loaded.
 struct Q4K {
     static constexpr int UNIT = 64;
-    struct X { int4 a0, a1, b0, b1; float s0, s1; };
+    struct X { int4 a0, a1, b0, b1; float s0, s1; int xl, xh; };
+    static UQ_DEV int sum16(const int4& v, int c) {
+        const int ones = 0x01010101;
+        c = uq_dot4(ones, v.x, c); c = uq_dot4(ones, v.y, c);
+        c = uq_dot4(ones, v.z, c); return uq_dot4(ones, v.w, c);
+    }
     static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
         const int4* p = (const int4*)(xq + (size_t)u * 64);
         x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
         x.s0 = xs[2 * u];
         x.s1 = xs[2 * u + 1];
+        x.xl = sum16(x.a1, sum16(x.a0, 0));
+        x.xh = sum16(x.b1, sum16(x.b0, 0));
     }
     static UQ_DEV void zero_x(X& x) {
         x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
         x.s0 = x.s1 = 0.0f;
+        x.xl = x.xh = 0;
     }
     static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
     static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
-    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+    struct W { int4 q0, q1, hdr; };
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
         const int64_t sb = (row * nu + u) >> 2;  // nu = 4 * superblocks per row
+        const uint8_t* q = (const uint8_t*)w.qs + sb * 128 + 32 * (u & 3);
+        return W{uq_ntload16(q), uq_ntload16(q + 16), *(const int4*)(w.sc + sb * 16)};
+    }
+    static UQ_DEV double dot(const W& wv, const X& x, int u) {
         const int j = u & 3;
-        const uint8_t* blk = (const uint8_t*)w.qs + sb * 144;
-        const int4 hdr = uq_ntload16(blk);
-        const int4 q0 = uq_ntload16(blk + 16 + 32 * j);
-        const int4 q1 = uq_ntload16(blk + 32 + 32 * j);
-        int il = 0, ih = 0, xl = 0, xh = 0;
+        const int4 q0 = wv.q0, q1 = wv.q1, hdr = wv.hdr;
+        int il = 0, ih = 0;
         il = uq_dot4(lo4(q0.x), x.a0.x, il); il = uq_dot4(lo4(q0.y), x.a0.y, il);
         il = uq_dot4(lo4(q0.z), x.a0.z, il); il = uq_dot4(lo4(q0.w), x.a0.w, il);
         il = uq_dot4(lo4(q1.x), x.a1.x, il); il = uq_dot4(lo4(q1.y), x.a1.y, il);
@@ -79,41 +97,42 @@ struct Q4K {
         ih = uq_dot4(hi4(q0.z), x.b0.z, ih); ih = uq_dot4(hi4(q0.w), x.b0.w, ih);
         ih = uq_dot4(hi4(q1.x), x.b1.x, ih); ih = uq_dot4(hi4(q1.y), x.b1.y, ih);
         ih = uq_dot4(hi4(q1.z), x.b1.z, ih); ih = uq_dot4(hi4(q1.w), x.b1.w, ih);
-        const int ones = 0x01010101;
-        xl = uq_dot4(ones, x.a0.x, xl); xl = uq_dot4(ones, x.a0.y, xl);
-        xl = uq_dot4(ones, x.a0.z, xl); xl = uq_dot4(ones, x.a0.w, xl);
-        xl = uq_dot4(ones, x.a1.x, xl); xl = uq_dot4(ones, x.a1.y, xl);
-        xl = uq_dot4(ones, x.a1.z, xl); xl = uq_dot4(ones, x.a1.w, xl);
-        xh = uq_dot4(ones, x.b0.x, xh); xh = uq_dot4(ones, x.b0.y, xh);
-        xh = uq_dot4(ones, x.b0.z, xh); xh = uq_dot4(ones, x.b0.w, xh);
-        xh = uq_dot4(ones, x.b1.x, xh); xh = uq_dot4(ones, x.b1.y, xh);
-        xh = uq_dot4(ones, x.b1.z, xh); xh = uq_dot4(ones, x.b1.w, xh);
         // header: d (bytes 0-1), dmin (2-3), 12 scale bytes (4-15)
         const float dd = uq_half((uint16_t)(hdr.x & 0xffff));
         const float dm = uq_half((uint16_t)((unsigned)hdr.x >> 16));
-        const uint64_t slo = (uint64_t)(uint32_t)hdr.y | ((uint64_t)(uint32_t)hdr.z << 32);
-        const uint32_t shi = (uint32_t)hdr.w;
         int sc0, m0, sc1, m1;
-        scale_min(2 * j, slo, shi, sc0, m0);
-        scale_min(2 * j + 1, slo, shi, sc1, m1);
+        scale_min_pair(j, (uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w, sc0, m0, sc1, m1);
         const float d0 = dd * (float)sc0, n0 = dm * (float)m0;
         const float d1 = dd * (float)sc1, n1 = dm * (float)m1;
-        const double t0 = (double)x.s0 * ((double)d0 * (double)il - (double)n0 * (double)xl);
-        const double t1 = (double)x.s1 * ((double)d1 * (double)ih - (double)n1 * (double)xh);
+        const double t0 = (double)x.s0 * ((double)d0 * (double)il - (double)n0 * (double)x.xl);
+        const double t1 = (double)x.s1 * ((double)d1 * (double)ih - (double)n1 * (double)x.xh);
         return t0 + t1;
     }
-    static UQ_DEV int sbyte(int k, uint64_t lo, uint32_t hi) {
-        return k < 8 ? (int)((lo >> (8 * k)) & 0xff) : (int)((hi >> (8 * (k - 8))) & 0xff);
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        return dot(load_w(w, row, nu, u), x, u);
     }
-    // ggml get_scale_min_k4 over the 12 scale bytes held in registers
-    static UQ_DEV void scale_min(int j, uint64_t lo, uint32_t hi, int& sc, int& m) {
-        if (j < 4) {
-            sc = sbyte(j, lo, hi) & 63;
-            m = sbyte(j + 4, lo, hi) & 63;
-        } else {
-            sc = (sbyte(j + 4, lo, hi) & 0xF) | ((sbyte(j - 4, lo, hi) >> 6) << 4);
-            m = (sbyte(j + 4, lo, hi) >> 4) | ((sbyte(j, lo, hi) >> 6) << 4);
-        }
+    // ggml get_scale_min_k4 for sub-blocks 2j and 2j+1 (j = 0..3), branch-free.
+    // Scale bytes b0..b11 arrive as three little-endian words s0, s1, s2.
+    // Sub-block k < 4: sc = b[k] & 63, m = b[k+4] & 63; k >= 4: sc = (b[k+4]
+    // & 15) | (b[k-4] >> 6) << 4, m = (b[k+4] >> 4) | (b[k] >> 6) << 4.
+    static UQ_DEV int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
+    static UQ_DEV void scale_min_pair(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc0, int& m0, int& sc1,
+                                      int& m1) {
+        const int k0 = 2 * j & 3;                    // byte index within its word
+        // low form (j < 2): sub-blocks 2j, 2j+1 in word s0, mins in word s1
+        const int ls0 = byte_of(s0, k0) & 63, ls1 = byte_of(s0, k0 + 1) & 63;
+        const int lm0 = byte_of(s1, k0) & 63, lm1 = byte_of(s1, k0 + 1) & 63;
+        // high form (j >= 2): b[k+4] in s2, b[k-4] in s0, b[k] in s1
+        const int h0 = byte_of(s2, k0), h1 = byte_of(s2, k0 + 1);
+        const int hs0 = (h0 & 15) | ((byte_of(s0, k0) >> 6) << 4);
+        const int hs1 = (h1 & 15) | ((byte_of(s0, k0 + 1) >> 6) << 4);
+        const int hm0 = (h0 >> 4) | ((byte_of(s1, k0) >> 6) << 4);
+        const int hm1 = (h1 >> 4) | ((byte_of(s1, k0 + 1) >> 6) << 4);
+        const bool hi = j >= 2;
+        sc0 = hi ? hs0 : ls0;
+        m0 = hi ? hm0 : lm0;
+        sc1 = hi ? hs1 : ls1;
+        m1 = hi ? hm1 : lm1;
     }
 };
 
@@ -155,20 +174,24 @@ struct Q3K {
         const int high = (int)((s2 >> (8 * (k & 3) + 2 * (2 * n + (k >> 2)))) & 3u);
         return low | (high << 4);
     }
-    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+    struct W { int4 h0, h1, q0, q1; uint32_t s0, s1, s2; uint16_t d; };
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
         const int64_t sb = (row * nu + u) >> 1;  // nu = 2 * superblocks per row
-        const int n = u & 1;
         const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
-        const int4 h0 = uq_ntload16(blk), h1 = uq_ntload16(blk + 16);
-        const int4 q0 = uq_ntload16(blk + 32 + 32 * n), q1 = uq_ntload16(blk + 48 + 32 * n);
+        const uint8_t* q = blk + 32 + 32 * (u & 1);
         const uint32_t* sp = (const uint32_t*)(w.sc + sb * 12);
-        const uint64_t slo = (uint64_t)sp[0] | ((uint64_t)sp[1] << 32);
-        const uint32_t s2 = sp[2];
-        const float dd = uq_half(w.d[sb]);
+        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sp[0], sp[1], sp[2],
+                 w.d[sb]};
+    }
+    static UQ_DEV double dot(const W& wv, const X& x, int u) {
+        const int n = u & 1;
+        const uint64_t slo = (uint64_t)wv.s0 | ((uint64_t)wv.s1 << 32);
+        const uint32_t s2 = wv.s2;
+        const float dd = uq_half(wv.d);
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int4 w0 = extract(q0, h0, 2 * j, 4 * n + j), w1 = extract(q1, h1, 2 * j, 4 * n + j);
+            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, 4 * n + j), w1 = extract(wv.q1, wv.h1, 2 * j, 4 * n + j);
             const int4 xa = x.v[2 * j], xb = x.v[2 * j + 1];
             const int ones = 0x01010101;
             int i0 = dot16(w0, xa, 0), i1 = dot16(w1, xb, 0);
@@ -183,27 +206,43 @@ struct Q3K {
         }
         return acc;
     }
+    static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
+        return dot(load_w(w, row, nu, u), x, u);
+    }
 };
 
 
 // Activation units of one lane (units sub, sub+LPR, ...) kept in registers.
+// Loads are issued unconditionally (a unit past the row end reads the last
+// unit) and zeroed afterwards, so they all go out before the first wait.
 template <class KQ, int LPR, int NBL>
 UQ_DEV void load_xr(typename KQ::X* xr, const int8_t* xq, const float* xs, int64_t nu, int sub) {
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int u = sub + LPR * i;
-        if (u < nu) KQ::load_x(xr[i], xq, xs, u);
-        else KQ::zero_x(xr[i]);
+        KQ::load_x(xr[i], xq, xs, u < nu ? u : (int)nu - 1);
     }
+#pragma unroll
+    for (int i = 0; i < NBL; i++)
+        if (sub + LPR * i >= nu) KQ::zero_x(xr[i]);
 }
-// This lane's share of row `row`, summed over the LPR lanes of its group.
+// This lane's share of row `row`, summed over the LPR lanes of its group: all
+// units' weight loads first, then the dots (a unit past the row end loads
+// the last unit and is dropped by a select).
 template <class KQ, int LPR, int NBL>
 UQ_DEV double row_dot(const WArgs& w, int64_t row, int64_t nu, int sub, const typename KQ::X* xr) {
+    typename KQ::W wv[NBL];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i;
+        wv[i] = KQ::load_w(w, row, nu, u < nu ? u : (int)nu - 1);
+    }
     double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int u = sub + LPR * i;
-        if (u < nu) acc += KQ::term(w, row, nu, u, xr[i]);
+        const double t = KQ::dot(wv[i], xr[i], u < nu ? u : (int)nu - 1);
+        acc += u < nu ? t : 0.0;
     }
     return uq_group_sum<LPR>(acc);
 }

@@ -137,7 +137,8 @@ def prefill_gemm_bench(tokens=512, reps=20):
 
 
 def q4k_sweep(copies=3, reps=30):
-    """The same bs=1 sweep with Q4_K weights (144 B per 256 values)."""
+    """The same bs=1 sweep with Q4_K weights (144 B per 256 values); lm_head
+    alone timed over back-to-back launches."""
     weights, pairs, names = [], [], []
     for c in range(copies):
         for name, N, K, pair in SHAPES:
@@ -148,8 +149,10 @@ def q4k_sweep(copies=3, reps=30):
                 names.append(name)
     q4 = lambda N, K: N * (K // 256) * 144 + K + (K // 32) * 4 + 4 * N
     step_bytes = sum(q4(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else q4(N, K) for _, N, K, pair in SHAPES)
-    lm = names.index("lm_head")
-    total_ms, lm_ms = uq.time_matvecs(weights, pairs, 8960, reps, 3, lm)
+    total_ms, _ = uq.time_matvecs(weights, pairs, 8960, reps, 3, -1)
+    lm_ws = [w for w, n in zip(weights, names) if n == "lm_head"]
+    lm_total, _ = uq.time_matvecs(lm_ws, [0] * len(lm_ws), 1536, reps, 3, -1)
+    lm_ms = lm_total / (reps * len(lm_ws))
     for w in weights:
         w.free()
     return {"GBs": round(step_bytes * reps * copies / (total_ms / 1e3) / 1e9, 1), "bytes_per_step": step_bytes,

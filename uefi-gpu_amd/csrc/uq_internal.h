@@ -53,9 +53,10 @@ void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStrea
 void launch_q8_repack(const uint8_t* gguf, int64_t rows, int64_t nb, int8_t* qs, uint16_t* d, hipStream_t s);
 void launch_q8_verify(const int8_t* qs, const uint16_t* d, const uint8_t* gguf, int64_t rows, int64_t nb,
                       unsigned* mismatches, hipStream_t s);
-void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* hdr, hipStream_t s);
-void launch_q4k_verify(const int8_t* q, const uint8_t* hdr, const uint8_t* gguf, int64_t blocks, unsigned* bad,
+void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int64_t spr, int8_t* q, uint8_t* scm, uint32_t* dm,
                        hipStream_t s);
+void launch_q4k_verify(const int8_t* q, const uint8_t* scm, const uint32_t* dm, const uint8_t* gguf, int64_t blocks,
+                       int64_t spr, unsigned* bad, hipStream_t s);
 void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s);
 void launch_q3k_verify(const int8_t* q, const uint8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
                        unsigned* mismatches, hipStream_t s);

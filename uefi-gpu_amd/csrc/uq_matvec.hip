@@ -6,7 +6,7 @@
 // Design (bandwidth-bound, no MFMA):
 //  * weights are repacked once so every lane issues 16-byte global loads:
 //    Q8_0 -> int8 plane [rows][K] + fp16 scale plane; Q4_K -> 128-byte nibble
-//    plane + 16-byte header plane (d, dmin, scales); Q3_K -> 96-byte quant
+//    plane + 16 unpacked scale/min bytes + d|dmin per superblock; Q3_K -> 96-byte quant
 //    plane + 12-byte scale plane + fp16 d plane. Each repack is checked by
 //    rebuilding the GGUF bytes on the device.
 //  * a row is owned by LPR consecutive lanes of a wave64; lane `sub` handles
@@ -68,26 +68,56 @@ __global__ __launch_bounds__(WG) void k_q8_verify(const int8_t* __restrict__ qs,
     for (int j = 0; j < 32; j++) miss += (uint8_t)qs[blk * 32 + j] != p[2 + j];
     if (miss) atomicAdd(bad, miss);
 }
-// Q4_K: 144-byte GGUF superblock (d, dmin, 12 scale bytes, qs 128) ->
-// qs[blk][128] and hdr[blk][16] = d | dmin | scales.
-__global__ __launch_bounds__(WG) void k_q4k_repack(const uint8_t* __restrict__ src, int64_t blocks,
-                                                   int8_t* __restrict__ q, uint8_t* __restrict__ hdr) {
-    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
-    if (blk >= blocks) return;
-    const uint8_t* p = src + blk * 144;
-    uint8_t* dq = (uint8_t*)q + blk * 128;
-    for (int j = 0; j < 16; j++) hdr[blk * 16 + j] = p[j];
-    for (int j = 0; j < 128; j++) dq[j] = p[16 + j];
+// Q4_K: 144-byte GGUF superblock (d, dmin, 12 packed scale/min bytes, qs 128)
+// -> nibble plane, scm[blk][4 pairs][4] (scale 2j, scale 2j+1, min 2j, min
+// 2j+1 as bytes) and
+// dm[blk] = d | dmin. In the nibble plane byte b of unit u (32 bytes of qs,
+// u = 4 * superblock-in-row + pair) of row r sits at r*nu*32 + (b/16)*nu*16 +
+// u*16 + b%16 (nu units per row). The verify kernel packs everything back.
+__device__ __forceinline__ int64_t q4k_qoff(int64_t blk, int64_t spr, int j, int b) {
+    const int64_t row = blk / spr, nu = 4 * spr, u = 4 * (blk % spr) + j;
+    return row * nu * 32 + (b >> 4) * nu * 16 + u * 16 + (b & 15);
 }
-__global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q, const uint8_t* __restrict__ hdr,
-                                                   const uint8_t* __restrict__ src, int64_t blocks,
-                                                   unsigned* __restrict__ bad) {
+__global__ __launch_bounds__(WG) void k_q4k_repack(const uint8_t* __restrict__ src, int64_t blocks, int64_t spr,
+                                                   int8_t* __restrict__ q, uint8_t* __restrict__ scm,
+                                                   uint32_t* __restrict__ dm) {
     const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
     if (blk >= blocks) return;
     const uint8_t* p = src + blk * 144;
+    uint8_t* dq = (uint8_t*)q;
+    dm[blk] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+    for (int j = 0; j < 4; j++) {
+        int s0, m0, s1, m1;
+        Q4K::scale_min_k4(p + 4, 2 * j, s0, m0);
+        Q4K::scale_min_k4(p + 4, 2 * j + 1, s1, m1);
+        uint8_t* o = scm + blk * 16 + 4 * j;
+        o[0] = (uint8_t)s0;
+        o[1] = (uint8_t)s1;
+        o[2] = (uint8_t)m0;
+        o[3] = (uint8_t)m1;
+    }
+    for (int i = 0; i < 128; i++) dq[q4k_qoff(blk, spr, i >> 5, i & 31)] = p[16 + i];
+}
+__global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q, const uint8_t* __restrict__ scm,
+                                                   const uint32_t* __restrict__ dm, const uint8_t* __restrict__ src,
+                                                   int64_t blocks, int64_t spr, unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint8_t* p = src + blk * 144;
+    uint8_t sc[8], mn[8];
+    for (int k = 0; k < 8; k++) {
+        sc[k] = scm[blk * 16 + 4 * (k >> 1) + (k & 1)];
+        mn[k] = scm[blk * 16 + 4 * (k >> 1) + 2 + (k & 1)];
+    }
     unsigned miss = 0;
-    for (int j = 0; j < 16; j++) miss += hdr[blk * 16 + j] != p[j];
-    for (int j = 0; j < 128; j++) miss += (uint8_t)q[blk * 128 + j] != p[16 + j];
+    for (int i = 0; i < 4; i++) miss += (uint8_t)(dm[blk] >> (8 * i)) != p[i];
+    for (int k = 0; k < 8; k++) miss += (sc[k] > 63) + (mn[k] > 63);
+    for (int k = 0; k < 4; k++) {
+        miss += (uint8_t)(sc[k] | ((sc[k + 4] >> 4) << 6)) != p[4 + k];
+        miss += (uint8_t)(mn[k] | ((mn[k + 4] >> 4) << 6)) != p[8 + k];
+        miss += (uint8_t)((sc[k + 4] & 0xF) | ((mn[k + 4] & 0xF) << 4)) != p[12 + k];
+    }
+    for (int i = 0; i < 128; i++) miss += (uint8_t)q[q4k_qoff(blk, spr, i >> 5, i & 31)] != p[16 + i];
     if (miss) atomicAdd(bad, miss);
 }
 // Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, scales 12, d 2) ->
@@ -131,7 +161,6 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
     load_xr<KQ, LPR, NBL>(xr, xq, xs, nu, sub);
     for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
         const int64_t row = row0 + wave * RPW + grp;
-        // rows past the end load the last row; every lane takes part in the reductions
         const int64_t rr = row < rows ? row : rows - 1;
         typename KQ::W wv[NBL], wv2[NBL];
 #pragma unroll
@@ -174,12 +203,12 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
         const int4* xp = (const int4*)x;
         c = uq_dot32(p[0], p[1], xp[0], xp[1]);
     } else if (kind == KIND_Q4_K) {
-        const int64_t sb = (row * (K / 256)) + b / 8;
-        const int a = (int)(b % 8), j = a >> 1, h = a & 1;
-        const uint8_t* qs = (const uint8_t*)w.qs + sb * 128 + 32 * j;
+        const int64_t nu = K / 64, u = (b / 8) * 4 + ((b % 8) >> 1);
+        const int h = (int)(b & 1);
+        const uint8_t* qs = (const uint8_t*)w.qs + row * nu * 32 + u * 16;
         const int* xp = (const int*)x;
         for (int k = 0; k < 8; k++) {
-            const int wq = *(const int*)(qs + 4 * k);
+            const int wq = *(const int*)(qs + (k >> 2) * nu * 16 + 4 * (k & 3));
             c = uq_dot4(h ? Q4K::hi4(wq) : Q4K::lo4(wq), xp[k], c);
         }
     } else {
@@ -223,6 +252,9 @@ int launch_kind(const Weight& w, const Weight* w2, const int8_t* xq, const float
     const int64_t nu = w.n / KQ::UNIT;
 #define UQ_TRY(L, B) \
     if (nu <= (int64_t)(L) * (B)) { launch_t<KQ, L, B>(w, w2, xq, xs, y, s); return OK; }
+    // K-quant units hold 64-128 activation values in registers: prefer two
+    // units per lane (occupancy) over full lanes
+    if (KQ::UNIT >= 64) { UQ_TRY(16, 2) }
     UQ_TRY(4, 1) UQ_TRY(4, 2)
     UQ_TRY(8, 1) UQ_TRY(8, 2) UQ_TRY(8, 3)
     UQ_TRY(16, 2) UQ_TRY(16, 3) UQ_TRY(16, 4)
@@ -245,12 +277,13 @@ void launch_q8_verify(const int8_t* qs, const uint16_t* d, const uint8_t* gguf, 
                       unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q8_verify, dim3(grid_for(rows * nb, WG)), dim3(WG), 0, s, qs, d, gguf, rows, nb, bad);
 }
-void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* hdr, hipStream_t s) {
-    hipLaunchKernelGGL(k_q4k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, hdr);
-}
-void launch_q4k_verify(const int8_t* q, const uint8_t* hdr, const uint8_t* gguf, int64_t blocks, unsigned* bad,
+void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int64_t spr, int8_t* q, uint8_t* scm, uint32_t* dm,
                        hipStream_t s) {
-    hipLaunchKernelGGL(k_q4k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, hdr, gguf, blocks, bad);
+    hipLaunchKernelGGL(k_q4k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, spr, q, scm, dm);
+}
+void launch_q4k_verify(const int8_t* q, const uint8_t* scm, const uint32_t* dm, const uint8_t* gguf, int64_t blocks,
+                       int64_t spr, unsigned* bad, hipStream_t s) {
+    hipLaunchKernelGGL(k_q4k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, scm, dm, gguf, blocks, spr, bad);
 }
 void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, sc, d);

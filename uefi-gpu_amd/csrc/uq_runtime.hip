@@ -152,7 +152,8 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
         off_sc = align256(blocks * 128);
-        total = off_sc + align256(blocks * 16);
+        off_d = off_sc + align256(blocks * 16);
+        total = off_d + align256(blocks * 4);
     } else {
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
@@ -164,7 +165,7 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
     w.alloc_bytes = total;
     uint8_t* base = (uint8_t*)w.alloc;
     w.qs = (const int8_t*)(base + off_q);
-    if (kind != KIND_Q4_K) w.d = (const uint16_t*)(base + off_d);
+    w.d = (const uint16_t*)(base + off_d);
     if (kind != KIND_Q8_0) w.sc = base + off_sc;
     int rc = OK;
     {
@@ -178,8 +179,10 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
                 launch_q8_verify(w.qs, w.d, (const uint8_t*)staging, m, n / 32, g_ctx.dcount, s);
             } else if (kind == KIND_Q4_K) {
                 const int64_t blocks = n / 256 * m;
-                launch_q4k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, s);
-                launch_q4k_verify(w.qs, w.sc, (const uint8_t*)staging, blocks, g_ctx.dcount, s);
+                launch_q4k_repack((const uint8_t*)staging, blocks, n / 256, (int8_t*)w.qs, (uint8_t*)w.sc, (uint32_t*)w.d,
+                                  s);
+                launch_q4k_verify(w.qs, w.sc, (const uint32_t*)w.d, (const uint8_t*)staging, blocks, n / 256,
+                                  g_ctx.dcount, s);
             } else {
                 const int64_t blocks = n / 256 * m;
                 launch_q3k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, (uint16_t*)w.d, s);

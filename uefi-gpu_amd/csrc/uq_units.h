@@ -51,14 +51,17 @@ struct Q8 {
 
 // Q4_K unit: pair j of a superblock = 32 bytes of qs holding sub-blocks 2j (low
 // nibbles) and 2j+1 (high nibbles). ggml value = d*sc*q - dmin*m per sub-block.
-// Planes (repacked at upload, byte-verified): qs[sb][128] streamed with
-// non-temporal loads, so a row's lanes read contiguous 32-byte pieces, and
-// the 16-byte headers hdr[sb] = d | dmin | 12 scale bytes, read through the
-// cache (the four lanes of a superblock share one). The activation sums of a
-// unit (for the min term) are formed once when the activation is loaded.
+// Planes (repacked at upload, byte-verified): the nibble plane holds, per row,
+// the first 16 bytes of every unit and then their second 16 bytes, so each of
+// a unit's two non-temporal 16-byte loads is contiguous across the row's lanes;
+// scm[sb][4 pairs] = one word per unit: scale(2j) | scale(2j+1) << 8 |
+// min(2j) << 16 | min(2j+1) << 24 (the 6-bit fields unpacked to bytes);
+// dm[sb] = d | dmin (fp16 pair). scm and dm go through the cache (the
+// four lanes of a superblock share them). The activation scales and sums of a
+// unit (the sums feed the min term) are formed once when it is loaded.
 struct Q4K {
     static constexpr int UNIT = 64;
-    struct X { int4 a0, a1, b0, b1; float s0, s1; int xl, xh; };
+    struct X { int4 a0, a1, b0, b1; double s0, s1, xl, xh; };
     static UQ_DEV int sum16(const int4& v, int c) {
         const int ones = 0x01010101;
         c = uq_dot4(ones, v.x, c); c = uq_dot4(ones, v.y, c);
@@ -67,27 +70,27 @@ struct Q4K {
     static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
         const int4* p = (const int4*)(xq + (size_t)u * 64);
         x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
-        x.s0 = xs[2 * u];
-        x.s1 = xs[2 * u + 1];
-        x.xl = sum16(x.a1, sum16(x.a0, 0));
-        x.xh = sum16(x.b1, sum16(x.b0, 0));
+        x.s0 = (double)xs[2 * u];
+        x.s1 = (double)xs[2 * u + 1];
+        x.xl = (double)sum16(x.a1, sum16(x.a0, 0));
+        x.xh = (double)sum16(x.b1, sum16(x.b0, 0));
     }
     static UQ_DEV void zero_x(X& x) {
         x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
-        x.s0 = x.s1 = 0.0f;
-        x.xl = x.xh = 0;
+        x.s0 = x.s1 = x.xl = x.xh = 0.0;
     }
     static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
     static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
-    struct W { int4 q0, q1, hdr; };
+    struct W { int4 q0, q1; uint32_t scm, dm; };
     static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
         const int64_t sb = (row * nu + u) >> 2;  // nu = 4 * superblocks per row
-        const uint8_t* q = (const uint8_t*)w.qs + sb * 128 + 32 * (u & 3);
-        return W{uq_ntload16(q), uq_ntload16(q + 16), *(const int4*)(w.sc + sb * 16)};
-    }
-    static UQ_DEV double dot(const W& wv, const X& x, int u) {
         const int j = u & 3;
-        const int4 q0 = wv.q0, q1 = wv.q1, hdr = wv.hdr;
+        const uint8_t* q = (const uint8_t*)w.qs + row * nu * 32 + (int64_t)u * 16;
+        const uint32_t scm = ((const uint32_t*)w.sc)[4 * sb + j];
+        return W{uq_ntload16(q), uq_ntload16(q + nu * 16), scm, ((const uint32_t*)w.d)[sb]};
+    }
+    static UQ_DEV double dot(const W& wv, const X& x, int = 0) {
+        const int4 q0 = wv.q0, q1 = wv.q1;
         int il = 0, ih = 0;
         il = uq_dot4(lo4(q0.x), x.a0.x, il); il = uq_dot4(lo4(q0.y), x.a0.y, il);
         il = uq_dot4(lo4(q0.z), x.a0.z, il); il = uq_dot4(lo4(q0.w), x.a0.w, il);
@@ -97,42 +100,26 @@ struct Q4K {
         ih = uq_dot4(hi4(q0.z), x.b0.z, ih); ih = uq_dot4(hi4(q0.w), x.b0.w, ih);
         ih = uq_dot4(hi4(q1.x), x.b1.x, ih); ih = uq_dot4(hi4(q1.y), x.b1.y, ih);
         ih = uq_dot4(hi4(q1.z), x.b1.z, ih); ih = uq_dot4(hi4(q1.w), x.b1.w, ih);
-        // header: d (bytes 0-1), dmin (2-3), 12 scale bytes (4-15)
-        const float dd = uq_half((uint16_t)(hdr.x & 0xffff));
-        const float dm = uq_half((uint16_t)((unsigned)hdr.x >> 16));
-        int sc0, m0, sc1, m1;
-        scale_min_pair(j, (uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w, sc0, m0, sc1, m1);
-        const float d0 = dd * (float)sc0, n0 = dm * (float)m0;
-        const float d1 = dd * (float)sc1, n1 = dm * (float)m1;
-        const double t0 = (double)x.s0 * ((double)d0 * (double)il - (double)n0 * (double)x.xl);
-        const double t1 = (double)x.s1 * ((double)d1 * (double)ih - (double)n1 * (double)x.xh);
+        const float dd = uq_half((uint16_t)(wv.dm & 0xffff));
+        const float dm = uq_half((uint16_t)(wv.dm >> 16));
+        const float d0 = dd * (float)(wv.scm & 0xff), n0 = dm * (float)((wv.scm >> 16) & 0xff);
+        const float d1 = dd * (float)((wv.scm >> 8) & 0xff), n1 = dm * (float)(wv.scm >> 24);
+        const double t0 = x.s0 * ((double)d0 * (double)il - (double)n0 * x.xl);
+        const double t1 = x.s1 * ((double)d1 * (double)ih - (double)n1 * x.xh);
         return t0 + t1;
     }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
         return dot(load_w(w, row, nu, u), x, u);
     }
-    // ggml get_scale_min_k4 for sub-blocks 2j and 2j+1 (j = 0..3), branch-free.
-    // Scale bytes b0..b11 arrive as three little-endian words s0, s1, s2.
-    // Sub-block k < 4: sc = b[k] & 63, m = b[k+4] & 63; k >= 4: sc = (b[k+4]
-    // & 15) | (b[k-4] >> 6) << 4, m = (b[k+4] >> 4) | (b[k] >> 6) << 4.
-    static UQ_DEV int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
-    static UQ_DEV void scale_min_pair(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc0, int& m0, int& sc1,
-                                      int& m1) {
-        const int k0 = 2 * j & 3;                    // byte index within its word
-        // low form (j < 2): sub-blocks 2j, 2j+1 in word s0, mins in word s1
-        const int ls0 = byte_of(s0, k0) & 63, ls1 = byte_of(s0, k0 + 1) & 63;
-        const int lm0 = byte_of(s1, k0) & 63, lm1 = byte_of(s1, k0 + 1) & 63;
-        // high form (j >= 2): b[k+4] in s2, b[k-4] in s0, b[k] in s1
-        const int h0 = byte_of(s2, k0), h1 = byte_of(s2, k0 + 1);
-        const int hs0 = (h0 & 15) | ((byte_of(s0, k0) >> 6) << 4);
-        const int hs1 = (h1 & 15) | ((byte_of(s0, k0 + 1) >> 6) << 4);
-        const int hm0 = (h0 >> 4) | ((byte_of(s1, k0) >> 6) << 4);
-        const int hm1 = (h1 >> 4) | ((byte_of(s1, k0 + 1) >> 6) << 4);
-        const bool hi = j >= 2;
-        sc0 = hi ? hs0 : ls0;
-        m0 = hi ? hm0 : lm0;
-        sc1 = hi ? hs1 : ls1;
-        m1 = hi ? hm1 : lm1;
+    // ggml get_scale_min_k4: 12 packed bytes b -> scale and min of sub-block k
+    static UQ_DEV void scale_min_k4(const uint8_t* b, int k, int& sc, int& m) {
+        if (k < 4) {
+            sc = b[k] & 63;
+            m = b[k + 4] & 63;
+        } else {
+            sc = (b[k + 4] & 0xF) | ((b[k - 4] >> 6) << 4);
+            m = (b[k + 4] >> 4) | ((b[k] >> 6) << 4);
+        }
     }
 };
 

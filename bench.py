@@ -136,19 +136,21 @@ def prefill_gemm_bench(tokens=512, reps=20):
     return out
 
 
-def q4k_sweep(copies=3, reps=30):
-    """The same bs=1 sweep with Q4_K weights (144 B per 256 values); lm_head
-    alone timed over back-to-back launches."""
+def kquant_sweep(kind, copies=3, reps=30):
+    """The same bs=1 sweep with K-quant weights: Q4_K (144 B per 256 values)
+    or Q3_K (110 B per 256 values); lm_head alone timed over back-to-back
+    launches."""
+    bpsb = {uq.KIND_Q4_K: 144, uq.KIND_Q3_K: 110}[kind]
     weights, pairs, names = [], [], []
     for c in range(copies):
         for name, N, K, pair in SHAPES:
             for i in range(2 if pair else 1):
-                raw = uq.synth_quant(uq.KIND_Q4_K, 0x5EED0011 + c * 16 + i * 4 + N, N, K)
-                weights.append(uq.Weight(uq.KIND_Q4_K, K, N, raw))
+                raw = uq.synth_quant(kind, 0x5EED0011 + kind * 256 + c * 16 + i * 4 + N, N, K)
+                weights.append(uq.Weight(kind, K, N, raw))
                 pairs.append(1 if (pair and i == 0) else 0)
                 names.append(name)
-    q4 = lambda N, K: N * (K // 256) * 144 + K + (K // 32) * 4 + 4 * N
-    step_bytes = sum(q4(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else q4(N, K) for _, N, K, pair in SHAPES)
+    kb = lambda N, K: N * (K // 256) * bpsb + K + (K // 32) * 4 + 4 * N
+    step_bytes = sum(kb(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else kb(N, K) for _, N, K, pair in SHAPES)
     total_ms, _ = uq.time_matvecs(weights, pairs, 8960, reps, 3, -1)
     lm_ws = [w for w, n in zip(weights, names) if n == "lm_head"]
     lm_total, _ = uq.time_matvecs(lm_ws, [0] * len(lm_ws), 1536, reps, 3, -1)
@@ -156,8 +158,16 @@ def q4k_sweep(copies=3, reps=30):
     for w in weights:
         w.free()
     return {"GBs": round(step_bytes * reps * copies / (total_ms / 1e3) / 1e9, 1), "bytes_per_step": step_bytes,
-            "lm_head_GBs": round(q4(151936, 1536) / (lm_ms / 1e3) / 1e9, 1),
-            "lm_head_frac": round(q4(151936, 1536) / (lm_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "lm_head_GBs": round(kb(151936, 1536) / (lm_ms / 1e3) / 1e9, 1),
+            "lm_head_frac": round(kb(151936, 1536) / (lm_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def q4k_sweep():
+    return kquant_sweep(uq.KIND_Q4_K)
+
+
+def q3k_sweep():
+    return kquant_sweep(uq.KIND_Q3_K)
 
 
 def moe_bench(steps=64):
@@ -185,7 +195,7 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
-    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "moe"],
+    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe"],
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -195,7 +205,8 @@ def main():
 
     uq.init(0)
     if args.leg:
-        leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "q4k": q4k_sweep, "moe": moe_bench}[args.leg]
+        leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "q4k": q4k_sweep, "q3k": q3k_sweep,
+               "moe": moe_bench}[args.leg]
         print(json.dumps({args.leg: leg()}), flush=True)
         return
     weights, pairs, shape_of = [], [], []
@@ -248,6 +259,7 @@ def main():
         result["decode"] = decode_bench()
         result["prefill_gemm"] = prefill_gemm_bench()
         result["q4k_sweep"] = q4k_sweep()
+        result["q3k_sweep"] = q3k_sweep()
         result["moe"] = moe_bench()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline()

@@ -57,8 +57,8 @@ void launch_q4k_repack(const uint8_t* gguf, int64_t blocks, int64_t spr, int8_t*
                        hipStream_t s);
 void launch_q4k_verify(const int8_t* q, const uint8_t* scm, const uint32_t* dm, const uint8_t* gguf, int64_t blocks,
                        int64_t spr, unsigned* bad, hipStream_t s);
-void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s);
-void launch_q3k_verify(const int8_t* q, const uint8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
+void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, int8_t* sc, uint16_t* d, hipStream_t s);
+void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
                        unsigned* mismatches, hipStream_t s);
 // y[m] = W x for any kind; gate/up fusion writes silu(gate)*up when w2 != null.
 int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s);

@@ -7,7 +7,7 @@
 //  * weights are repacked once so every lane issues 16-byte global loads:
 //    Q8_0 -> int8 plane [rows][K] + fp16 scale plane; Q4_K -> 128-byte nibble
 //    plane + 16 unpacked scale/min bytes + d|dmin per superblock; Q3_K -> 96-byte quant
-//    plane + 12-byte scale plane + fp16 d plane. Each repack is checked by
+//    plane + 16 unpacked signed scale bytes + fp16 d plane. Each repack is checked by
 //    rebuilding the GGUF bytes on the device.
 //  * a row is owned by LPR consecutive lanes of a wave64; lane `sub` handles
 //    work units sub, sub+LPR, ... (Q8_0 unit = 16 values, Q4_K = 64, Q3_K = 128).
@@ -120,20 +120,21 @@ __global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q,
     for (int i = 0; i < 128; i++) miss += (uint8_t)q[q4k_qoff(blk, spr, i >> 5, i & 31)] != p[16 + i];
     if (miss) atomicAdd(bad, miss);
 }
-// Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, scales 12, d 2) ->
-// q[blk][96] = hmask|qs, sc[blk][12], d[blk].
+// Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, 12 packed scale bytes, d 2)
+// -> q[blk][96] = hmask|qs, sc[blk][16] = the sixteen 6-bit scales minus 32 as
+// signed bytes, d[blk]. The verify kernel packs the scales back to 12 bytes.
 __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
-                                                   int8_t* __restrict__ q, uint8_t* __restrict__ sc,
+                                                   int8_t* __restrict__ q, int8_t* __restrict__ sc,
                                                    uint16_t* __restrict__ d) {
     const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
     if (blk >= blocks) return;
     const uint8_t* p = src + blk * 110;
     uint8_t* dq = (uint8_t*)q + blk * 96;
     for (int j = 0; j < 96; j++) dq[j] = p[j];
-    for (int j = 0; j < 12; j++) sc[blk * 12 + j] = p[96 + j];
+    for (int k = 0; k < 16; k++) sc[blk * 16 + k] = (int8_t)(Q3K::scale6_k(p + 96, k) - 32);
     d[blk] = (uint16_t)(p[108] | (p[109] << 8));
 }
-__global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const uint8_t* __restrict__ sc,
+__global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const int8_t* __restrict__ sc,
                                                    const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
                                                    int64_t blocks, unsigned* __restrict__ bad) {
     const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
@@ -141,7 +142,17 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
     const uint8_t* p = src + blk * 110;
     unsigned miss = 0;
     for (int j = 0; j < 96; j++) miss += (uint8_t)q[blk * 96 + j] != p[j];
-    for (int j = 0; j < 12; j++) miss += sc[blk * 12 + j] != p[96 + j];
+    int v[16];
+    for (int k = 0; k < 16; k++) {
+        v[k] = sc[blk * 16 + k] + 32;
+        miss += v[k] < 0 || v[k] > 63;
+    }
+    for (int k = 0; k < 8; k++) miss += (uint8_t)((v[k] & 0xF) | ((v[k + 8] & 0xF) << 4)) != p[96 + k];
+    for (int m = 0; m < 4; m++) {
+        int b = 0;
+        for (int g = 0; g < 4; g++) b |= ((v[4 * g + m] >> 4) & 3) << (2 * g);
+        miss += (uint8_t)b != p[104 + m];
+    }
     miss += (uint8_t)(d[blk] & 0xff) != p[108];
     miss += (uint8_t)(d[blk] >> 8) != p[109];
     if (miss) atomicAdd(bad, miss);
@@ -161,6 +172,7 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
     load_xr<KQ, LPR, NBL>(xr, xq, xs, nu, sub);
     for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
         const int64_t row = row0 + wave * RPW + grp;
+        // rows past the end load the last row; every lane takes part in the reductions
         const int64_t rr = row < rows ? row : rows - 1;
         typename KQ::W wv[NBL], wv2[NBL];
 #pragma unroll
@@ -177,6 +189,62 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
             acc += u < nu ? t : 0.0;
             if (GATEUP) {
                 const double t2 = KQ::dot(wv2[i], xr[i], uc);
+                acc2 += u < nu ? t2 : 0.0;
+            }
+        }
+        acc = uq_group_sum<LPR>(acc);
+        if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
+        if (row < rows && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+    }
+}
+
+// K-quant variant: units carry 64-128 activation values, too many to keep in
+// registers across rows, so the workgroup stages the quantized activation,
+// its scales and its 16-value sums in LDS once and each unit reads its slice
+// from LDS right before its dot. K <= MAX_XL.
+constexpr int MAX_XL = 16384;
+template <class KQ, int LPR, int NBL, bool GATEUP>
+__global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
+                                                  const float* __restrict__ xs, float* __restrict__ y,
+                                                  int64_t rows, int64_t K) {
+    __shared__ __attribute__((aligned(16))) int8_t lx[MAX_XL];
+    __shared__ float lxs[MAX_XL / 32];
+    __shared__ int ls16[MAX_XL / 16];
+    constexpr int RPW = 64 / LPR;
+    constexpr int RPB = RPW * (WG / 64);
+    const int64_t nu = K / KQ::UNIT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    for (int g = threadIdx.x; g < K / 16; g += WG) {
+        const int4 v = ((const int4*)xq)[g];
+        ((int4*)lx)[g] = v;
+        const int ones = 0x01010101;
+        int c = uq_dot4(ones, v.x, 0);
+        c = uq_dot4(ones, v.y, c);
+        c = uq_dot4(ones, v.z, c);
+        ls16[g] = uq_dot4(ones, v.w, c);
+    }
+    for (int b = threadIdx.x; b < K / 32; b += WG) lxs[b] = xs[b];
+    __syncthreads();
+    for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
+        const int64_t row = row0 + wave * RPW + grp;
+        const int64_t rr = row < rows ? row : rows - 1;
+        typename KQ::W wv[NBL], wv2[NBL];
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = KQ::load_w(w, rr, nu, uc);
+            if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
+        }
+        double acc = 0.0, acc2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            asm volatile("" ::: "memory");  // one unit's activation reads at a time
+            const double t = KQ::dot_lds(wv[i], lx, lxs, ls16, uc);
+            acc += u < nu ? t : 0.0;
+            if (GATEUP) {
+                const double t2 = KQ::dot_lds(wv2[i], lx, lxs, ls16, uc);
                 acc2 += u < nu ? t2 : 0.0;
             }
         }
@@ -231,17 +299,19 @@ inline unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)((items + per_block - 1) / per_block);
 }
 
-template <class KQ, int LPR, int NBL>
+template <class KQ, int LPR, int NBL, bool XL = false>
 void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
     constexpr int RPB = (64 / LPR) * (WG / 64);
     int64_t sets = (w.m + RPB - 1) / RPB;
     const unsigned grid = (unsigned)(sets < 2048 ? sets : 2048);
     WArgs a{w.qs, w.d, w.sc}, b{nullptr, nullptr, nullptr};
-    if (w2) {
-        b = WArgs{w2->qs, w2->d, w2->sc};
-        hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+    if (w2) b = WArgs{w2->qs, w2->d, w2->sc};
+    if constexpr (XL) {
+        if (w2) hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+        else hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
     } else {
-        hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+        if (w2) hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+        else hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
     }
 }
 
@@ -252,9 +322,17 @@ int launch_kind(const Weight& w, const Weight* w2, const int8_t* xq, const float
     const int64_t nu = w.n / KQ::UNIT;
 #define UQ_TRY(L, B) \
     if (nu <= (int64_t)(L) * (B)) { launch_t<KQ, L, B>(w, w2, xq, xs, y, s); return OK; }
-    // K-quant units hold 64-128 activation values in registers: prefer two
-    // units per lane (occupancy) over full lanes
-    if (KQ::UNIT >= 64) { UQ_TRY(16, 2) }
+    // K-quants: activation staged in LDS, lane groups sized to fit the row
+#define UQ_TRYX(L, B) \
+    if (nu <= (int64_t)(L) * (B)) { launch_t<KQ, L, B, true>(w, w2, xq, xs, y, s); return OK; }
+    if constexpr (KQ::UNIT >= 64) {
+        if (w.n <= MAX_XL) {
+            if (KQ::UNIT >= 128) { UQ_TRYX(16, 1) }
+            UQ_TRYX(4, 1) UQ_TRYX(4, 2) UQ_TRYX(4, 3) UQ_TRYX(8, 3) UQ_TRYX(16, 3) UQ_TRYX(32, 3) UQ_TRYX(64, 3)
+            UQ_TRYX(64, 4) UQ_TRYX(64, 6) UQ_TRYX(64, 8)
+        }
+    }
+#undef UQ_TRYX
     UQ_TRY(4, 1) UQ_TRY(4, 2)
     UQ_TRY(8, 1) UQ_TRY(8, 2) UQ_TRY(8, 3)
     UQ_TRY(16, 2) UQ_TRY(16, 3) UQ_TRY(16, 4)
@@ -285,10 +363,10 @@ void launch_q4k_verify(const int8_t* q, const uint8_t* scm, const uint32_t* dm, 
                        int64_t spr, unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q4k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, scm, dm, gguf, blocks, spr, bad);
 }
-void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, uint8_t* sc, uint16_t* d, hipStream_t s) {
+void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, int8_t* sc, uint16_t* d, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, q, sc, d);
 }
-void launch_q3k_verify(const int8_t* q, const uint8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
+void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
                        unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, sc, d, gguf, blocks, bad);
 }

@@ -158,7 +158,7 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
         off_sc = align256(blocks * 96);
-        off_d = off_sc + align256(blocks * 12);
+        off_d = off_sc + align256(blocks * 16);
         total = off_d + align256(blocks * 2);
     }
     UQ_CHECK_HIP(hipMalloc(&w.alloc, total));
@@ -185,8 +185,8 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
                                   g_ctx.dcount, s);
             } else {
                 const int64_t blocks = n / 256 * m;
-                launch_q3k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (uint8_t*)w.sc, (uint16_t*)w.d, s);
-                launch_q3k_verify(w.qs, w.sc, w.d, (const uint8_t*)staging, blocks, g_ctx.dcount, s);
+                launch_q3k_repack((const uint8_t*)staging, blocks, (int8_t*)w.qs, (int8_t*)w.sc, (uint16_t*)w.d, s);
+                launch_q3k_verify(w.qs, (const int8_t*)w.sc, w.d, (const uint8_t*)staging, blocks, g_ctx.dcount, s);
             }
             e = hipGetLastError();
         }

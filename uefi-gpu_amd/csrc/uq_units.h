@@ -61,7 +61,7 @@ struct Q8 {
 // unit (the sums feed the min term) are formed once when it is loaded.
 struct Q4K {
     static constexpr int UNIT = 64;
-    struct X { int4 a0, a1, b0, b1; double s0, s1, xl, xh; };
+    struct X { int4 a0, a1, b0, b1; double s0, s1; int xl, xh; };
     static UQ_DEV int sum16(const int4& v, int c) {
         const int ones = 0x01010101;
         c = uq_dot4(ones, v.x, c); c = uq_dot4(ones, v.y, c);
@@ -72,12 +72,22 @@ struct Q4K {
         x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
         x.s0 = (double)xs[2 * u];
         x.s1 = (double)xs[2 * u + 1];
-        x.xl = (double)sum16(x.a1, sum16(x.a0, 0));
-        x.xh = (double)sum16(x.b1, sum16(x.b0, 0));
+        x.xl = sum16(x.a1, sum16(x.a0, 0));
+        x.xh = sum16(x.b1, sum16(x.b0, 0));
     }
     static UQ_DEV void zero_x(X& x) {
         x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
-        x.s0 = x.s1 = x.xl = x.xh = 0.0;
+        x.s0 = x.s1 = 0.0;
+        x.xl = x.xh = 0;
+    }
+    // from an activation staged with its 16-value sums s16 (LDS)
+    static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 64);
+        x.a0 = p[0]; x.a1 = p[1]; x.b0 = p[2]; x.b1 = p[3];
+        x.s0 = (double)xs[2 * u];
+        x.s1 = (double)xs[2 * u + 1];
+        x.xl = s16[4 * u] + s16[4 * u + 1];
+        x.xh = s16[4 * u + 2] + s16[4 * u + 3];
     }
     static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
     static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
@@ -100,16 +110,24 @@ struct Q4K {
         ih = uq_dot4(hi4(q0.z), x.b0.z, ih); ih = uq_dot4(hi4(q0.w), x.b0.w, ih);
         ih = uq_dot4(hi4(q1.x), x.b1.x, ih); ih = uq_dot4(hi4(q1.y), x.b1.y, ih);
         ih = uq_dot4(hi4(q1.z), x.b1.z, ih); ih = uq_dot4(hi4(q1.w), x.b1.w, ih);
-        const float dd = uq_half((uint16_t)(wv.dm & 0xffff));
-        const float dm = uq_half((uint16_t)(wv.dm >> 16));
-        const float d0 = dd * (float)(wv.scm & 0xff), n0 = dm * (float)((wv.scm >> 16) & 0xff);
-        const float d1 = dd * (float)((wv.scm >> 8) & 0xff), n1 = dm * (float)(wv.scm >> 24);
-        const double t0 = x.s0 * ((double)d0 * (double)il - (double)n0 * x.xl);
-        const double t1 = x.s1 * ((double)d1 * (double)ih - (double)n1 * x.xh);
+        // d*sc and dmin*m are exact in f32 (11-bit x 6-bit), so (d*sc)*isum ==
+        // d*(sc*isum) with an exact integer inner product; same for the min term
+        const double dd = (double)uq_half((uint16_t)(wv.dm & 0xffff));
+        const double dm = (double)uq_half((uint16_t)(wv.dm >> 16));
+        const int sc0 = (int)(wv.scm & 0xff), sc1 = (int)((wv.scm >> 8) & 0xff);
+        const int m0 = (int)((wv.scm >> 16) & 0xff), m1 = (int)(wv.scm >> 24);
+        const double t0 = x.s0 * (dd * (double)(sc0 * il) - dm * (double)(m0 * x.xl));
+        const double t1 = x.s1 * (dd * (double)(sc1 * ih) - dm * (double)(m1 * x.xh));
         return t0 + t1;
     }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
         return dot(load_w(w, row, nu, u), x, u);
+    }
+    // dot against an activation staged in LDS with its 16-value sums
+    static UQ_DEV double dot_lds(const W& wv, const int8_t* lx, const float* lxs, const int* ls16, int u) {
+        X x;
+        load_x_pre(x, lx, lxs, ls16, u);
+        return dot(wv, x, u);
     }
     // ggml get_scale_min_k4: 12 packed bytes b -> scale and min of sub-block k
     static UQ_DEV void scale_min_k4(const uint8_t* b, int k, int& sc, int& m) {
@@ -125,79 +143,116 @@ struct Q4K {
 
 // Q3_K unit: half n of a superblock = 128 values = 4 activation blocks j.
 // Block j's 32 values use qs[32n .. 32n+31] bits 2j..2j+1 and hmask[0..31]
-// bit 4n+j; value = low2 - 4*(1-hbit); sub-blocks of 16 carry 6-bit scales.
+// bit 4n+j; value = low2 - 4*(1-hbit) = (low2 | hbit << 2) - 4; each 16
+// values carry a 6-bit scale s (factor s - 32). Planes (repacked at upload,
+// byte-verified): q[sb][96] = hmask | qs (non-temporal loads), sc[sb][16] =
+// the sixteen (s - 32) as signed bytes, d[sb] fp16. The activation scales and
+// the sums of each 16 activations (for the -4 offset) are formed once at load.
 struct Q3K {
     static constexpr int UNIT = 128;
-    struct X { int4 v[8]; float s[4]; };
+    struct X { int4 v[8]; double s[4]; int sx[8]; };
+    static UQ_DEV int dot16(const int4& w, const int4& xv, int c) {
+        c = uq_dot4(w.x, xv.x, c); c = uq_dot4(w.y, xv.y, c);
+        c = uq_dot4(w.z, xv.z, c); return uq_dot4(w.w, xv.w, c);
+    }
     static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
         const int4* p = (const int4*)(xq + (size_t)u * 128);
 #pragma unroll
         for (int k = 0; k < 8; k++) x.v[k] = p[k];
 #pragma unroll
-        for (int k = 0; k < 4; k++) x.s[k] = xs[4 * u + k];
+        for (int k = 0; k < 4; k++) x.s[k] = (double)xs[4 * u + k];
+        const int ones = 0x01010101;
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.sx[k] = dot16(make_int4(ones, ones, ones, ones), x.v[k], 0);
     }
     static UQ_DEV void zero_x(X& x) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) x.v[k] = make_int4(0, 0, 0, 0);
+        for (int k = 0; k < 8; k++) { x.v[k] = make_int4(0, 0, 0, 0); x.sx[k] = 0; }
 #pragma unroll
-        for (int k = 0; k < 4; k++) x.s[k] = 0.0f;
+        for (int k = 0; k < 4; k++) x.s[k] = 0.0;
     }
-    static UQ_DEV int dot16(const int4& w, const int4& xv, int c) {
-        c = uq_dot4(w.x, xv.x, c); c = uq_dot4(w.y, xv.y, c);
-        c = uq_dot4(w.z, xv.z, c); return uq_dot4(w.w, xv.w, c);
+    static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
+        const int4* p = (const int4*)(xq + (size_t)u * 128);
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.v[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.s[k] = (double)xs[4 * u + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) x.sx[k] = s16[8 * u + k];
     }
-    static UQ_DEV int4 extract(const int4& q, const int4& h, int shift, int hshift) {
-        int4 r;
-        r.x = (int)((((unsigned)q.x >> shift) & 0x03030303u) | ((((unsigned)h.x >> hshift) & 0x01010101u) << 2));
-        r.y = (int)((((unsigned)q.y >> shift) & 0x03030303u) | ((((unsigned)h.y >> hshift) & 0x01010101u) << 2));
-        r.z = (int)((((unsigned)q.z >> shift) & 0x03030303u) | ((((unsigned)h.z >> hshift) & 0x01010101u) << 2));
-        r.w = (int)((((unsigned)q.w >> shift) & 0x03030303u) | ((((unsigned)h.w >> hshift) & 0x01010101u) << 2));
-        return r;
+    // low2 (bits 2j..2j+1 of each q byte) | hbit (bit 4n+j of each h byte) << 2:
+    // the h word is rotated so the bit lands on bit 2 of its byte
+    static UQ_DEV int v3(uint32_t q, uint32_t h, int sq, int rot) {
+        const uint32_t hb = __builtin_amdgcn_alignbit(h, h, rot) & 0x04040404u;
+        return (int)(((q >> sq) & 0x03030303u) | hb);
     }
-    // 6-bit scale s = 8n + k (k < 8) from the 12 packed bytes held as
-    // lo = bytes 0..7 and s2 = bytes 8..11 (ggml Q3_K scale packing).
-    static UQ_DEV int scale6(uint64_t lo, uint32_t s2, int n, int k) {
-        const int low = (int)((lo >> (8 * k + 4 * n)) & 0xF);
-        const int high = (int)((s2 >> (8 * (k & 3) + 2 * (2 * n + (k >> 2)))) & 3u);
-        return low | (high << 4);
+    static UQ_DEV int4 extract(const int4& q, const int4& h, int sq, int rot) {
+        return make_int4(v3((uint32_t)q.x, (uint32_t)h.x, sq, rot), v3((uint32_t)q.y, (uint32_t)h.y, sq, rot),
+                         v3((uint32_t)q.z, (uint32_t)h.z, sq, rot), v3((uint32_t)q.w, (uint32_t)h.w, sq, rot));
     }
-    struct W { int4 h0, h1, q0, q1; uint32_t s0, s1, s2; uint16_t d; };
+    struct W { int4 h0, h1, q0, q1; uint32_t sc0, sc1; uint16_t d; };
     static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
         const int64_t sb = (row * nu + u) >> 1;  // nu = 2 * superblocks per row
+        const int n = u & 1;
         const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
-        const uint8_t* q = blk + 32 + 32 * (u & 1);
-        const uint32_t* sp = (const uint32_t*)(w.sc + sb * 12);
-        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sp[0], sp[1], sp[2],
-                 w.d[sb]};
+        const uint8_t* q = blk + 32 + 32 * n;
+        const uint2 sc = *(const uint2*)(w.sc + sb * 16 + 8 * n);
+        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sc.x, sc.y, w.d[sb]};
     }
+    // d*(s-32) is exact in f32 (11-bit x 6-bit), so the block's
+    // (d*s0)*i0 + (d*s1)*i1 equals d*(s0*i0 + s1*i1) with an exact integer sum
     static UQ_DEV double dot(const W& wv, const X& x, int u) {
         const int n = u & 1;
-        const uint64_t slo = (uint64_t)wv.s0 | ((uint64_t)wv.s1 << 32);
-        const uint32_t s2 = wv.s2;
-        const float dd = uq_half(wv.d);
+        const double dd = (double)uq_half(wv.d);
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, 4 * n + j), w1 = extract(wv.q1, wv.h1, 2 * j, 4 * n + j);
-            const int4 xa = x.v[2 * j], xb = x.v[2 * j + 1];
-            const int ones = 0x01010101;
-            int i0 = dot16(w0, xa, 0), i1 = dot16(w1, xb, 0);
-            const int s0x = dot16(make_int4(ones, ones, ones, ones), xa, 0);
-            const int s1x = dot16(make_int4(ones, ones, ones, ones), xb, 0);
-            i0 -= 4 * s0x;
-            i1 -= 4 * s1x;
-            const float dl0 = dd * (float)(scale6(slo, s2, n, 2 * j) - 32);
-            const float dl1 = dd * (float)(scale6(slo, s2, n, 2 * j + 1) - 32);
-            const double inner = (double)dl0 * (double)i0 + (double)dl1 * (double)i1;
-            acc += (double)x.s[j] * inner;
+            const int rot = (4 * n + j - 2) & 31;
+            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, rot), w1 = extract(wv.q1, wv.h1, 2 * j, rot);
+            const int i0 = dot16(w0, x.v[2 * j], 0) - 4 * x.sx[2 * j];
+            const int i1 = dot16(w1, x.v[2 * j + 1], 0) - 4 * x.sx[2 * j + 1];
+            const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
+            const int b = 16 * (j & 1);
+            const int t = (int)(int8_t)(scw >> b) * i0 + (int)(int8_t)(scw >> (b + 8)) * i1;
+            acc += x.s[j] * (dd * (double)t);
         }
         return acc;
     }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
         return dot(load_w(w, row, nu, u), x, u);
     }
+    // dot against an activation staged in LDS with its 16-value sums; block j's
+    // 32 activations are read just before they are used (a compiler barrier
+    // keeps the four blocks' reads from being hoisted together)
+    static UQ_DEV double dot_lds(const W& wv, const int8_t* lx, const float* lxs, const int* ls16, int u) {
+        const int n = u & 1;
+        const double dd = (double)uq_half(wv.d);
+        const int4* xv = (const int4*)(lx + (size_t)u * 128);
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            asm volatile("" ::: "memory");
+            const int4 xa = xv[2 * j], xb = xv[2 * j + 1];
+            const int sa = ls16[8 * u + 2 * j], sb = ls16[8 * u + 2 * j + 1];
+            const double xsj = (double)lxs[4 * u + j];
+            const int rot = (4 * n + j - 2) & 31;
+            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, rot), w1 = extract(wv.q1, wv.h1, 2 * j, rot);
+            const int i0 = dot16(w0, xa, 0) - 4 * sa;
+            const int i1 = dot16(w1, xb, 0) - 4 * sb;
+            const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
+            const int b = 16 * (j & 1);
+            const int t = (int)(int8_t)(scw >> b) * i0 + (int)(int8_t)(scw >> (b + 8)) * i1;
+            acc += xsj * (dd * (double)t);
+        }
+        return acc;
+    }
+    // ggml Q3_K 6-bit scale k (0..15) of the 12 packed bytes b
+    static UQ_DEV int scale6_k(const uint8_t* b, int k) {
+        const int low = k < 8 ? (b[k] & 0xF) : (b[k - 8] >> 4);
+        const int high = (b[8 + (k & 3)] >> (2 * (k >> 2))) & 3;
+        return low | (high << 4);
+    }
 };
-
 
 // Activation units of one lane (units sub, sub+LPR, ...) kept in registers.
 // Loads are issued unconditionally (a unit past the row end reads the last

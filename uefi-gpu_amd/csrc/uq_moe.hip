@@ -48,157 +48,305 @@ struct MoeDev {
     int D, F, E, top_k;
 };
 
-// ------------------------------------------------------------------ routing + input quant
-__global__ __launch_bounds__(256) void k_moe_route(MoeDev a) {
-    __shared__ float p[MAX_EXPERTS];
-    __shared__ double red[4];
-    __shared__ float redf[4];
-    __shared__ float sum_s;
-    const int t = threadIdx.x, E = a.E, D = a.D;
-    unsigned bad = 0;
-    // softmax: max, exp, f32 running sum in expert order (frontier_forward.rs:47-51)
-    float mx = -__builtin_inff();
-    for (int e = t; e < E; e += 256) {
-        const float l = a.logits[e];
-        bad |= !isfinite(l);
-        mx = fmaxf(mx, l);
-    }
-    mx = block_max_f<256>(mx, redf);
-    for (int e = t; e < E; e += 256) p[e] = uq_expf(a.logits[e] - mx);
-    __syncthreads();
-    if (t == 0) {
-        float s = 0.0f;
-        for (int e = 0; e < E; e++) s = s + p[e];
-        sum_s = s;
-    }
-    __syncthreads();
-    const float sum = sum_s;
-    for (int e = t; e < E; e += 256) p[e] = p[e] / sum;
-    __syncthreads();
-    // stable top-k: rank = number of experts ordered before e
-    for (int e = t; e < E; e += 256) {
-        const float pe = p[e];
-        int rank = 0;
-        for (int j = 0; j < E; j++) rank += (p[j] > pe) || (p[j] == pe && j < e);
-        if (rank < a.top_k) a.ids[rank] = e;
-    }
-    __syncthreads();
-    // input quant (per 32) and the shared-expert gate dot in double
-    double dot = 0.0;
-    for (int i = t; i < D; i += 256) {
-        const float v = a.x[i];
-        bad |= !isfinite(v);
-        if (a.sh_gate) dot = __builtin_fma((double)a.sh_gate[i], (double)v, dot);
-        float s;
-        const int8_t q = uq_quant_lane(v, &s);
-        a.xq[i] = q;
-        if ((t & 31) == 0) a.xs[i >> 5] = s;
-    }
-    dot = block_sum_d<256>(dot, red);
-    bad = __syncthreads_or(bad);
-    if (t == 0) {
-        float tot = 0.0f;
-        for (int k = 0; k < a.top_k; k++) tot = tot + p[a.ids[k]];
-        if (!(sum > 0.0f) || !isfinite(sum) || !(tot > 0.0f)) bad = 1;
-        for (int k = 0; k < a.top_k; k++) a.wts[k] = p[a.ids[k]] / tot;
-        a.wts[a.top_k] = a.sh_gate ? uq_sigmoid((float)dot) : 1.0f;
-        a.status[0] = bad;
-    }
-}
+// ------------------------------------------------------------------ routing + gate/up
+// One launch does routing, input quant and the gate/up projections. Every
+// 512-thread workgroup owns 32 consecutive rows of one expert slot's gate and
+// up matrices (16 lanes per row); slot < top_k is the routed expert of that
+// rank, slot == top_k the shared expert. Each workgroup recomputes the routing
+// (128 scores from 512 bytes of logits: cheaper than a dependent launch) and
+// quantizes x into LDS; workgroup (0, 0) publishes ids, weights and the
+// status flag, workgroup (top_k, 0) the shared expert's sigmoid gate. The
+// shared slot's weight loads are issued before the routing work.
+constexpr int GU_WG = 512;
+constexpr int GU_PE = (MAX_EXPERTS + GU_WG - 1) / GU_WG, GU_C = 4;
 
-// ------------------------------------------------------------------ gate/up + SiLU + quant
-// 512 threads = 32 consecutive rows of one expert's gate and up projections
-// (16 lanes per row); slot < top_k is routed expert ids[slot], slot == top_k
-// the shared expert. Output quantized per 32 into midq/mids[slot].
-template <class KQ, int NBL>
-__device__ void gateup_rows(const MoeDev& a, WArgs wg, WArgs wu, int64_t row_base, int rb, int slot, float* ys) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
-    const int64_t nu = a.D / KQ::UNIT;
-    const int64_t row = row_base + rb * 32 + wave * 4 + grp;
-    typename KQ::X xr[NBL];
-    load_xr<KQ, 16, NBL>(xr, a.xq, a.xs, nu, sub);
-    double g = 0.0, u = 0.0;
+struct RouteLds {
+    float p[MAX_EXPERTS];
+    int sid[MAX_TOPK];
+    double red[GU_WG / 64];
+    float redf[GU_WG / 64];
+    float sum;
+    unsigned bad;
+};
+
+// softmax (f32 running sum in expert order, frontier_forward.rs:47-51) and
+// stable top-k (score descending, id ascending) into L.sid; returns the sum.
+__device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& bad) {
+    const int t = threadIdx.x, E = a.E;
+    float mx = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < NBL; i++) {
-        const int un = sub + 16 * i;
-        if (un < nu) {
-            g += KQ::term(wg, row, nu, un, xr[i]);
-            u += KQ::term(wu, row, nu, un, xr[i]);
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        if (e < E) {
+            bad |= !isfinite(lg[j]);
+            mx = fmaxf(mx, lg[j]);
         }
     }
-    g = uq_group_sum<16>(g);
-    u = uq_group_sum<16>(u);
-    if (sub == 0) {
+    mx = block_max_f<GU_WG>(mx, L.redf);
+#pragma unroll
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        if (e < E) L.p[e] = uq_expf(lg[j] - mx);
+    }
+    // entries past E hold -1: never above a score, never equal to one
+    const int E4 = (E + 3) & ~3;
+    if (t < E4 - E) L.p[E + t] = -1.0f;
+    // with a NaN score no rank is unique; the slots then keep ids 0..k-1 and
+    // the status flag reports the input
+    if (t < a.top_k) L.sid[t] = t;
+    __syncthreads();
+    if (t == 0) {
+        const float4* p4 = (const float4*)L.p;
+        float s = 0.0f;
+        for (int q = 0; q < E / 4; q++) {
+            const float4 v = p4[q];
+            s = s + v.x;
+            s = s + v.y;
+            s = s + v.z;
+            s = s + v.w;
+        }
+        for (int e = E & ~3; e < E; e++) s = s + L.p[e];
+        L.sum = s;
+    }
+    __syncthreads();
+    const float sum = L.sum;
+    float pe[GU_PE];
+#pragma unroll
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        pe[j] = e < E ? L.p[e] / sum : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        if (e < E) L.p[e] = pe[j];
+    }
+    __syncthreads();
+    const float4* p4 = (const float4*)L.p;
+#pragma unroll
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        if (e < E) {
+            const float v = pe[j];
+            int rank = 0;
+            // bitwise (not short-circuit) tests keep the loop branch-free
+#pragma unroll 4
+            for (int q = 0; q < E4 / 4; q++) {
+                const float4 w = p4[q];
+                const int i0 = 4 * q;
+                rank += (int)(w.x > v) | ((int)(w.x == v) & (int)(i0 < e));
+                rank += (int)(w.y > v) | ((int)(w.y == v) & (int)(i0 + 1 < e));
+                rank += (int)(w.z > v) | ((int)(w.z == v) & (int)(i0 + 2 < e));
+                rank += (int)(w.w > v) | ((int)(w.w == v) & (int)(i0 + 3 < e));
+            }
+            if (rank < a.top_k) L.sid[rank] = e;
+        }
+    }
+    __syncthreads();
+    return sum;
+}
+
+// this lane's gate/up units of row `row`: loads, then dots (16 lanes per row)
+template <class KQ, int NBL>
+struct GuLane {
+    typename KQ::W gw[NBL], uw[NBL];
+    __device__ void load(WArgs wg, WArgs wu, int64_t row, int64_t nu, int sub) {
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int un = sub + 16 * i, uc = un < nu ? un : (int)nu - 1;
+            gw[i] = KQ::load_w(wg, row, nu, uc);
+            uw[i] = KQ::load_w(wu, row, nu, uc);
+        }
+    }
+    __device__ float silu_mul(const int8_t* xq, const float* xs, int64_t nu, int sub) const {
+        typename KQ::X xr[NBL];
+        load_xr<KQ, 16, NBL>(xr, xq, xs, nu, sub);
+        double g = 0.0, u = 0.0;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int un = sub + 16 * i, uc = un < nu ? un : (int)nu - 1;
+            const double tg = KQ::dot(gw[i], xr[i], uc), tu = KQ::dot(uw[i], xr[i], uc);
+            g += un < nu ? tg : 0.0;
+            u += un < nu ? tu : 0.0;
+        }
+        g = uq_group_sum<16>(g);
+        u = uq_group_sum<16>(u);
         const float gf = (float)g, uf = (float)u;
         const float sg = gf * uq_sigmoid(gf);
-        ys[wave * 4 + grp] = sg * uf;
+        return sg * uf;
+    }
+};
+
+template <class KR, int NR, class KS, int NS>
+__global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs ru, WArgs sg, WArgs su) {
+    __shared__ RouteLds L;
+    __shared__ __attribute__((aligned(16))) int8_t lxq[MAX_D];
+    __shared__ float lxs[MAX_D / 32];
+    __shared__ float ys[32];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
+    const int blocks = a.F / 32;
+    const int slot = blockIdx.x / blocks, rb = blockIdx.x % blocks;
+    const bool shared = slot == a.top_k;
+    const int D = a.D;
+    // global inputs up front
+    float lg[GU_PE], xv[GU_C];
+#pragma unroll
+    for (int j = 0; j < GU_PE; j++) {
+        const int e = j * GU_WG + t;
+        lg[j] = e < a.E ? a.logits[e] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < GU_C; j++) {
+        const int i = j * GU_WG + t;
+        xv[j] = i < D ? a.x[i] : 0.0f;
+    }
+    GuLane<KS, NS> sl;
+    const int64_t srow = (int64_t)rb * 32 + wave * 4 + grp;
+    if (shared) sl.load(sg, su, srow, D / KS::UNIT, sub);
+    unsigned bad = 0;
+    const float sum = route(a, lg, L, bad);
+    // input quant (per 32) into LDS, GU_C elements per thread per pass
+    for (int base = 0; base < D; base += GU_C * GU_WG) {
+        if (base > 0) {
+#pragma unroll
+            for (int j = 0; j < GU_C; j++) {
+                const int i = base + j * GU_WG + t;
+                xv[j] = i < D ? a.x[i] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < GU_C; j++) {
+            const int i = base + j * GU_WG + t;
+            if (i < D) {
+                bad |= !isfinite(xv[j]);
+                float sc;
+                const int8_t q = uq_quant_lane(xv[j], &sc);
+                lxq[i] = q;
+                if ((t & 31) == 0) lxs[i >> 5] = sc;
+            }
+        }
+    }
+    bad = __syncthreads_or(bad);  // also publishes lxq/lxs
+    if (blockIdx.x == 0 && t == 0) {
+        float tot = 0.0f;
+        for (int k = 0; k < a.top_k; k++) tot = tot + L.p[L.sid[k]];
+        if (!(sum > 0.0f) || !isfinite(sum) || !(tot > 0.0f)) bad = 1;
+        for (int k = 0; k < a.top_k; k++) {
+            a.ids[k] = L.sid[k];
+            a.wts[k] = L.p[L.sid[k]] / tot;
+        }
+        a.status[0] = bad;
+    }
+    if (shared && rb == 0) {
+        // shared expert weight sigmoid(shexp_gate . x), dot in double
+        double dot = 0.0;
+        if (a.sh_gate)
+            for (int i = t; i < D; i += GU_WG) dot = __builtin_fma((double)a.sh_gate[i], (double)a.x[i], dot);
+        dot = block_sum_d<GU_WG>(dot, L.red);
+        if (t == 0) a.wts[a.top_k] = a.sh_gate ? uq_sigmoid((float)dot) : 1.0f;
+    }
+    float v;
+    if (shared) {
+        v = sl.silu_mul(lxq, lxs, D / KS::UNIT, sub);
+    } else {
+        const int e = L.sid[slot];
+        const int ec = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
+        GuLane<KR, NR> rl;
+        rl.load(rg, ru, (int64_t)ec * a.F + srow, D / KR::UNIT, sub);
+        v = rl.silu_mul(lxq, lxs, D / KR::UNIT, sub);
+    }
+    if (sub == 0) ys[wave * 4 + grp] = v;
+    __syncthreads();
+    if (t < 32) {
+        const float y = ys[t];
+        float s;
+        const int8_t q = uq_quant_lane(y, &s);
+        a.midq[(size_t)slot * a.F + rb * 32 + t] = q;
+        if (t == 0) a.mids[(size_t)slot * (a.F / 32) + rb] = s;
     }
 }
 
-template <class KR, int NR, class KS, int NS>
-__global__ __launch_bounds__(512) void k_moe_gateup(MoeDev a, WArgs rg, WArgs ru, WArgs sg, WArgs su) {
-    __shared__ float ys[32];
-    const int blocks = a.F / 32;
-    const int slot = blockIdx.x / blocks, rb = blockIdx.x % blocks;
-    if (slot < a.top_k) {
-        const int64_t base = (int64_t)a.ids[slot] * a.F;
-        gateup_rows<KR, NR>(a, rg, ru, base, rb, slot, ys);
-    } else {
-        gateup_rows<KS, NS>(a, sg, su, 0, rb, slot, ys);
-    }
-    __syncthreads();
-    if (threadIdx.x < 32) {
-        const float v = ys[threadIdx.x];
-        float s;
-        const int8_t q = uq_quant_lane(v, &s);
-        a.midq[(size_t)slot * a.F + rb * 32 + threadIdx.x] = q;
-        if (threadIdx.x == 0) a.mids[(size_t)slot * (a.F / 32) + rb] = s;
-    }
+// Routed expert id of slot k, clamped into the bank: a row address is never
+// formed from an id outside [0, E).
+__device__ __forceinline__ int expert_id(const MoeDev& a, int k) {
+    const int e = a.ids[k];
+    return e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
 }
 
 // ------------------------------------------------------------------ down + combine
-// One wave per output row: each routed expert's and the shared expert's down
-// row dotted with that expert's quantized mid vector, then combined in rank
-// order as out = out + w*v (separate multiply and add), shared expert last.
-template <class KR, int NR, class KS, int NS>
+// Two output rows per 256-thread workgroup. Waves 0 and 1 take the routed
+// experts of rows r and r+1: lane group g of LS lanes is slot k = pass*SPW + g
+// and its lanes cover that expert's down row (NR units each); waves 2 and 3
+// take the shared expert's row over all 64 lanes (NS units each). Every load
+// of a pass is issued before its dots. The per-slot sums meet in LDS and one
+// lane per row combines them in rank order as out = out + w*v (separate
+// multiply and add), shared expert last.
+template <class KR, int LS, int NR, class KS, int NS>
 __global__ __launch_bounds__(256) void k_moe_down(MoeDev a, WArgs rd, WArgs sd) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-    if (row >= a.D) return;  // whole wave
-    const int64_t nur = a.F / KR::UNIT, nus = a.F / KS::UNIT;
-    float o = 0.0f;
-    for (int k = 0; k <= a.top_k; k++) {
-        const bool shared = k == a.top_k;
-        double acc = 0.0;
-        const int8_t* xq = a.midq + (size_t)k * a.F;
-        const float* xs = a.mids + (size_t)k * (a.F / 32);
-        if (!shared) {
-            const int64_t r = (int64_t)a.ids[k] * a.D + row;
+    constexpr int SPW = 64 / LS;
+    __shared__ float vs[2][MAX_TOPK + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = wave & 1;
+    const int64_t row = (int64_t)blockIdx.x * 2 + half;
+    const bool live = row < a.D;
+    const int64_t rr = live ? row : a.D - 1;
+    if (wave < 2) {
+        const int64_t nu = a.F / KR::UNIT;
+        const int g = lane / LS, sub = lane % LS;
+        for (int k0 = 0; k0 < a.top_k; k0 += SPW) {
+            const int k = k0 + g, kc = k < a.top_k ? k : a.top_k - 1;
+            const int64_t r = (int64_t)expert_id(a, kc) * a.D + rr;
+            const int8_t* xq = a.midq + (size_t)kc * a.F;
+            const float* xs = a.mids + (size_t)kc * (a.F / 32);
+            typename KR::W wv[NR];
 #pragma unroll
             for (int i = 0; i < NR; i++) {
-                const int u = lane + 64 * i;
-                if (u < nur) {
-                    typename KR::X x;
-                    KR::load_x(x, xq, xs, u);
-                    acc += KR::term(rd, r, nur, u, x);
-                }
+                const int u = sub + LS * i, uc = u < nu ? u : (int)nu - 1;
+                wv[i] = KR::load_w(rd, r, nu, uc);
             }
-        } else {
+            typename KR::X xr[NR];
+            load_xr<KR, LS, NR>(xr, xq, xs, nu, sub);
+            double acc = 0.0;
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                const int u = lane + 64 * i;
-                if (u < nus) {
-                    typename KS::X x;
-                    KS::load_x(x, xq, xs, u);
-                    acc += KS::term(sd, row, nus, u, x);
-                }
+            for (int i = 0; i < NR; i++) {
+                const int u = sub + LS * i, uc = u < nu ? u : (int)nu - 1;
+                const double t = KR::dot(wv[i], xr[i], uc);
+                acc += u < nu ? t : 0.0;
             }
+            acc = uq_group_sum<LS>(acc);
+            if (sub == 0 && k < a.top_k) vs[half][k] = (float)acc;
         }
-        const float v = (float)uq_group_sum<64>(acc);
-        const float tv = a.wts[k] * v;
-        o = o + tv;
+    } else {
+        const int64_t nu = a.F / KS::UNIT;
+        const int8_t* xq = a.midq + (size_t)a.top_k * a.F;
+        const float* xs = a.mids + (size_t)a.top_k * (a.F / 32);
+        typename KS::W wv[NS];
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int u = lane + 64 * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = KS::load_w(sd, rr, nu, uc);
+        }
+        typename KS::X xr[NS];
+        load_xr<KS, 64, NS>(xr, xq, xs, nu, lane);
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int u = lane + 64 * i, uc = u < nu ? u : (int)nu - 1;
+            const double t = KS::dot(wv[i], xr[i], uc);
+            acc += u < nu ? t : 0.0;
+        }
+        acc = uq_group_sum<64>(acc);
+        if (lane == 0) vs[half][a.top_k] = (float)acc;
     }
-    if (lane == 0) a.out[row] = o;
+    __syncthreads();
+    if (threadIdx.x < 2 && (int64_t)blockIdx.x * 2 + threadIdx.x < a.D) {
+        float o = 0.0f;
+        for (int k = 0; k <= a.top_k; k++) {
+            const float tv = a.wts[k] * vs[threadIdx.x][k];
+            o = o + tv;
+        }
+        a.out[(int64_t)blockIdx.x * 2 + threadIdx.x] = o;
+    }
 }
 
 }  // namespace
@@ -340,41 +488,49 @@ static int moe_finalize(uq_moe* m) {
 namespace uq {
 namespace {
 
-template <class KR, int NR, class KS, int NS, int DR, int DS>
+// NR/NS: gate/up units per lane (16 lanes per row over D); LS/DR: lanes per
+// routed slot and units per lane over F in the down kernel; DS: shared-expert
+// down units per lane (64 lanes over F).
+template <class KR, int NR, class KS, int NS, int LS, int DR, int DS>
 void moe_launch_t(const uq_moe* m, const MoeDev& d, hipStream_t s) {
     const WArgs rg{m->gate.qs, m->gate.d, m->gate.sc}, ru{m->up.qs, m->up.d, m->up.sc};
     const WArgs sg{m->sgate.qs, m->sgate.d, m->sgate.sc}, su{m->sup.qs, m->sup.d, m->sup.sc};
     const WArgs rd{m->down.qs, m->down.d, m->down.sc}, sd{m->sdown.qs, m->sdown.d, m->sdown.sc};
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, d);
-    hipLaunchKernelGGL((k_moe_gateup<KR, NR, KS, NS>), dim3((unsigned)((m->K + 1) * (m->F / 32))), dim3(512), 0, s, d,
-                       rg, ru, sg, su);
-    hipLaunchKernelGGL((k_moe_down<KR, DR, KS, DS>), dim3((unsigned)((m->D + 3) / 4)), dim3(256), 0, s, d, rd, sd);
+    hipLaunchKernelGGL((k_moe_gateup<KR, NR, KS, NS>), dim3((unsigned)((m->K + 1) * (m->F / 32))), dim3(GU_WG), 0, s,
+                       d, rg, ru, sg, su);
+    hipLaunchKernelGGL((k_moe_down<KR, LS, DR, KS, DS>), dim3((unsigned)((m->D + 1) / 2)), dim3(256), 0, s, d, rd,
+                       sd);
 }
 
-// units per lane: gate/up rows use 16 lanes over D, down rows 64 lanes over F
+int unit_of(uint32_t kind) { return kind == KIND_Q3_K ? 128 : kind == KIND_Q4_K ? 64 : 16; }
+
 int moe_launch(const uq_moe* m, const MoeDev& d, hipStream_t s) {
     const int D = m->D, F = m->F;
-    if (m->kind == KIND_Q3_K && m->shared_kind == KIND_Q8_0 && D == 2048 && F == 768) {
-        moe_launch_t<Q3K, 1, Q8, 8, 1, 1>(m, d, s);  // D/128/16 = 1, D/16/16 = 8; F/128/64, F/16/64 <= 1
-        return OK;
+    const int nr = (D / unit_of(m->kind) + 15) / 16, ns = (D / unit_of(m->shared_kind) + 15) / 16;
+    const int ndr = F / unit_of(m->kind), ds = (F / unit_of(m->shared_kind) + 63) / 64;
+    // routed down row: the first (smallest) lane group in the table that holds it
+#define UQ_MOE(KR, NR_, KS, NS_, LS_, DR_, DS_)                                                            \
+    if (nr <= NR_ && ns <= NS_ && ndr <= LS_ * DR_ && ds <= DS_) {                                       \
+        moe_launch_t<KR, NR_, KS, NS_, LS_, DR_, DS_>(m, d, s);                                             \
+        return OK;                                                                                         \
     }
-    // general shapes: bounds on the register arrays
-    const int nr = (int)((D / (m->kind == KIND_Q3_K ? 128 : m->kind == KIND_Q4_K ? 64 : 16) + 15) / 16);
-    const int ns = (int)((D / (m->shared_kind == KIND_Q3_K ? 128 : m->shared_kind == KIND_Q4_K ? 64 : 16) + 15) / 16);
-    const int dr = (int)((F / (m->kind == KIND_Q3_K ? 128 : m->kind == KIND_Q4_K ? 64 : 16) + 63) / 64);
-    const int ds = (int)((F / (m->shared_kind == KIND_Q3_K ? 128 : m->shared_kind == KIND_Q4_K ? 64 : 16) + 63) / 64);
-    if (m->kind == KIND_Q3_K && m->shared_kind == KIND_Q8_0 && nr <= 2 && ns <= 16 && dr <= 1 && ds <= 4) {
-        moe_launch_t<Q3K, 2, Q8, 16, 1, 4>(m, d, s);
-        return OK;
+    if (m->kind == KIND_Q3_K && m->shared_kind == KIND_Q8_0) {
+        UQ_MOE(Q3K, 1, Q8, 8, 8, 1, 1)
+        UQ_MOE(Q3K, 2, Q8, 16, 8, 1, 1)
+        UQ_MOE(Q3K, 2, Q8, 16, 16, 1, 2)
+        UQ_MOE(Q3K, 2, Q8, 16, 32, 1, 4)
     }
-    if (m->kind == KIND_Q4_K && m->shared_kind == KIND_Q8_0 && nr <= 4 && ns <= 16 && dr <= 1 && ds <= 4) {
-        moe_launch_t<Q4K, 4, Q8, 16, 1, 4>(m, d, s);
-        return OK;
+    if (m->kind == KIND_Q4_K && m->shared_kind == KIND_Q8_0) {
+        UQ_MOE(Q4K, 2, Q8, 8, 16, 1, 1)
+        UQ_MOE(Q4K, 4, Q8, 16, 16, 1, 2)
+        UQ_MOE(Q4K, 4, Q8, 16, 32, 1, 4)
+        UQ_MOE(Q4K, 4, Q8, 16, 64, 1, 4)
     }
-    if (m->kind == KIND_Q8_0 && m->shared_kind == KIND_Q8_0 && nr <= 16 && ns <= 16 && dr <= 4 && ds <= 4) {
-        moe_launch_t<Q8, 16, Q8, 16, 4, 4>(m, d, s);
-        return OK;
+    if (m->kind == KIND_Q8_0 && m->shared_kind == KIND_Q8_0) {
+        UQ_MOE(Q8, 8, Q8, 8, 64, 1, 1)
+        UQ_MOE(Q8, 16, Q8, 16, 64, 4, 4)
     }
+#undef UQ_MOE
     return set_error(ERR_SHAPE, "moe: unsupported kind/shape combination");
 }
 

@@ -23,18 +23,6 @@ struct NormQuantArgs {
     float eps;
 };
 
-struct AttnArgs {
-    const float* q;
-    const uint16_t* kcache;
-    const uint16_t* vcache;
-    const int* pos;
-    float* out;              // [heads*hd]
-    int8_t* xq;              // quantized out
-    float* xs;
-    int heads, kv_heads, head_dim, max_seq;
-    float qscale;
-};
-
 void launch_resnorm_quant(const NormQuantArgs& a, hipStream_t s);
 
 }  // namespace uq

@@ -34,6 +34,8 @@ struct Model {
     uint32_t *token = nullptr, *history = nullptr, *result = nullptr;
     int* pos = nullptr;
     uint32_t* partial = nullptr;
+    float *SC = nullptr, *CM = nullptr;  // attention scores [heads][max_seq], chunk maxima [heads][ATT_SPLIT]
+    double* ACC = nullptr;               // attention output accumulator [heads*hd]
     uint32_t host_io[4] = {0, 0, 0, 0};
 
     // prefill arenas, sized for pcap tokens (padded to the GEMM tile)

@@ -200,6 +200,9 @@ int Model::build_buffers() {
     if (int rc = alloc(&history, c.max_seq)) return rc;
     if (int rc = alloc(&partial, 4 * (size_t)LM_MAX_WG)) return rc;
     if (int rc = alloc(&result, 4)) return rc;
+    if (int rc = alloc(&SC, (size_t)c.heads * c.max_seq)) return rc;
+    if (int rc = alloc(&CM, (size_t)c.heads * ATT_SPLIT)) return rc;
+    if (int rc = alloc(&ACC, (size_t)c.heads * c.head_dim)) return rc;
     // RoPE table, gpu_graph.rs:131-133: angle = pos * powf(theta, -(2i)/hd), cos | sin
     std::vector<float> t((size_t)c.max_seq * c.head_dim);
     const int half = c.head_dim / 2;
@@ -248,10 +251,12 @@ int Model::enqueue_step(hipStream_t s) {
                    vec(lname(l, "attn_v.bias")), trig, pos, QKV, kcache + l * kvl, vcache + l * kvl,
                    c.dim, c.heads, c.kv_heads, c.head_dim};
         if (launch_qkv_rope(qa, s)) return fail(ERR_SHAPE, "qkv_rope: unsupported dim");
-        AttnArgs aa{QKV, kcache + l * kvl, vcache + l * kvl, pos, nullptr, XQ, XS, c.heads, c.kv_heads, c.head_dim,
-                    c.max_seq, (float)(1.0 / std::sqrt((double)c.head_dim))};
-        if (launch_attention_q(aa, s)) return fail(ERR_SHAPE, "attention: head_dim / max_seq beyond the LDS budget");
-        if (int rc = launch_matvec(*weight(lname(l, "attn_output.weight")), nullptr, XQ, XS, TMP, s)) return rc;
+        AttSplitArgs aa{QKV, kcache + l * kvl, vcache + l * kvl, pos, SC, CM, ACC, c.heads, c.kv_heads, c.head_dim,
+                        c.max_seq, (float)(1.0 / std::sqrt((double)c.head_dim))};
+        if (launch_attention_split(aa, s)) return fail(ERR_SHAPE, "attention: head_dim / max_seq beyond the LDS budget");
+        const Weight* wo = weight(lname(l, "attn_output.weight"));
+        WoArgs wa{wo->qs, wo->d, ACC, TMP, wo->m, wo->n};
+        if (launch_wo_acc(wa, s)) return fail(ERR_SHAPE, "o projection: unsupported dim");
         const Weight *wg = weight(lname(l, "ffn_gate.weight")), *wu = weight(lname(l, "ffn_up.weight"));
         GateArgs ga{wg->qs, wu->qs, wg->d, wu->d, nq_args(R0, TMP, vec(lname(l, "ffn_norm.weight")), R1),
                     nullptr, XQH, XSH, c.hidden, c.dim};

@@ -47,8 +47,35 @@ struct LmArgs {
     int max_seq;
 };
 
+// Decode attention split over ATT_SPLIT position chunks per query head:
+// scores -> [heads][max_seq] and per-chunk maxima, then each chunk's P.V
+// (with the exact global softmax) added into a double accumulator, which the
+// o projection reads, converts and quantizes in its prologue.
+constexpr int ATT_SPLIT = 8;
+struct AttSplitArgs {
+    const float* q;           // rotated q [heads*hd]
+    const uint16_t* kcache;   // this layer [max_seq][kv*hd]
+    const uint16_t* vcache;
+    const int* pos;
+    float* scores;            // [heads][max_seq]
+    float* cmax;              // [heads][ATT_SPLIT]
+    double* acc;              // [heads*hd], zeroed by the scores kernel
+    int heads, kv_heads, head_dim, max_seq;
+    float qscale;
+};
+
+// o projection with the attention accumulator as input: y = W quant((float)acc)
+struct WoArgs {
+    const int8_t* w_qs;
+    const uint16_t* w_d;
+    const double* acc;        // [k]
+    float* y;                 // [rows]
+    int64_t rows, k;
+};
+
 int launch_qkv_rope(const QkvArgs& a, hipStream_t s);
-int launch_attention_q(const AttnArgs& a, hipStream_t s);
+int launch_attention_split(const AttSplitArgs& a, hipStream_t s);
+int launch_wo_acc(const WoArgs& a, hipStream_t s);
 int launch_gateup_q(const GateArgs& a, hipStream_t s);
 int launch_lm_greedy(const LmArgs& a, hipStream_t s);
 

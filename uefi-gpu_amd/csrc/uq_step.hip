@@ -5,9 +5,11 @@
 //              RoPE, fp16 K/V store at `pos` (fused_resnorm + quant_act +
 //              qkv_dp4a + rope_bias: gpu_fused.cu:193-200, gpu_dp4a.cu:23-59,
 //              gpu_ops.cu:235-246)
-//   attention  GQA softmax attention over the fp16 cache, output quantized
-//              (fused_attention + quant_act, gpu_attention.cu:202-226)
-//   o matvec   generic matvec (linear_dp4a)
+//   attention  GQA softmax attention over the fp16 cache split over position
+//              chunks: scores, then P.V into a double accumulator
+//              (fused_attention, gpu_attention.cu:202-226)
+//   o matvec   accumulator -> f32 -> block-32 quant prologue, Q8_0 matvec
+//              (quant_act + linear_dp4a)
 //   gateup_q   residual + RMSNorm + quant prologue, gate/up matvec, SiLU*up,
 //              block-32 quant (gateup_dp4a, gpu_dp4a.cu:60-64)
 //   down       generic matvec
@@ -109,110 +111,195 @@ __global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ attention
-// One 1024-thread workgroup per query head; HD/8 lanes cover one position
-// (each lane 8 dims = one 16-byte fp16 load), so a pass covers 1024/(HD/8)
-// positions and two passes are issued back to back.
-// Scores: q.k in double, butterfly over the position's lanes, * 1/sqrt(hd).
-// Softmax: max subtraction, exp, total in double, p = e/total.
-// P.V: lane (chunk c, position slice) accumulates 8 dims in double; slices in
-// a wave combine by butterfly, the 16 waves through LDS.
-constexpr int AT_WG = 1024;
+// ------------------------------------------------------------------ split attention
+// Scores: workgroup (head, chunk) covers positions [lo, hi) of the chunk with
+// HD/8 lanes per position (8 dims each, one 16-byte fp16 load), AS_B
+// positions per lane in flight. q.k in double, butterfly over the position's
+// lanes, * 1/sqrt(hd), rounded to f32 -- the oracle's score bits.
+constexpr int AS_WG = 256, AS_B = 4;
 template <int HD>
-__global__ __launch_bounds__(AT_WG) void k_attention(AttnArgs a) {
-    constexpr int LP = HD / 8, NPASS = AT_WG / LP, NW = AT_WG / 64;
-    extern __shared__ double dyn[];  // [NW*HD] P.V partials, then [max_seq] floats
-    __shared__ double qd[HD];
-    __shared__ double red_d[NW];
-    __shared__ float red_f[NW];
-    const int tid = threadIdx.x, kvd = a.kv_heads * HD;
-    double* part = dyn;
-    float* sc = (float*)(dyn + NW * HD);
-    const int pos = *a.pos, T = pos + 1;
-    const int h = blockIdx.x, kh = h / (a.heads / a.kv_heads);
-    if (tid < HD) qd[tid] = (double)a.q[h * HD + tid];
-    __syncthreads();
+__global__ __launch_bounds__(AS_WG) void k_att_scores(AttSplitArgs a) {
+    constexpr int LP = HD / 8, NG = AS_WG / LP;
+    __shared__ float redf[AS_WG / 64];
+    const int tid = threadIdx.x, h = blockIdx.x, s = blockIdx.y;
+    const int kvd = a.kv_heads * HD, kh = h / (a.heads / a.kv_heads);
+    const int T = *a.pos + 1;
+    const int lo = (int)((int64_t)s * T / ATT_SPLIT), hi = (int)((int64_t)(s + 1) * T / ATT_SPLIT);
     const int grp = tid / LP, c = tid % LP;
+    if (s == 0 && tid < HD) a.acc[h * HD + tid] = 0.0;
+    double q8[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q8[i] = (double)a.q[h * HD + 8 * c + i];
     const uint16_t* kb = a.kcache + kh * HD + 8 * c;
     float mx = -3.402823466e38f;
-    for (int t0 = grp; t0 < T; t0 += 2 * NPASS) {
-        const int t1 = t0 + NPASS;
-        const int4 k0 = *(const int4*)(kb + (size_t)t0 * kvd);
-        const int4 k1 = t1 < T ? *(const int4*)(kb + (size_t)t1 * kvd) : make_int4(0, 0, 0, 0);
-        const uint32_t w0[4] = {(uint32_t)k0.x, (uint32_t)k0.y, (uint32_t)k0.z, (uint32_t)k0.w};
-        const uint32_t w1[4] = {(uint32_t)k1.x, (uint32_t)k1.y, (uint32_t)k1.z, (uint32_t)k1.w};
-        double a0 = 0.0, a1 = 0.0;
+    for (int t0 = lo; t0 < hi; t0 += AS_B * NG) {
+        int4 kk[AS_B];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const double q0 = qd[8 * c + 2 * i], q1 = qd[8 * c + 2 * i + 1];
-            a0 = __builtin_fma(q0, (double)uq_half((uint16_t)(w0[i] & 0xffff)), a0);
-            a0 = __builtin_fma(q1, (double)uq_half((uint16_t)(w0[i] >> 16)), a0);
-            a1 = __builtin_fma(q0, (double)uq_half((uint16_t)(w1[i] & 0xffff)), a1);
-            a1 = __builtin_fma(q1, (double)uq_half((uint16_t)(w1[i] >> 16)), a1);
+        for (int u = 0; u < AS_B; u++) {
+            const int t = t0 + u * NG + grp;
+            kk[u] = t < hi ? *(const int4*)(kb + (size_t)t * kvd) : make_int4(0, 0, 0, 0);
         }
-        a0 = uq_group_sum<LP>(a0);
-        a1 = uq_group_sum<LP>(a1);
-        const float s0 = (float)a0 * a.qscale;
-        mx = fmaxf(mx, s0);
-        if (c == 0) sc[t0] = s0;
-        if (t1 < T) {
-            const float s1 = (float)a1 * a.qscale;
-            mx = fmaxf(mx, s1);
-            if (c == 0) sc[t1] = s1;
-        }
-    }
-    mx = block_max_f<AT_WG>(mx, red_f);
-    double tot = 0.0;
-    for (int t = tid; t < T; t += AT_WG) {
-        const float ev = uq_expf(sc[t] - mx);
-        sc[t] = ev;
-        tot += (double)ev;
-    }
-    tot = block_sum_d<AT_WG>(tot, red_d);
-    const float total = (float)tot;
-    for (int t = tid; t < T; t += AT_WG) sc[t] = sc[t] / total;
-    __syncthreads();
-    double acc[8];
+        double d[AS_B];
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0;
-    const uint16_t* vb = a.vcache + kh * HD + 8 * c;
-    constexpr int U = 4;
-    for (int t0 = grp; t0 < T; t0 += U * NPASS) {
-        int4 vv[U];
-        double pt[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int t = t0 + u * NPASS;
-            vv[u] = t < T ? *(const int4*)(vb + (size_t)t * kvd) : make_int4(0, 0, 0, 0);
-            pt[u] = t < T ? (double)sc[t] : 0.0;
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t w[4] = {(uint32_t)vv[u].x, (uint32_t)vv[u].y, (uint32_t)vv[u].z, (uint32_t)vv[u].w};
+        for (int u = 0; u < AS_B; u++) {
+            const uint32_t w[4] = {(uint32_t)kk[u].x, (uint32_t)kk[u].y, (uint32_t)kk[u].z, (uint32_t)kk[u].w};
+            double acc = 0.0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                acc[2 * i] = __builtin_fma(pt[u], (double)uq_half((uint16_t)(w[i] & 0xffff)), acc[2 * i]);
-                acc[2 * i + 1] = __builtin_fma(pt[u], (double)uq_half((uint16_t)(w[i] >> 16)), acc[2 * i + 1]);
+                acc = __builtin_fma(q8[2 * i], (double)uq_half((uint16_t)(w[i] & 0xffff)), acc);
+                acc = __builtin_fma(q8[2 * i + 1], (double)uq_half((uint16_t)(w[i] >> 16)), acc);
+            }
+            d[u] = uq_group_sum<LP>(acc);
+        }
+#pragma unroll
+        for (int u = 0; u < AS_B; u++) {
+            const int t = t0 + u * NG + grp;
+            if (t < hi) {
+                const float sc = (float)d[u] * a.qscale;
+                mx = fmaxf(mx, sc);
+                if (c == 0) a.scores[(size_t)h * a.max_seq + t] = sc;
             }
         }
     }
-    // lanes with the same chunk in a wave: c = lane % LP
+    mx = block_max_f<AS_WG>(mx, redf);
+    if (tid == 0) a.cmax[h * ATT_SPLIT + s] = mx;
+}
+
+// P.V: every chunk workgroup of a head recomputes the global max (from the
+// chunk maxima), all exps and their double total (same operations in the
+// same order in each workgroup, so the same f32 total); p = e/total for its
+// own positions, P.V in double, and the chunk's partial sums are added into
+// the accumulator (double atomics: their order only moves the double's last
+// bits, far below the one f32 rounding the consumer applies).
+template <int HD>
+__global__ __launch_bounds__(AS_WG) void k_att_pv(AttSplitArgs a) {
+    constexpr int LP = HD / 8, NG = AS_WG / LP, NW = AS_WG / 64;
+    extern __shared__ float es[];  // [max_seq]
+    __shared__ double red_d[NW];
+    __shared__ double part[NW][HD];
+    const int tid = threadIdx.x, h = blockIdx.x, s = blockIdx.y;
+    const int kvd = a.kv_heads * HD, kh = h / (a.heads / a.kv_heads);
+    const int T = *a.pos + 1;
+    const int lo = (int)((int64_t)s * T / ATT_SPLIT), hi = (int)((int64_t)(s + 1) * T / ATT_SPLIT);
+    const int grp = tid / LP, c = tid % LP;
+    // first V batch in flight during the softmax work
+    const uint16_t* vb = a.vcache + kh * HD + 8 * c;
+    int4 vv[AS_B];
+#pragma unroll
+    for (int u = 0; u < AS_B; u++) {
+        const int t = lo + u * NG + grp;
+        vv[u] = t < hi ? *(const int4*)(vb + (size_t)t * kvd) : make_int4(0, 0, 0, 0);
+    }
+    float mx = -3.402823466e38f;
+#pragma unroll
+    for (int j = 0; j < ATT_SPLIT; j++) mx = fmaxf(mx, a.cmax[h * ATT_SPLIT + j]);
+    const float* sc = a.scores + (size_t)h * a.max_seq;
+    double tot = 0.0;
+    for (int t = tid; t < T; t += AS_WG) {
+        const float ev = uq_expf(sc[t] - mx);
+        es[t] = ev;
+        tot += (double)ev;
+    }
+    tot = block_sum_d<AS_WG>(tot, red_d);  // its barriers also publish es
+    const float total = (float)tot;
+    double acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0;
+    for (int t0 = lo; t0 < hi; t0 += AS_B * NG) {
+        if (t0 > lo) {
+#pragma unroll
+            for (int u = 0; u < AS_B; u++) {
+                const int t = t0 + u * NG + grp;
+                vv[u] = t < hi ? *(const int4*)(vb + (size_t)t * kvd) : make_int4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < AS_B; u++) {
+            const int t = t0 + u * NG + grp;
+            const float pt = t < hi ? es[t] / total : 0.0f;
+            const uint32_t w[4] = {(uint32_t)vv[u].x, (uint32_t)vv[u].y, (uint32_t)vv[u].z, (uint32_t)vv[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[2 * i] = __builtin_fma((double)pt, (double)uq_half((uint16_t)(w[i] & 0xffff)), acc[2 * i]);
+                acc[2 * i + 1] = __builtin_fma((double)pt, (double)uq_half((uint16_t)(w[i] >> 16)), acc[2 * i + 1]);
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = uq_rows_sum<LP>(acc[i]);
     const int wave = tid >> 6, lane = tid & 63;
     if (lane < LP)
 #pragma unroll
-        for (int i = 0; i < 8; i++) part[wave * HD + 8 * lane + i] = acc[i];
+        for (int i = 0; i < 8; i++) part[wave][8 * lane + i] = acc[i];
     __syncthreads();
-    if (tid < HD) {
-        double s = 0.0;
-        for (int w = 0; w < NW; w++) s += part[w * HD + tid];
-        const float o = (float)s;
-        if (a.out) a.out[h * HD + tid] = o;
-        float qs;
-        const int8_t qv = uq_quant_lane(o, &qs);
-        a.xq[h * HD + tid] = qv;
-        if ((tid & 31) == 0) a.xs[(h * HD + tid) >> 5] = qs;
+    if (tid < HD && hi > lo) {
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) sum += part[w][tid];
+        atomicAdd(&a.acc[h * HD + tid], sum);
+    }
+}
+
+// ------------------------------------------------------------------ o projection from the accumulator
+// Q8_0 matvec whose input is the attention accumulator: the accumulator is
+// loaded first, then this workgroup's first row set of weights, then the
+// accumulator is rounded to f32 and quantized per 32 into LDS.
+template <int LPR, int NBL>
+__global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t lq[MAX_DIM];
+    __shared__ float ls[MAX_DIM / 32];
+    constexpr int RPW = 64 / LPR, RPB = RPW * 4, PER = MAX_DIM / 256;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPR, grp = lane / LPR;
+    const int64_t nu = a.k / Q8::UNIT, K = a.k;
+    double av[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * 256 + tid;
+        av[j] = i < K ? a.acc[i] : 0.0;
+    }
+    const WArgs w{a.w_qs, a.w_d, nullptr};
+    int64_t row0 = (int64_t)blockIdx.x * RPB;
+    Q8::W wv[NBL];
+    {
+        const int64_t row = row0 + wave * RPW + grp, rr = row < a.rows ? row : a.rows - 1;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = Q8::load_w(w, rr, nu, uc);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * 256 + tid;
+        if (i < K) {
+            float sc;
+            const int8_t q = uq_quant_lane((float)av[j], &sc);
+            lq[i] = q;
+            if ((tid & 31) == 0) ls[i >> 5] = sc;
+        }
+    }
+    __syncthreads();
+    Q8::X xr[NBL];
+    load_xr<Q8, LPR, NBL>(xr, lq, ls, nu, sub);
+    for (;;) {
+        const int64_t row = row0 + wave * RPW + grp;
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i;
+            const double t = Q8::dot(wv[i], xr[i]);
+            acc += u < nu ? t : 0.0;
+        }
+        acc = uq_group_sum<LPR>(acc);
+        if (row < a.rows && sub == 0) a.y[row] = (float)acc;
+        row0 += (int64_t)gridDim.x * RPB;
+        if (row0 >= a.rows) break;
+        const int64_t nrow = row0 + wave * RPW + grp, rr = nrow < a.rows ? nrow : a.rows - 1;
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = Q8::load_w(w, rr, nu, uc);
+        }
     }
 }
 
@@ -360,15 +447,34 @@ int launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
     const int units = (a.heads + 2 * a.kv_heads) * (a.head_dim / 2);
     return pick_nbl<32, QkvRope>(a.dim / Q8::UNIT, dim3((units + 3) / 4), dim3(256), 0, s, a);
 }
-int launch_attention_q(const AttnArgs& a, hipStream_t s) {
-    const size_t lds = sizeof(double) * (size_t)(AT_WG / 64) * a.head_dim + sizeof(float) * (size_t)a.max_seq;
-    if (lds + sizeof(double) * a.head_dim + 256 > 65536) return -1;
+int launch_attention_split(const AttSplitArgs& a, hipStream_t s) {
+    const size_t lds = sizeof(float) * (size_t)a.max_seq;
+    if (lds + sizeof(double) * (AS_WG / 64) * (size_t)a.head_dim + 256 > 65536) return -1;
+    if (a.heads % a.kv_heads) return -1;
+    const dim3 grid((unsigned)a.heads, ATT_SPLIT);
     switch (a.head_dim) {
-    case 64: hipLaunchKernelGGL(k_attention<64>, dim3(a.heads), dim3(AT_WG), lds, s, a); return 0;
-    case 128: hipLaunchKernelGGL(k_attention<128>, dim3(a.heads), dim3(AT_WG), lds, s, a); return 0;
-    case 256: hipLaunchKernelGGL(k_attention<256>, dim3(a.heads), dim3(AT_WG), lds, s, a); return 0;
+    case 64:
+        hipLaunchKernelGGL(k_att_scores<64>, grid, dim3(AS_WG), 0, s, a);
+        hipLaunchKernelGGL(k_att_pv<64>, grid, dim3(AS_WG), lds, s, a);
+        return 0;
+    case 128:
+        hipLaunchKernelGGL(k_att_scores<128>, grid, dim3(AS_WG), 0, s, a);
+        hipLaunchKernelGGL(k_att_pv<128>, grid, dim3(AS_WG), lds, s, a);
+        return 0;
+    case 256:
+        hipLaunchKernelGGL(k_att_scores<256>, grid, dim3(AS_WG), 0, s, a);
+        hipLaunchKernelGGL(k_att_pv<256>, grid, dim3(AS_WG), lds, s, a);
+        return 0;
     default: return -1;
     }
+}
+template <int LPR, int NBL> struct WoAcc { static constexpr auto fn = k_wo_acc<LPR, NBL>; };
+int launch_wo_acc(const WoArgs& a, hipStream_t s) {
+    if (a.k > MAX_DIM || a.k % 32) return -1;
+    constexpr int RPB = 4 * (64 / 32);
+    const int64_t sets = (a.rows + RPB - 1) / RPB;
+    const unsigned grid = (unsigned)(sets < 2048 ? sets : 2048);
+    return pick_nbl<32, WoAcc>(a.k / Q8::UNIT, dim3(grid), dim3(256), 0, s, a);
 }
 int launch_gateup_q(const GateArgs& a, hipStream_t s) {
     if (a.k > MAX_DIM || a.rows % 32) return -1;

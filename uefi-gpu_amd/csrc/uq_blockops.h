@@ -114,6 +114,110 @@ __device__ __forceinline__ void norm_quant_finish(const NormQuantArgs& a, const 
     __syncthreads();
 }
 
+// The same residual + RMSNorm + block-32 quant done by ONE wave, for kernels
+// whose other waves stream weights meanwhile, in two halves: issue() pulls the
+// raw vectors (x, residual, gamma) into LDS staging by DMA (the embedding row
+// into registers), so they hold no VGPRs while in flight; finish() waits for
+// them and computes, with the sum of squares as a wave butterfly (no
+// workgroup barrier). A kernel puts a barrier between the two halves and its
+// weight loads after it, so that these loads enter the CU's memory queue
+// ahead of the weight stream. Element i = 256*j + 4*lane + c, so a 32-block is
+// 8 lanes. Requires dim % 32 == 0 and dim <= 256*NC; lx/lr/lg hold 256*NC
+// floats each. The quantized vector goes to q (int8) and s (one f32 per block)
+// in LDS; the caller's barrier publishes it.
+template <int NC>
+struct NormQuantWave {
+    uint32_t e[NC];
+    uint16_t d[NC];
+
+    __device__ __forceinline__ void issue(const NormQuantArgs& a, float* lx, float* lr, float* lg) {
+        const int lane = threadIdx.x & 63, D = a.dim;
+        if (a.embed_qs) {
+            const int64_t row = (int64_t)*a.token;
+#pragma unroll
+            for (int j = 0; j < NC; j++) {
+                const int i = 256 * j + 4 * lane, ic = i < D ? i : D - 4;
+                e[j] = *(const uint32_t*)(a.embed_qs + row * D + ic);
+                d[j] = a.embed_d[row * (D / 32) + ic / 32];
+                uq_lds_load16(a.gamma + ic, lg + 256 * j);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NC; j++) {
+                const int i = 256 * j + 4 * lane, ic = i < D ? i : D - 4;
+                uq_lds_load16(a.x + ic, lx + 256 * j);
+                if (a.residual) uq_lds_load16(a.residual + ic, lr + 256 * j);
+                uq_lds_load16(a.gamma + ic, lg + 256 * j);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void finish(const NormQuantArgs& a, bool write_x, const float* lx, const float* lr,
+                                           const float* lg, int8_t* q, float* s) {
+        const int lane = threadIdx.x & 63, D = a.dim;
+        uq_wait_vm0();
+        asm volatile("" ::: "memory");
+        float xv[NC][4];
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int i = 256 * j + 4 * lane;
+            if (a.embed_qs) {
+                const float dd = uq_half(d[j]);
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[j][c] = dd * (float)(int8_t)(e[j] >> (8 * c));
+            } else {
+                const float4 xx = ((const float4*)lx)[64 * j + lane];
+                xv[j][0] = xx.x;
+                xv[j][1] = xx.y;
+                xv[j][2] = xx.z;
+                xv[j][3] = xx.w;
+                if (a.residual) {
+                    const float4 rr = ((const float4*)lr)[64 * j + lane];
+                    xv[j][0] = xv[j][0] + rr.x;
+                    xv[j][1] = xv[j][1] + rr.y;
+                    xv[j][2] = xv[j][2] + rr.z;
+                    xv[j][3] = xv[j][3] + rr.w;
+                }
+            }
+            if (i < D) {
+                if (write_x && a.x_out)
+                    *(float4*)(a.x_out + i) = make_float4(xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float sq = xv[j][c] * xv[j][c];
+                    ss += (double)sq;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; c++) xv[j][c] = 0.0f;
+            }
+        }
+        ss = uq_group_sum<64>(ss);
+        const float mean = (float)(ss / (double)D);
+        const float scale = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int i = 256 * j + 4 * lane;
+            const float4 g4 = ((const float4*)lg)[64 * j + lane];
+            const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
+            float y[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float tmp = xv[j][c] * scale;
+                y[c] = tmp * gg[c];
+            }
+            // lanes past dim hold zeros and form whole 8-lane groups
+            uint32_t packed;
+            const float sc = uq_quant4_group8(y, &packed);
+            if (i < D) {
+                *(uint32_t*)(q + i) = packed;
+                if ((lane & 7) == 0) s[i >> 5] = sc;
+            }
+        }
+    }
+};
+
 template <int WG>
 __device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red,
                                   int sstride = 1) {

@@ -13,6 +13,22 @@
 
 #define UQ_DEV __device__ __forceinline__
 
+// s_waitcnt vmcnt(0): every vector-memory op this wave has issued (LDS DMA
+// included) has completed; expcnt and lgkmcnt are not waited on.
+UQ_DEV void uq_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
+// lane l's bytes land at lds_wave_base + 16*l; lds_wave_base is wave-uniform.
+typedef __attribute__((address_space(3))) void uq_lds_void;
+UQ_DEV void uq_lds_load16(const void* g, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (uq_lds_void*)lds_wave_base, 16, 0, 0);
+}
+// Workgroup barrier that waits for no memory operation (s_barrier alone):
+// orders instruction issue across the waves, publishes nothing.
+UQ_DEV void uq_issue_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 UQ_DEV float uq_half(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 UQ_DEV uint16_t uq_f16_rne(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
@@ -183,4 +199,24 @@ UQ_DEV int8_t uq_quant_lane(float v, float* scale_out) {
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     *scale_out = a / 127.0f;
     return (int8_t)(int)r;
+}
+// The same quant with 4 consecutive values per lane, a 32-block = 8 lanes:
+// returns the block scale and packs the 4 int8 codes (lowest value in the low
+// byte). The amax is an fmaxf tree like uq_quant_lane's (a NaN is dropped
+// unless the whole block is NaN), so both give the same codes and scale.
+UQ_DEV float uq_quant4_group8(const float v[4], uint32_t* packed) {
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    a = uq_group_max<8>(a);
+    const float inv = a > 0.0f ? 127.0f / a : 0.0f;
+    uint32_t p = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float t = v[c] * inv;
+        float r = __builtin_rintf(t);
+        if (r != r) r = 0.0f;
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        p |= ((uint32_t)(uint8_t)(int8_t)(int)r) << (8 * c);
+    }
+    *packed = p;
+    return a / 127.0f;
 }

@@ -46,6 +46,9 @@ struct Weight {
     int64_t gguf_bytes = 0;        // bytes of the original GGUF tensor
 };
 
+// Compute units of the current device (queried once).
+int cu_count();
+
 int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank);
 
 // ---- kernel launchers (uq_matvec.hip) ----

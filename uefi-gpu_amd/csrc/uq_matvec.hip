@@ -159,10 +159,42 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
 }
 
 // ---------------------------------------------------------------- matvec kernel
+
+// One row of a lane group: every weight load of the row is issued, then the
+// dots run (a unit past the row end loads the last unit and is dropped by a
+// select), the lane group reduces, lane 0 stores.
+template <class KQ, int LPR, int NBL, bool GATEUP>
+__device__ __forceinline__ void matvec_row(const WArgs& w, const WArgs& w2, const typename KQ::X* xr, float* y,
+                                           int64_t row, int64_t end, int64_t nu, int sub) {
+    // rows past the end load the last row; every lane takes part in the reductions
+    const int64_t rr = row < end ? row : end - 1;
+    typename KQ::W wv[NBL], wv2[NBL];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+        wv[i] = KQ::load_w(w, rr, nu, uc);
+        if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
+    }
+    double acc = 0.0, acc2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+        const double t = KQ::dot(wv[i], xr[i], uc);
+        acc += u < nu ? t : 0.0;
+        if (GATEUP) {
+            const double t2 = KQ::dot(wv2[i], xr[i], uc);
+            acc2 += u < nu ? t2 : 0.0;
+        }
+    }
+    acc = uq_group_sum<LPR>(acc);
+    if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
+    if (row < end && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+}
+
 template <class KQ, int LPR, int NBL, bool GATEUP>
 __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
                                                const float* __restrict__ xs, float* __restrict__ y,
-                                               int64_t rows, int64_t K) {
+                                               int64_t rows, int64_t K, int64_t share) {
     constexpr int RPW = 64 / LPR;
     constexpr int RPB = RPW * (WG / 64);
     const int64_t nu = K / KQ::UNIT;
@@ -170,32 +202,46 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
     const int sub = lane % LPR, grp = lane / LPR;
     typename KQ::X xr[NBL];
     load_xr<KQ, LPR, NBL>(xr, xq, xs, nu, sub);
-    for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
-        const int64_t row = row0 + wave * RPW + grp;
-        // rows past the end load the last row; every lane takes part in the reductions
-        const int64_t rr = row < rows ? row : rows - 1;
-        typename KQ::W wv[NBL], wv2[NBL];
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-            wv[i] = KQ::load_w(w, rr, nu, uc);
-            if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
-        }
-        double acc = 0.0, acc2 = 0.0;
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-            const double t = KQ::dot(wv[i], xr[i], uc);
-            acc += u < nu ? t : 0.0;
-            if (GATEUP) {
-                const double t2 = KQ::dot(wv2[i], xr[i], uc);
-                acc2 += u < nu ? t2 : 0.0;
-            }
-        }
-        acc = uq_group_sum<LPR>(acc);
-        if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
-        if (row < rows && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+    if (rows <= (int64_t)gridDim.x * RPB) {
+        // one pass: this workgroup's even share of the rows
+        const RowSpan sp = even_span(rows, share);
+        const int64_t row = sp.begin + wave * RPW + grp;
+        if (sp.begin + wave * RPW < sp.end) matvec_row<KQ, LPR, NBL, GATEUP>(w, w2, xr, y, row, sp.end, nu, sub);
+    } else {
+        for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB)
+            matvec_row<KQ, LPR, NBL, GATEUP>(w, w2, xr, y, row0 + wave * RPW + grp, rows, nu, sub);
     }
+}
+
+// One row with the activation read from LDS (K-quant units), same order of
+// work as matvec_row.
+template <class KQ, int LPR, int NBL, bool GATEUP>
+__device__ __forceinline__ void matvec_row_lds(const WArgs& w, const WArgs& w2, const int8_t* lx, const float* lxs,
+                                               const int* ls16, float* y, int64_t row, int64_t end, int64_t nu,
+                                               int sub) {
+    const int64_t rr = row < end ? row : end - 1;
+    typename KQ::W wv[NBL], wv2[NBL];
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+        wv[i] = KQ::load_w(w, rr, nu, uc);
+        if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
+    }
+    double acc = 0.0, acc2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+        asm volatile("" ::: "memory");  // one unit's activation reads at a time
+        const double t = KQ::dot_lds(wv[i], lx, lxs, ls16, uc);
+        acc += u < nu ? t : 0.0;
+        if (GATEUP) {
+            const double t2 = KQ::dot_lds(wv2[i], lx, lxs, ls16, uc);
+            acc2 += u < nu ? t2 : 0.0;
+        }
+    }
+    acc = uq_group_sum<LPR>(acc);
+    if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
+    if (row < end && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
 }
 
 // K-quant variant: units carry 64-128 activation values, too many to keep in
@@ -206,7 +252,7 @@ constexpr int MAX_XL = 16384;
 template <class KQ, int LPR, int NBL, bool GATEUP>
 __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, float* __restrict__ y,
-                                                  int64_t rows, int64_t K) {
+                                                  int64_t rows, int64_t K, int64_t share) {
     __shared__ __attribute__((aligned(16))) int8_t lx[MAX_XL];
     __shared__ float lxs[MAX_XL / 32];
     __shared__ int ls16[MAX_XL / 16];
@@ -226,31 +272,14 @@ __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_
     }
     for (int b = threadIdx.x; b < K / 32; b += WG) lxs[b] = xs[b];
     __syncthreads();
-    for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB) {
-        const int64_t row = row0 + wave * RPW + grp;
-        const int64_t rr = row < rows ? row : rows - 1;
-        typename KQ::W wv[NBL], wv2[NBL];
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-            wv[i] = KQ::load_w(w, rr, nu, uc);
-            if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
-        }
-        double acc = 0.0, acc2 = 0.0;
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-            asm volatile("" ::: "memory");  // one unit's activation reads at a time
-            const double t = KQ::dot_lds(wv[i], lx, lxs, ls16, uc);
-            acc += u < nu ? t : 0.0;
-            if (GATEUP) {
-                const double t2 = KQ::dot_lds(wv2[i], lx, lxs, ls16, uc);
-                acc2 += u < nu ? t2 : 0.0;
-            }
-        }
-        acc = uq_group_sum<LPR>(acc);
-        if (GATEUP) acc2 = uq_group_sum<LPR>(acc2);
-        if (row < rows && sub == 0) y[row] = GATEUP ? uq_silu_mul((float)acc, (float)acc2) : (float)acc;
+    if (rows <= (int64_t)gridDim.x * RPB) {
+        // one pass: this workgroup's even share of the rows
+        const RowSpan sp = even_span(rows, share);
+        if (sp.begin + wave * RPW < sp.end)
+            matvec_row_lds<KQ, LPR, NBL, GATEUP>(w, w2, lx, lxs, ls16, y, sp.begin + wave * RPW + grp, sp.end, nu, sub);
+    } else {
+        for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < rows; row0 += (int64_t)gridDim.x * RPB)
+            matvec_row_lds<KQ, LPR, NBL, GATEUP>(w, w2, lx, lxs, ls16, y, row0 + wave * RPW + grp, rows, nu, sub);
     }
 }
 
@@ -302,16 +331,22 @@ inline unsigned grid_for(int64_t items, int per_block) {
 template <class KQ, int LPR, int NBL, bool XL = false>
 void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
     constexpr int RPB = (64 / LPR) * (WG / 64);
-    int64_t sets = (w.m + RPB - 1) / RPB;
-    const unsigned grid = (unsigned)(sets < 2048 ? sets : 2048);
+    // a multiple of the CU count with at most one pass of rows per workgroup,
+    // or 2048 workgroups striding over the rows
+    const int64_t cu = cu_count(), m = (w.m + cu * RPB - 1) / (cu * RPB);
+    int64_t g = m * cu;
+    if (g > 2048) g = 2048;
+    if (g > w.m) g = w.m;
+    const unsigned grid = (unsigned)g;
+    const int64_t share = w.m / g;
     WArgs a{w.qs, w.d, w.sc}, b{nullptr, nullptr, nullptr};
     if (w2) b = WArgs{w2->qs, w2->d, w2->sc};
     if constexpr (XL) {
-        if (w2) hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
-        else hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+        if (w2) hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
+        else hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
     } else {
-        if (w2) hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
-        else hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n);
+        if (w2) hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
+        else hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
     }
 }
 
@@ -344,6 +379,17 @@ int launch_kind(const Weight& w, const Weight* w2, const int8_t* xq, const float
 }
 
 }  // namespace
+
+int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            return 256;
+        n = v;
+    }
+    return n;
+}
 
 void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s) {
     hipLaunchKernelGGL(k_quant_act, dim3(grid_for(n, WG)), dim3(WG), 0, s, x, n, xq, xs);

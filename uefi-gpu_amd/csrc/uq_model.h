@@ -28,8 +28,7 @@ struct Model {
 
     float *R0 = nullptr, *R1 = nullptr, *TMP = nullptr, *XN = nullptr, *QKV = nullptr, *ATT = nullptr, *GATE = nullptr,
           *LOGITS = nullptr, *XS = nullptr, *trig = nullptr;
-    int8_t *XQ = nullptr, *XQH = nullptr;  // quantized activations: dim-sized, hidden-sized
-    float* XSH = nullptr;
+    int8_t* XQ = nullptr;  // quantized dim-sized activation (lm_head input)
     uint16_t *kcache = nullptr, *vcache = nullptr;
     uint32_t *token = nullptr, *history = nullptr, *result = nullptr;
     int* pos = nullptr;

@@ -53,7 +53,7 @@ int uq_model_create(const uq_qwen2_config* cfg, uq_model_t* out) {
     if (!cfg || !out) return set_error(ERR_ARG, "model_create: null pointer");
     const auto& c = *cfg;
     if (c.layers <= 0 || c.dim <= 0 || c.dim % 256 || c.dim > 4096 || c.hidden <= 0 || c.hidden % 256 ||
-        c.hidden > 16384 || c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 32 ||
+        c.hidden > 9216 || c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads || c.head_dim % 32 ||
         c.heads * c.head_dim != c.dim || c.head_dim % 64 || c.head_dim > 256 || 1024 % c.head_dim || c.vocab <= 0 || c.max_seq <= 0 || c.max_seq > 8192)
         return set_error(ERR_SHAPE, "model_create: unsupported configuration");
     void* stream = uq_stream();
@@ -179,7 +179,7 @@ int Model::alloc(T** p, size_t count) {
 
 int Model::build_buffers() {
     const auto& c = cfg;
-    const int kvd = c.kv_heads * c.head_dim, big = c.hidden > c.dim ? c.hidden : c.dim;
+    const int kvd = c.kv_heads * c.head_dim;
     if (int rc = alloc(&R0, c.dim)) return rc;
     if (int rc = alloc(&R1, c.dim)) return rc;
     if (int rc = alloc(&TMP, c.dim)) return rc;
@@ -190,8 +190,6 @@ int Model::build_buffers() {
     if (int rc = alloc(&LOGITS, c.vocab)) return rc;
     if (int rc = alloc(&XQ, c.dim)) return rc;
     if (int rc = alloc(&XS, c.dim / 32)) return rc;
-    if (int rc = alloc(&XQH, big)) return rc;
-    if (int rc = alloc(&XSH, big / 32)) return rc;
     if (int rc = alloc(&kcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
     if (int rc = alloc(&vcache, (size_t)c.layers * c.max_seq * kvd)) return rc;
     if (int rc = alloc(&trig, (size_t)c.max_seq * c.head_dim)) return rc;
@@ -258,10 +256,12 @@ int Model::enqueue_step(hipStream_t s) {
         WoArgs wa{wo->qs, wo->d, ACC, TMP, wo->m, wo->n};
         if (launch_wo_acc(wa, s)) return fail(ERR_SHAPE, "o projection: unsupported dim");
         const Weight *wg = weight(lname(l, "ffn_gate.weight")), *wu = weight(lname(l, "ffn_up.weight"));
-        GateArgs ga{wg->qs, wu->qs, wg->d, wu->d, nq_args(R0, TMP, vec(lname(l, "ffn_norm.weight")), R1),
-                    nullptr, XQH, XSH, c.hidden, c.dim};
-        if (launch_gateup_q(ga, s)) return fail(ERR_SHAPE, "gate/up: unsupported dim");
-        if (int rc = launch_matvec(*weight(lname(l, "ffn_down.weight")), nullptr, XQH, XSH, TMP, s)) return rc;
+        GateArgs ga{wg->qs, wu->qs, wg->d, wu->d, nq_args(R0, TMP, vec(lname(l, "ffn_norm.weight")), R1), GATE,
+                    c.hidden, c.dim};
+        if (launch_gateup_h(ga, s)) return fail(ERR_SHAPE, "gate/up: unsupported dim");
+        const Weight* wd = weight(lname(l, "ffn_down.weight"));
+        DownArgs da{wd->qs, wd->d, GATE, TMP, wd->m, wd->n};
+        if (launch_down_h(da, s)) return fail(ERR_SHAPE, "down: unsupported hidden size");
     }
     NormQuantArgs no = nq_args(R1, TMP, vec("output_norm.weight"), nullptr);
     no.xq = XQ;

@@ -91,11 +91,7 @@ template <bool GU>
 constexpr int gemm_lps() { return GU ? 7 : 5; }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 16, 0, 0);
-}
+__device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) { uq_lds_load16(g, lds_wave_base); }
 // rows r and r+16 (read by one ds_read2 of the two MFMA row tiles) get different slots
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
 

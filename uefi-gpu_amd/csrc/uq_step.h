@@ -22,14 +22,27 @@ struct QkvArgs {
     int dim, heads, kv_heads, head_dim;
 };
 
+// Gate/up of the decode FFN: h = silu(gate x) * (up x) in f32, with the
+// residual + RMSNorm + quant of the input in the prologue. One workgroup per
+// CU, rows split evenly over the grid.
 struct GateArgs {
     const int8_t *g_qs, *u_qs;
     const uint16_t *g_d, *u_d;
     NormQuantArgs nq;         // prologue: residual sum, RMSNorm, quant of the input
-    float* out;               // optional silu(g)*u [rows]
-    int8_t* oq;               // quantized output [rows]
-    float* os;                // [rows/32]
-    int64_t rows, k;          // rows % 32 == 0
+    float* h;                 // silu(g)*u [rows]
+    int64_t rows, k;
+    int64_t share;            // rows / grid, set by the launcher
+};
+
+// Down projection y = W quant(h): the block-32 quant of h happens in the
+// kernel's prologue, in the waves that have no rows to stream.
+struct DownArgs {
+    const int8_t* w_qs;
+    const uint16_t* w_d;
+    const float* h;           // [k]
+    float* y;                 // [rows]
+    int64_t rows, k;
+    int64_t share;            // rows / grid, set by the launcher
 };
 
 struct LmArgs {
@@ -71,12 +84,14 @@ struct WoArgs {
     const double* acc;        // [k]
     float* y;                 // [rows]
     int64_t rows, k;
+    int64_t share;            // rows / grid, set by the launcher
 };
 
 int launch_qkv_rope(const QkvArgs& a, hipStream_t s);
 int launch_attention_split(const AttSplitArgs& a, hipStream_t s);
 int launch_wo_acc(const WoArgs& a, hipStream_t s);
-int launch_gateup_q(const GateArgs& a, hipStream_t s);
+int launch_gateup_h(const GateArgs& a, hipStream_t s);
+int launch_down_h(const DownArgs& a, hipStream_t s);
 int launch_lm_greedy(const LmArgs& a, hipStream_t s);
 
 }  // namespace uq

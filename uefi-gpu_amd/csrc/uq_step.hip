@@ -26,6 +26,7 @@
 #include "uq_units.h"
 #include "uq_blockops.h"
 #include "uq_step.h"
+#include "uq_internal.h"
 
 namespace uq {
 namespace {
@@ -258,10 +259,11 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
         av[j] = i < K ? a.acc[i] : 0.0;
     }
     const WArgs w{a.w_qs, a.w_d, nullptr};
-    int64_t row0 = (int64_t)blockIdx.x * RPB;
+    const RowSpan sp = row_span<RPB>(a.rows, a.share);
+    int64_t row0 = sp.begin;
     Q8::W wv[NBL];
     {
-        const int64_t row = row0 + wave * RPW + grp, rr = row < a.rows ? row : a.rows - 1;
+        const int64_t row = row0 + wave * RPW + grp, rr = row < sp.end ? row : sp.end - 1;
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
@@ -282,6 +284,7 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
     Q8::X xr[NBL];
     load_xr<Q8, LPR, NBL>(xr, lq, ls, nu, sub);
     for (;;) {
+        if (row0 + wave * RPW >= sp.end) break;  // no row of this wave left (wave-uniform)
         const int64_t row = row0 + wave * RPW + grp;
         double acc = 0.0;
 #pragma unroll
@@ -291,10 +294,10 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
             acc += u < nu ? t : 0.0;
         }
         acc = uq_group_sum<LPR>(acc);
-        if (row < a.rows && sub == 0) a.y[row] = (float)acc;
-        row0 += (int64_t)gridDim.x * RPB;
-        if (row0 >= a.rows) break;
-        const int64_t nrow = row0 + wave * RPW + grp, rr = nrow < a.rows ? nrow : a.rows - 1;
+        if (row < sp.end && sub == 0) a.y[row] = (float)acc;
+        row0 += sp.step;
+        if (row0 >= sp.end) break;
+        const int64_t nrow = row0 + wave * RPW + grp, rr = nrow < sp.end ? nrow : sp.end - 1;
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
@@ -303,56 +306,124 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ gate/up + SiLU + quant
-// 32 consecutive rows per 1024-thread workgroup (two rows per wave), so the
-// block-32 quantization of the outputs stays inside the workgroup.
+// ------------------------------------------------------------------ decode FFN
+// Both FFN launches use one 1024-thread workgroup per CU with the rows split
+// evenly over the grid: a CU's share of a weight stream is bounded by its
+// share of HBM bandwidth, so a CU holding two workgroups would finish last and
+// set the kernel's duration. Waves that hold no rows do the prologue work
+// meanwhile: a wave stalls at issue while its CU's weight stream drains, so a
+// wave that also streams weights could not start its prologue until then.
+
+// Gate/up: 4 rows per wave (16 lanes per row), waves 0..14 hold rows, wave 15
+// runs the RMSNorm + quant prologue of the input.
+constexpr int GH_RPW = 4, GH_ROWS_MAX = 15 * GH_RPW;
 template <int NBL>
-__global__ __launch_bounds__(1024) void k_gateup_q(GateArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t sq[MAX_DIM];
-    __shared__ float ssc[MAX_DIM / 32];
-    __shared__ double red[16];
-    __shared__ float ys[32];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 31, grp = lane >> 5;
+__global__ __launch_bounds__(1024) void k_gateup_h(GateArgs a) {
+    constexpr int NC = NBL < MAX_DIM / 256 ? NBL : MAX_DIM / 256;  // dim <= 16 lanes x NBL units x 16
+    __shared__ __attribute__((aligned(16))) float lx[NC * 256];
+    __shared__ __attribute__((aligned(16))) float lr[NC * 256];
+    __shared__ __attribute__((aligned(16))) float lg[NC * 256];
+    __shared__ __attribute__((aligned(16))) int8_t sq[NC * 256];
+    __shared__ float ssc[NC * 8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
     const int64_t nu = a.k / Q8::UNIT;
-    const int64_t row = (int64_t)blockIdx.x * 32 + wave * 2 + grp;
+    const RowSpan sp = even_span(a.rows, a.share);
+    const int64_t lo = sp.begin, hi = sp.end;
+    const bool rows_wave = wave < 15 && wave * GH_RPW < hi - lo;  // wave-uniform
+    const int64_t row = lo + wave * GH_RPW + grp, rr = row < hi ? row : hi - 1;
     const WArgs wg{a.g_qs, a.g_d, nullptr}, wu{a.u_qs, a.u_d, nullptr};
-    NqRegsFor<1024, NBL * 32 * Q8::UNIT> nqv;  // dim <= 32 lanes x NBL units x 16
-    norm_quant_load<1024>(a.nq, nqv);  // activations first: the prologue waits only for them
+    NormQuantWave<NC> nw;
+    if (wave == 15) nw.issue(a.nq, lx, lr, lg);
+    uq_issue_barrier();  // the prologue's loads are queued before any weight load of this CU
+    if (wave == 15) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
     Q8::W gw[NBL], uw[NBL];
+    if (rows_wave) {
 #pragma unroll
-    for (int i = 0; i < NBL; i++) {
-        const int u = sub + 32 * i;
-        if (u < nu) {
-            gw[i] = Q8::load_w(wg, row, nu, u);
-            uw[i] = Q8::load_w(wu, row, nu, u);
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + 16 * i, uc = u < nu ? u : (int)nu - 1;
+            gw[i] = Q8::load_w(wg, rr, nu, uc);
+            uw[i] = Q8::load_w(wu, rr, nu, uc);
         }
     }
-    norm_quant_finish<1024>(a.nq, nqv, blockIdx.x == 0, sq, ssc, red);
+    __syncthreads();
+    if (!rows_wave) return;
     double g = 0.0, uacc = 0.0;
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
-        const int u = sub + 32 * i;
-        if (u < nu) {
-            Q8::X x;
-            x.a = *(const int4*)(sq + 16 * u);
-            x.s = ssc[u >> 1];
-            g += Q8::dot(gw[i], x);
-            uacc += Q8::dot(uw[i], x);
+        const int u = sub + 16 * i, uc = u < nu ? u : (int)nu - 1;
+        Q8::X x;
+        x.a = *(const int4*)(sq + 16 * uc);
+        x.s = ssc[uc >> 1];
+        const double tg = Q8::dot(gw[i], x), tu = Q8::dot(uw[i], x);
+        g += u < nu ? tg : 0.0;
+        uacc += u < nu ? tu : 0.0;
+    }
+    g = uq_group_sum<16>(g);
+    uacc = uq_group_sum<16>(uacc);
+    if (sub == 0 && row < hi) a.h[row] = uq_silu_mul((float)g, (float)uacc);
+}
+
+// Down: one row per wave (64 lanes per row) in waves 0..RW-1, RW = rows per
+// workgroup (the same in every workgroup, <= 14); waves RW..15 pull h into
+// LDS by DMA and quantize it per 32 (the quant of quant_act, element i =
+// 256*c + 4*lane + j, a block = 8 lanes).
+constexpr int DH_ROWS_MAX = 14;
+template <int NBL>
+__global__ __launch_bounds__(1024) void k_down_h(DownArgs a) {
+    constexpr int MAXK = NBL * 64 * Q8::UNIT;
+    __shared__ __attribute__((aligned(16))) float lh[MAXK];
+    __shared__ __attribute__((aligned(16))) int8_t sq[MAXK];
+    __shared__ float ssc[MAXK / 32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t nu = a.k / Q8::UNIT, K = a.k;
+    const RowSpan sp = even_span(a.rows, a.share);
+    const int64_t lo = sp.begin, hi = sp.end;
+    const int RW = (int)(a.share + (a.rows > a.share * (int64_t)gridDim.x ? 1 : 0));  // rows of the largest share
+    const int64_t row = lo + wave, rr = row < hi ? row : hi - 1;
+    const int P = 16 - RW, pw = wave - RW, nch = (int)((K + 255) / 256);
+    if (wave >= RW)
+        for (int c = pw; c < nch; c += P) {
+            const int64_t i = 256 * (int64_t)c + 4 * lane, ic = i < K ? i : K - 4;
+            uq_lds_load16(a.h + ic, lh + 256 * c);
+        }
+    uq_issue_barrier();  // h's loads are queued before any weight load of this CU
+    Q8::W wv[NBL];
+    if (wave < RW) {
+        const WArgs w{a.w_qs, a.w_d, nullptr};
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = lane + 64 * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = Q8::load_w(w, rr, nu, uc);
+        }
+    } else {
+        uq_wait_vm0();
+        asm volatile("" ::: "memory");
+        for (int c = pw; c < nch; c += P) {
+            const int64_t i = 256 * (int64_t)c + 4 * lane;
+            const float4 v4 = ((const float4*)lh)[64 * c + lane];
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            uint32_t packed;
+            const float sc = uq_quant4_group8(v, &packed);
+            if (i < K) {
+                *(uint32_t*)(sq + i) = packed;
+                if ((lane & 7) == 0) ssc[i >> 5] = sc;
+            }
         }
     }
-    g = uq_group_sum<32>(g);
-    uacc = uq_group_sum<32>(uacc);
-    if (sub == 0) ys[wave * 2 + grp] = uq_silu_mul((float)g, (float)uacc);
     __syncthreads();
-    if (threadIdx.x < 32) {
-        const float v = ys[threadIdx.x];
-        const int64_t r = (int64_t)blockIdx.x * 32 + threadIdx.x;
-        if (a.out) a.out[r] = v;
-        float s;
-        const int8_t q = uq_quant_lane(v, &s);
-        a.oq[r] = q;
-        if (threadIdx.x == 0) a.os[blockIdx.x] = s;
+    if (wave >= RW || row >= hi) return;
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < NBL; i++) {
+        const int u = lane + 64 * i, uc = u < nu ? u : (int)nu - 1;
+        Q8::X x;
+        x.a = *(const int4*)(sq + 16 * uc);
+        x.s = ssc[uc >> 1];
+        const double t = Q8::dot(wv[i], x);
+        acc += u < nu ? t : 0.0;
     }
+    acc = uq_group_sum<64>(acc);
+    if (lane == 0) a.y[row] = (float)acc;
 }
 
 // ------------------------------------------------------------------ lm_head + argmax partials
@@ -436,7 +507,8 @@ int pick_nbl(int64_t nu, dim3 grid, dim3 block, size_t lds, hipStream_t s, const
 }
 template <int LPR, int NBL> struct LmArgmax { static constexpr auto fn = k_lm_argmax<LPR, NBL>; };
 template <int LPR, int NBL> struct QkvRope { static constexpr auto fn = k_qkv_rope<NBL>; };
-template <int LPR, int NBL> struct GateUpQ { static constexpr auto fn = k_gateup_q<NBL>; };
+template <int LPR, int NBL> struct GateUpH { static constexpr auto fn = k_gateup_h<NBL>; };
+
 
 int step_lpr(int64_t k) { return k / Q8::UNIT <= 256 ? 32 : 64; }
 
@@ -472,13 +544,36 @@ template <int LPR, int NBL> struct WoAcc { static constexpr auto fn = k_wo_acc<L
 int launch_wo_acc(const WoArgs& a, hipStream_t s) {
     if (a.k > MAX_DIM || a.k % 32) return -1;
     constexpr int RPB = 4 * (64 / 32);
-    const int64_t sets = (a.rows + RPB - 1) / RPB;
-    const unsigned grid = (unsigned)(sets < 2048 ? sets : 2048);
-    return pick_nbl<32, WoAcc>(a.k / Q8::UNIT, dim3(grid), dim3(256), 0, s, a);
+    const int64_t cu = cu_count(), m = (a.rows + cu * RPB - 1) / (cu * RPB);
+    int64_t g = m * cu;
+    if (g > 2048) g = 2048;
+    if (g > a.rows) g = a.rows;
+    const unsigned grid = (unsigned)g;
+    WoArgs b = a;
+    b.share = a.rows / g;
+    return pick_nbl<32, WoAcc>(a.k / Q8::UNIT, dim3(grid), dim3(256), 0, s, b);
 }
-int launch_gateup_q(const GateArgs& a, hipStream_t s) {
-    if (a.k > MAX_DIM || a.rows % 32) return -1;
-    return pick_nbl<32, GateUpQ>(a.k / Q8::UNIT, dim3((unsigned)(a.rows / 32)), dim3(1024), 0, s, a);
+int launch_gateup_h(const GateArgs& a, hipStream_t s) {
+    if (a.k > MAX_DIM || a.k % 32 || a.nq.dim != a.k || a.rows <= 0) return -1;
+    int64_t g = cu_count();
+    if (g > a.rows) g = a.rows;
+    if ((a.rows + g - 1) / g > GH_ROWS_MAX) g = (a.rows + GH_ROWS_MAX - 1) / GH_ROWS_MAX;
+    GateArgs b = a;
+    b.share = a.rows / g;
+    return pick_nbl<16, GateUpH>(a.k / Q8::UNIT, dim3((unsigned)g), dim3(1024), 0, s, b);
+}
+int launch_down_h(const DownArgs& a, hipStream_t s) {
+    if (a.k % 32 || a.k > 9 * 64 * Q8::UNIT || a.rows <= 0) return -1;
+    int64_t g = cu_count();
+    if (g > a.rows) g = a.rows;
+    if ((a.rows + g - 1) / g > DH_ROWS_MAX) g = (a.rows + DH_ROWS_MAX - 1) / DH_ROWS_MAX;
+    const int64_t nu = a.k / Q8::UNIT;
+    DownArgs b = a;
+    b.share = a.rows / g;
+    if (nu <= 64 * 3) { hipLaunchKernelGGL(k_down_h<3>, dim3((unsigned)g), dim3(1024), 0, s, b); return 0; }
+    if (nu <= 64 * 6) { hipLaunchKernelGGL(k_down_h<6>, dim3((unsigned)g), dim3(1024), 0, s, b); return 0; }
+    hipLaunchKernelGGL(k_down_h<9>, dim3((unsigned)g), dim3(1024), 0, s, b);
+    return 0;
 }
 int launch_lm_greedy(const LmArgs& a, hipStream_t s) {
     const int lpr = step_lpr(a.k);

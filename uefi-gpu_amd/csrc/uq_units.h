@@ -254,6 +254,32 @@ struct Q3K {
     }
 };
 
+// Rows of this workgroup. When one pass of the grid covers every row, each
+// workgroup takes an even contiguous share (one pass), so every CU streams
+// the same number of rows: a CU's stream rate is its share of HBM bandwidth,
+// and a CU with more rows than the others would set the kernel's duration.
+// share = rows / gridDim.x comes from the host (a 64-bit division on the
+// device costs hundreds of instructions ahead of the first weight load); the
+// first rows % gridDim.x workgroups take one row more. Otherwise the grid
+// strides over passes of RPB rows.
+struct RowSpan {
+    int64_t begin, end, step;
+};
+__device__ __forceinline__ RowSpan even_span(int64_t rows, int64_t share) {
+    const int64_t b = blockIdx.x, extra = rows - share * (int64_t)gridDim.x;
+    const int64_t begin = b * share + (b < extra ? b : extra);
+    return RowSpan{begin, begin + share + (b < extra ? 1 : 0), share + 1};
+}
+template <int RPB>
+__device__ __forceinline__ RowSpan row_span(int64_t rows, int64_t share) {
+    if (rows <= (int64_t)gridDim.x * RPB) {
+        RowSpan r = even_span(rows, share);
+        r.step = RPB;
+        return r;
+    }
+    return RowSpan{(int64_t)blockIdx.x * RPB, rows, (int64_t)gridDim.x * RPB};
+}
+
 // Activation units of one lane (units sub, sub+LPR, ...) kept in registers.
 // Loads are issued unconditionally (a unit past the row end reads the last
 // unit) and zeroed afterwards, so they all go out before the first wait.

@@ -253,9 +253,11 @@ template <class KQ, int LPR, int NBL, bool GATEUP>
 __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, float* __restrict__ y,
                                                   int64_t rows, int64_t K, int64_t share) {
-    __shared__ __attribute__((aligned(16))) int8_t lx[MAX_XL];
-    __shared__ float lxs[MAX_XL / 32];
-    __shared__ int ls16[MAX_XL / 16];
+    // dynamic LDS sized to K (xl_lds_bytes): x (K int8), its scales (K/32 f32), its 16-value sums (K/16 int)
+    extern __shared__ __attribute__((aligned(16))) int8_t xl_lds[];
+    int8_t* lx = xl_lds;
+    float* lxs = (float*)(xl_lds + K);
+    int* ls16 = (int*)(xl_lds + K + K / 8);
     constexpr int RPW = 64 / LPR;
     constexpr int RPB = RPW * (WG / 64);
     const int64_t nu = K / KQ::UNIT;
@@ -328,22 +330,45 @@ inline unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)((items + per_block - 1) / per_block);
 }
 
+inline size_t xl_lds_bytes(int64_t K) { return (size_t)K + (size_t)K / 8 + (size_t)K / 4; }
+
+// Workgroups of `kern` (WG threads, `lds` dynamic LDS bytes) resident per CU,
+// from the runtime's occupancy query, cached per kernel and LDS size.
+int resident_blocks(const void* kern, size_t lds) {
+    struct Entry { const void* k; size_t lds; int n; };
+    static Entry cache[64];
+    static int used = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].k == kern && cache[i].lds == lds) return cache[i].n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, WG, lds) != hipSuccess || n <= 0) n = 1;
+    if (n > 8) n = 8;
+    if (used < 64) cache[used++] = Entry{kern, lds, n};
+    return n;
+}
+
 template <class KQ, int LPR, int NBL, bool XL = false>
 void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
     constexpr int RPB = (64 / LPR) * (WG / 64);
+    const size_t lds = XL ? xl_lds_bytes(w.n) : 0;
+    const void* kern;
+    if constexpr (XL) kern = w2 ? (const void*)k_matvec_xl<KQ, LPR, NBL, true> : (const void*)k_matvec_xl<KQ, LPR, NBL, false>;
+    else kern = w2 ? (const void*)k_matvec<KQ, LPR, NBL, true> : (const void*)k_matvec<KQ, LPR, NBL, false>;
     // a multiple of the CU count with at most one pass of rows per workgroup,
-    // or 2048 workgroups striding over the rows
+    // or as many workgroups as fit on the chip at once striding over the rows
+    // (a grid beyond that would run its last workgroups as a second wave)
     const int64_t cu = cu_count(), m = (w.m + cu * RPB - 1) / (cu * RPB);
+    const int64_t fit = cu * resident_blocks(kern, lds);
     int64_t g = m * cu;
-    if (g > 2048) g = 2048;
+    if (g > fit) g = fit;
     if (g > w.m) g = w.m;
     const unsigned grid = (unsigned)g;
     const int64_t share = w.m / g;
     WArgs a{w.qs, w.d, w.sc}, b{nullptr, nullptr, nullptr};
     if (w2) b = WArgs{w2->qs, w2->d, w2->sc};
     if constexpr (XL) {
-        if (w2) hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
-        else hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
+        if (w2) hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), lds, s, a, b, xq, xs, y, w.m, w.n, share);
+        else hipLaunchKernelGGL((k_matvec_xl<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), lds, s, a, b, xq, xs, y, w.m, w.n, share);
     } else {
         if (w2) hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, true>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);
         else hipLaunchKernelGGL((k_matvec<KQ, LPR, NBL, false>), dim3(grid), dim3(WG), 0, s, a, b, xq, xs, y, w.m, w.n, share);

@@ -29,6 +29,8 @@ UQ_DEV void uq_issue_barrier() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
+// a * b for |a|, |b| < 2^23 whose product fits in 32 bits (v_mul_i32_i24, full rate)
+UQ_DEV int uq_mul24(int a, int b) { return __mul24(a, b); }
 UQ_DEV float uq_half(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 UQ_DEV uint16_t uq_f16_rne(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 

@@ -169,11 +169,14 @@ __device__ __forceinline__ void matvec_row(const WArgs& w, const WArgs& w2, cons
     // rows past the end load the last row; every lane takes part in the reductions
     const int64_t rr = row < end ? row : end - 1;
     typename KQ::W wv[NBL], wv2[NBL];
+    const typename KQ::R rp = KQ::row_ptr(w, rr, nu);
+    typename KQ::R rp2{};
+    if (GATEUP) rp2 = KQ::row_ptr(w2, rr, nu);
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-        wv[i] = KQ::load_w(w, rr, nu, uc);
-        if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
+        wv[i] = KQ::load_u(rp, uc);
+        if (GATEUP) wv2[i] = KQ::load_u(rp2, uc);
     }
     double acc = 0.0, acc2 = 0.0;
 #pragma unroll
@@ -221,11 +224,14 @@ __device__ __forceinline__ void matvec_row_lds(const WArgs& w, const WArgs& w2, 
                                                int sub) {
     const int64_t rr = row < end ? row : end - 1;
     typename KQ::W wv[NBL], wv2[NBL];
+    const typename KQ::R rp = KQ::row_ptr(w, rr, nu);
+    typename KQ::R rp2{};
+    if (GATEUP) rp2 = KQ::row_ptr(w2, rr, nu);
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
-        wv[i] = KQ::load_w(w, rr, nu, uc);
-        if (GATEUP) wv2[i] = KQ::load_w(w2, rr, nu, uc);
+        wv[i] = KQ::load_u(rp, uc);
+        if (GATEUP) wv2[i] = KQ::load_u(rp2, uc);
     }
     double acc = 0.0, acc2 = 0.0;
 #pragma unroll

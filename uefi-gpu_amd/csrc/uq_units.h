@@ -31,11 +31,14 @@ struct Q8 {
     }
     static UQ_DEV void zero_x(X& x) { x.a = make_int4(0, 0, 0, 0); x.s = 0.0f; }
     struct W { int4 q; uint16_t d; };
-    // weight part of a unit, loadable before the activations are known
-    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
-        const int64_t piece = row * nu + u;
-        return W{uq_ntload16(w.qs + piece * 16), w.d[piece >> 1]};
+    // row base pointers, formed once per row (nu is even: K % 32 == 0)
+    struct R { const int8_t* q; const uint16_t* d; };
+    static UQ_DEV R row_ptr(const WArgs& w, int64_t row, int64_t nu) {
+        return R{w.qs + row * nu * 16, w.d + row * (nu >> 1)};
     }
+    // weight part of unit u of the row, loadable before the activations are known
+    static UQ_DEV W load_u(const R& r, int u) { return W{uq_ntload16(r.q + (int64_t)u * 16), r.d[u >> 1]}; }
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) { return load_u(row_ptr(w, row, nu), u); }
     static UQ_DEV double dot(const W& wv, const X& x, int = 0) {
         int c = uq_dot4(wv.q.x, x.a.x, 0);
         c = uq_dot4(wv.q.y, x.a.y, c);
@@ -92,13 +95,19 @@ struct Q4K {
     static UQ_DEV int lo4(int w) { return w & 0x0F0F0F0F; }
     static UQ_DEV int hi4(int w) { return (int)(((unsigned)w >> 4) & 0x0F0F0F0Fu); }
     struct W { int4 q0, q1; uint32_t scm, dm; };
-    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
-        const int64_t sb = (row * nu + u) >> 2;  // nu = 4 * superblocks per row
-        const int j = u & 3;
-        const uint8_t* q = (const uint8_t*)w.qs + row * nu * 32 + (int64_t)u * 16;
-        const uint32_t scm = ((const uint32_t*)w.sc)[4 * sb + j];
-        return W{uq_ntload16(q), uq_ntload16(q + nu * 16), scm, ((const uint32_t*)w.d)[sb]};
+    // row base pointers (nu = 4 * superblocks per row): the nibble plane row,
+    // its second halves nu*16 bytes on, one scm word per unit, one dm word per
+    // superblock
+    struct R { const uint8_t* q; int64_t half; const uint32_t* scm; const uint32_t* dm; };
+    static UQ_DEV R row_ptr(const WArgs& w, int64_t row, int64_t nu) {
+        return R{(const uint8_t*)w.qs + row * nu * 32, nu * 16, (const uint32_t*)w.sc + row * nu,
+                 (const uint32_t*)w.d + row * (nu >> 2)};
     }
+    static UQ_DEV W load_u(const R& r, int u) {
+        const uint8_t* q = r.q + (int64_t)u * 16;
+        return W{uq_ntload16(q), uq_ntload16(q + r.half), r.scm[u], r.dm[u >> 2]};
+    }
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) { return load_u(row_ptr(w, row, nu), u); }
     static UQ_DEV double dot(const W& wv, const X& x, int = 0) {
         const int4 q0 = wv.q0, q1 = wv.q1;
         int il = 0, ih = 0;
@@ -116,8 +125,9 @@ struct Q4K {
         const double dm = (double)uq_half((uint16_t)(wv.dm >> 16));
         const int sc0 = (int)(wv.scm & 0xff), sc1 = (int)((wv.scm >> 8) & 0xff);
         const int m0 = (int)((wv.scm >> 16) & 0xff), m1 = (int)(wv.scm >> 24);
-        const double t0 = x.s0 * (dd * (double)(sc0 * il) - dm * (double)(m0 * x.xl));
-        const double t1 = x.s1 * (dd * (double)(sc1 * ih) - dm * (double)(m1 * x.xh));
+        // 24-bit multiplies (full rate): |sc|, |m| <= 63, |il| <= 61,440, |xl| <= 4,064
+        const double t0 = x.s0 * (dd * (double)uq_mul24(sc0, il) - dm * (double)uq_mul24(m0, x.xl));
+        const double t1 = x.s1 * (dd * (double)uq_mul24(sc1, ih) - dm * (double)uq_mul24(m1, x.xh));
         return t0 + t1;
     }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
@@ -191,14 +201,20 @@ struct Q3K {
                          v3((uint32_t)q.z, (uint32_t)h.z, sq, rot), v3((uint32_t)q.w, (uint32_t)h.w, sq, rot));
     }
     struct W { int4 h0, h1, q0, q1; uint32_t sc0, sc1; uint16_t d; };
-    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) {
-        const int64_t sb = (row * nu + u) >> 1;  // nu = 2 * superblocks per row
-        const int n = u & 1;
-        const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
-        const uint8_t* q = blk + 32 + 32 * n;
-        const uint2 sc = *(const uint2*)(w.sc + sb * 16 + 8 * n);
-        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sc.x, sc.y, w.d[sb]};
+    // row base pointers (nu = 2 * superblocks per row)
+    struct R { const uint8_t* blk; const uint8_t* sc; const uint16_t* d; };
+    static UQ_DEV R row_ptr(const WArgs& w, int64_t row, int64_t nu) {
+        const int64_t sb0 = row * (nu >> 1);
+        return R{(const uint8_t*)w.qs + sb0 * 96, w.sc + sb0 * 16, w.d + sb0};
     }
+    static UQ_DEV W load_u(const R& r, int u) {
+        const int sb = u >> 1, n = u & 1;
+        const uint8_t* blk = r.blk + sb * 96;
+        const uint8_t* q = blk + 32 + 32 * n;
+        const uint2 sc = *(const uint2*)(r.sc + sb * 16 + 8 * n);
+        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sc.x, sc.y, r.d[sb]};
+    }
+    static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) { return load_u(row_ptr(w, row, nu), u); }
     // d*(s-32) is exact in f32 (11-bit x 6-bit), so the block's
     // (d*s0)*i0 + (d*s1)*i1 equals d*(s0*i0 + s1*i1) with an exact integer sum
     static UQ_DEV double dot(const W& wv, const X& x, int u) {
@@ -213,7 +229,8 @@ struct Q3K {
             const int i1 = dot16(w1, x.v[2 * j + 1], 0) - 4 * x.sx[2 * j + 1];
             const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
             const int b = 16 * (j & 1);
-            const int t = (int)(int8_t)(scw >> b) * i0 + (int)(int8_t)(scw >> (b + 8)) * i1;
+            // 24-bit multiplies (full rate): |s| <= 32, |i| <= 16 * 7 * 128
+            const int t = uq_mul24((int)(int8_t)(scw >> b), i0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), i1);
             acc += x.s[j] * (dd * (double)t);
         }
         return acc;
@@ -241,7 +258,8 @@ struct Q3K {
             const int i1 = dot16(w1, xb, 0) - 4 * sb;
             const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
             const int b = 16 * (j & 1);
-            const int t = (int)(int8_t)(scw >> b) * i0 + (int)(int8_t)(scw >> (b + 8)) * i1;
+            // 24-bit multiplies (full rate): |s| <= 32, |i| <= 16 * 7 * 128
+            const int t = uq_mul24((int)(int8_t)(scw >> b), i0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), i1);
             acc += xsj * (dd * (double)t);
         }
         return acc;
@@ -300,10 +318,11 @@ UQ_DEV void load_xr(typename KQ::X* xr, const int8_t* xq, const float* xs, int64
 template <class KQ, int LPR, int NBL>
 UQ_DEV double row_dot(const WArgs& w, int64_t row, int64_t nu, int sub, const typename KQ::X* xr) {
     typename KQ::W wv[NBL];
+    const typename KQ::R rp = KQ::row_ptr(w, row, nu);
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
         const int u = sub + LPR * i;
-        wv[i] = KQ::load_w(w, row, nu, u < nu ? u : (int)nu - 1);
+        wv[i] = KQ::load_u(rp, u < nu ? u : (int)nu - 1);
     }
     double acc = 0.0;
 #pragma unroll

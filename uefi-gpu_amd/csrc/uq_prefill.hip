@@ -310,100 +310,196 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(PfRopeArgs a) {
 }
 
 // ------------------------------------------------------------------ causal attention
-// Workgroup = (query head, tile of QT consecutive queries); 32 threads per query.
-// Same arithmetic as decode attention: scores in double, * 1/sqrt(hd),
-// max-subtracted exp, total in double, p = e/total, P.V in double.
-constexpr int QT = 8;
+// Workgroup = (query head, tile of 16 consecutive queries), 4 waves. Same
+// arithmetic as decode attention: q.k in double (each product f32 x fp16 is
+// exact in double), * 1/sqrt(hd) in f32, max-subtracted exp, total in double,
+// p = e/total, P.V in double. Both contractions run on the FP64 MFMA
+// v_mfma_f64_16x16x4_f64 (D += A B, A 16x4, B 4x16): lane l holds A[l%16][l/16]
+// and B[l/16][l%16], and register r of lane l holds D[4r + l/16][l%16].
+//   q.k: A = Q (16 queries x 4 dims), B = K^T (4 dims x 16 keys); lane group
+//        g = l/16 takes dims [g*HD/4, (g+1)*HD/4), one per MFMA step, so each
+//        lane's q and k pieces are contiguous. Waves take key tiles of 16 in turn.
+//   P.V: A = P (16 queries x 4 keys) from LDS, B = V (4 keys x 16 dims); each
+//        wave owns HD/64 tiles of 16 dims.
+// The double sums run in MFMA order instead of the oracle's sequential order;
+// every term is exact, so the f32 results agree except when a double sum
+// lands within an ulp of an f32 rounding boundary.
+constexpr int PA_Q = 16;
 template <int HD>
 __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
-    extern __shared__ float scs[];  // [QT][kmax]
-    __shared__ double qd[QT][HD];
-    const int tid = threadIdx.x, qi = tid >> 5, kj = tid & 31;
+    extern __shared__ float ps[];  // [PA_Q][sst]: scores, then p (0 past each query's causal end)
+    constexpr int DG = HD / 4;     // dims per lane group in q.k
+    constexpr int DT = HD / 64;    // 16-dim tiles per wave in P.V
+    typedef double d4 __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
     const int h = blockIdx.x, kh = h / (a.heads / a.kv_heads), kvd = a.kv_heads * HD;
-    const int tq0 = blockIdx.y * QT;                 // first query (token index)
-    const int kmax = a.p0 + tq0 + QT;                // keys covered by this tile (exclusive bound)
-    for (int e = tid; e < QT * HD; e += 256) {
-        const int qq = e / HD, d = e % HD;
-        const int t = tq0 + qq;
-        qd[qq][d] = t < a.n ? (double)a.qkv[(size_t)t * a.stride + h * HD + d] : 0.0;
+    // the longest query tiles (most keys) are dispatched first
+    const int tq0 = (gridDim.y - 1 - blockIdx.y) * PA_Q;
+    const int nq = a.n - tq0 < PA_Q ? a.n - tq0 : PA_Q;  // live queries of the tile
+    const int sst = (a.p0 + a.n + 15) & ~15;              // LDS row stride (keys)
+    const int kend = a.p0 + tq0 + nq;                     // keys needed by the tile: [0, kend)
+    const int kpad = (kend + 3) & ~3;                     // P.V runs over whole 4-key steps
+    // q operand: query c of the tile, dims [g*DG, (g+1)*DG) as doubles
+    double qa[DG];
+    {
+        const bool qlive = c < nq;
+        const float* qr = a.qkv + (size_t)(tq0 + (qlive ? c : 0)) * a.stride + h * HD + g * DG;
+#pragma unroll
+        for (int i = 0; i < DG; i += 4) {
+            const float4 v = *(const float4*)(qr + i);
+            qa[i] = qlive ? (double)v.x : 0.0;
+            qa[i + 1] = qlive ? (double)v.y : 0.0;
+            qa[i + 2] = qlive ? (double)v.z : 0.0;
+            qa[i + 3] = qlive ? (double)v.w : 0.0;
+        }
+    }
+    // scores of key tiles kt = wave, wave + 4, ...; the next tile's K is
+    // loaded before the current tile's MFMAs
+    const int ntile = (kend + 15) >> 4;
+    auto load_k = [&](int kt, uint32_t* kw) {
+        int key = kt * 16 + c;
+        key = key < a.kcap ? key : a.kcap - 1;
+        const uint16_t* kr = a.kcache + (size_t)key * kvd + kh * HD + g * DG;
+#pragma unroll
+        for (int i = 0; i < DG / 8; i++) {
+            const int4 v = *(const int4*)(kr + 8 * i);
+            kw[4 * i] = (uint32_t)v.x;
+            kw[4 * i + 1] = (uint32_t)v.y;
+            kw[4 * i + 2] = (uint32_t)v.z;
+            kw[4 * i + 3] = (uint32_t)v.w;
+        }
+    };
+    // four independent accumulator chains (steps i mod 4), summed at the end
+    auto score_tile = [&](int kt, const uint32_t* kw) {
+        d4 acc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[k] = d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int i = 0; i < DG; i++) {
+            const uint16_t hk = (uint16_t)(i & 1 ? kw[i >> 1] >> 16 : kw[i >> 1] & 0xffff);
+            acc[i & 3] = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[i], (double)uq_half(hk), acc[i & 3], 0, 0, 0);
+        }
+        const d4 sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) ps[(4 * r + g) * sst + kt * 16 + c] = (float)sum[r] * a.qscale;
+    };
+    {
+        uint32_t ka[DG / 2], kb[DG / 2];
+        int kt = wave;
+        if (kt < ntile) load_k(kt, ka);
+        // sched_barrier: the scheduler would otherwise sink the prefetch below the MFMAs
+        while (kt < ntile) {
+            if (kt + 4 < ntile) load_k(kt + 4, kb);
+            __builtin_amdgcn_sched_barrier(0);
+            score_tile(kt, ka);
+            kt += 4;
+            if (kt >= ntile) break;
+            if (kt + 4 < ntile) load_k(kt + 4, ka);
+            __builtin_amdgcn_sched_barrier(0);
+            score_tile(kt, kb);
+            kt += 4;
+        }
     }
     __syncthreads();
-    const int tq = tq0 + qi;
-    const bool live = tq < a.n;
-    const int T = a.p0 + tq + 1;                     // causal: keys [0, T)
-    float* sc = scs + qi * a.kcap;
-    float mx = -3.402823466e38f;
-    if (live) {
-        for (int t = kj; t < T; t += 32) {
-            const uint16_t* kr = a.kcache + (size_t)t * kvd + kh * HD;
-            double acc = 0.0;
-            for (int d = 0; d < HD; d += 8) {
-                const int4 kk = *(const int4*)(kr + d);
-                const uint32_t w[4] = {(uint32_t)kk.x, (uint32_t)kk.y, (uint32_t)kk.z, (uint32_t)kk.w};
+    // softmax: 16 lanes per query (query tid/16 of the tile), 4 consecutive
+    // keys per lane per LDS read; keys past the causal end become p = 0
+    {
+        const int qi = tid >> 4, cj = tid & 15;
+        const int T = qi < nq ? a.p0 + tq0 + qi + 1 : 0;  // causal: keys [0, T)
+        float* sr = ps + qi * sst;
+        float mx = -3.402823466e38f;
+        for (int t0 = 4 * cj; t0 < T; t0 += 64) {
+            const float4 v = *(const float4*)(sr + t0);
+            mx = fmaxf(mx, v.x);
+            if (t0 + 1 < T) mx = fmaxf(mx, v.y);
+            if (t0 + 2 < T) mx = fmaxf(mx, v.z);
+            if (t0 + 3 < T) mx = fmaxf(mx, v.w);
+        }
+        mx = uq_group_max<16>(mx);
+        double tot = 0.0;
+        for (int t0 = 4 * cj; t0 < T; t0 += 64) {
+            const float4 v = *(const float4*)(sr + t0);
+            const float e0 = uq_expf(v.x - mx);
+            const float e1 = t0 + 1 < T ? uq_expf(v.y - mx) : 0.0f;
+            const float e2 = t0 + 2 < T ? uq_expf(v.z - mx) : 0.0f;
+            const float e3 = t0 + 3 < T ? uq_expf(v.w - mx) : 0.0f;
+            *(float4*)(sr + t0) = make_float4(e0, e1, e2, e3);
+            tot += (double)e0;
+            tot += (double)e1;
+            tot += (double)e2;
+            tot += (double)e3;
+        }
+        tot = uq_group_sum<16>(tot);
+        const float total = (float)tot;
+        for (int t0 = 4 * cj; t0 < kpad; t0 += 64) {
+            const float4 v = *(const float4*)(sr + t0);
+            const float p0 = t0 < T ? v.x / total : 0.0f;
+            const float p1 = t0 + 1 < T ? v.y / total : 0.0f;
+            const float p2 = t0 + 2 < T ? v.z / total : 0.0f;
+            const float p3 = t0 + 3 < T ? v.w / total : 0.0f;
+            *(float4*)(sr + t0) = make_float4(p0, p1, p2, p3);
+        }
+    }
+    __syncthreads();
+    // P.V: this wave's dim tiles d0 = (wave * DT + j) * 16
+    d4 o[DT];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    acc = __builtin_fma(qd[qi][d + 2 * i], (double)uq_half((uint16_t)(w[i] & 0xffff)), acc);
-                    acc = __builtin_fma(qd[qi][d + 2 * i + 1], (double)uq_half((uint16_t)(w[i] >> 16)), acc);
-                }
+    for (int j = 0; j < DT; j++) o[j] = d4{0.0, 0.0, 0.0, 0.0};
+    const float* pr = ps + c * sst;  // A row: query c
+    const uint16_t* vb = a.vcache + kh * HD + wave * DT * 16 + c;
+    // batches of SU 4-key steps in a two-stage register pipeline: the next
+    // batch's P and V loads are issued before the current batch's MFMAs
+    constexpr int SU = 8;
+    struct PvBatch { double p[SU]; uint16_t v[SU][DT]; };
+    auto load_pv = [&](int k0, PvBatch& bt) {
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int kk = k0 + 4 * u + g;
+            const int kl = kk < kpad ? kk : kpad - 1;
+            const int kv = kl < a.kcap ? kl : a.kcap - 1;
+            bt.p[u] = kk < kpad ? (double)pr[kl] : 0.0;
+#pragma unroll
+            for (int j = 0; j < DT; j++) bt.v[u][j] = vb[(size_t)kv * kvd + j * 16];
+        }
+    };
+    // two accumulator chains per dim tile (even and odd steps), summed at the end
+    d4 o2[DT];
+#pragma unroll
+    for (int j = 0; j < DT; j++) o2[j] = d4{0.0, 0.0, 0.0, 0.0};
+    auto mma_pv = [&](const PvBatch& bt) {
+#pragma unroll
+        for (int u = 0; u < SU; u += 2)
+#pragma unroll
+            for (int j = 0; j < DT; j++) {
+                o[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(bt.p[u], (double)uq_half(bt.v[u][j]), o[j], 0, 0, 0);
+                o2[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(bt.p[u + 1], (double)uq_half(bt.v[u + 1][j]), o2[j], 0, 0, 0);
             }
-            const float s = (float)acc * a.qscale;
-            sc[t] = s;
-            mx = fmaxf(mx, s);
+    };
+    {
+        PvBatch ba, bb;
+        int k0 = 0;
+        if (k0 < kpad) load_pv(k0, ba);
+        while (k0 < kpad) {
+            if (k0 + 4 * SU < kpad) load_pv(k0 + 4 * SU, bb);
+            __builtin_amdgcn_sched_barrier(0);
+            mma_pv(ba);
+            k0 += 4 * SU;
+            if (k0 >= kpad) break;
+            if (k0 + 4 * SU < kpad) load_pv(k0 + 4 * SU, ba);
+            __builtin_amdgcn_sched_barrier(0);
+            mma_pv(bb);
+            k0 += 4 * SU;
         }
     }
-    mx = uq_group_max<32>(mx);
-    double tot = 0.0;
-    if (live)
-        for (int t = kj; t < T; t += 32) {
-            const float ev = uq_expf(sc[t] - mx);
-            sc[t] = ev;
-            tot += (double)ev;
-        }
-    tot = uq_group_sum<32>(tot);
-    const float total = (float)tot;
-    if (live)
-        for (int t = kj; t < T; t += 32) sc[t] = sc[t] / total;
-    __syncthreads();  // p of every key visible to the 32 threads of the query
-    (void)kmax;
-    if (!live) return;
-    // P.V: thread kj owns dims [kj*HD/32, +HD/32)
-    constexpr int DPT = HD / 32;
-    double acc[DPT];
 #pragma unroll
-    for (int i = 0; i < DPT; i++) acc[i] = 0.0;
-    // one 8-byte (HD 128) or 4-byte (HD 64) load per position, 4 positions in flight
-    typedef uint32_t vw_t __attribute__((ext_vector_type(DPT / 2)));
-    const uint16_t* vb = a.vcache + kh * HD + kj * DPT;
-    constexpr int PU = 4;
-    int t = 0;
-    for (; t + PU <= T; t += PU) {
-        vw_t vv[PU];
-        double pp[PU];
+    for (int r = 0; r < 4; r++) {
+        const int qi = 4 * r + g;
+        if (qi < nq) {
+            float* out = a.out + (size_t)(tq0 + qi) * (a.heads * HD) + h * HD + wave * DT * 16 + c;
 #pragma unroll
-        for (int u = 0; u < PU; u++) {
-            vv[u] = *(const vw_t*)(vb + (size_t)(t + u) * kvd);
-            pp[u] = (double)sc[t + u];
-        }
-#pragma unroll
-        for (int u = 0; u < PU; u++)
-#pragma unroll
-            for (int i = 0; i < DPT / 2; i++) {
-                acc[2 * i] = __builtin_fma(pp[u], (double)uq_half((uint16_t)(vv[u][i] & 0xffff)), acc[2 * i]);
-                acc[2 * i + 1] = __builtin_fma(pp[u], (double)uq_half((uint16_t)(vv[u][i] >> 16)), acc[2 * i + 1]);
-            }
-    }
-    for (; t < T; t++) {
-        const double p = (double)sc[t];
-        const vw_t v = *(const vw_t*)(vb + (size_t)t * kvd);
-#pragma unroll
-        for (int i = 0; i < DPT / 2; i++) {
-            acc[2 * i] = __builtin_fma(p, (double)uq_half((uint16_t)(v[i] & 0xffff)), acc[2 * i]);
-            acc[2 * i + 1] = __builtin_fma(p, (double)uq_half((uint16_t)(v[i] >> 16)), acc[2 * i + 1]);
+            for (int j = 0; j < DT; j++) out[j * 16] = (float)(o[j][r] + o2[j][r]);
         }
     }
-    float* out = a.out + (size_t)tq * (a.heads * HD) + h * HD + kj * DPT;
-#pragma unroll
-    for (int i = 0; i < DPT; i++) out[i] = (float)acc[i];
 }
 
 }  // namespace
@@ -428,9 +524,10 @@ void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_rope_kv, dim3(tokens), dim3(256), 0, s, a);
 }
 int launch_pf_attention(const PfAttnArgs& a, hipStream_t s) {
-    const size_t lds = sizeof(float) * QT * (size_t)a.kcap;
-    if (lds + sizeof(double) * QT * a.head_dim > 65536) return -1;
-    const dim3 grid(a.heads, (a.n + QT - 1) / QT);
+    const size_t sst = (size_t)((a.p0 + a.n + 15) & ~15);
+    const size_t lds = sizeof(float) * PA_Q * sst;
+    if (lds > 65536 || a.n <= 0 || a.p0 + a.n > a.kcap || a.heads % a.kv_heads) return -1;
+    const dim3 grid(a.heads, (a.n + PA_Q - 1) / PA_Q);
     switch (a.head_dim) {
     case 64: hipLaunchKernelGGL(k_pf_attention<64>, grid, dim3(256), lds, s, a); return 0;
     case 128: hipLaunchKernelGGL(k_pf_attention<128>, grid, dim3(256), lds, s, a); return 0;

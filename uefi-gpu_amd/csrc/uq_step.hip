@@ -37,15 +37,18 @@ constexpr int MAX_DIM = 4096;
 // One wave per row pair (32 lanes per row): pair (j, j+hd/2) of a q or k head
 // is rotated together; v rows are paired the same way and stored unrotated.
 template <int NBL>
-__global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t sq[MAX_DIM];
-    __shared__ float ssc[MAX_DIM / 32];
-    __shared__ double red[4];
+__global__ __launch_bounds__(320) void k_qkv_rope(QkvArgs a) {
+    constexpr int NC = 2 * NBL < MAX_DIM / 256 ? 2 * NBL : MAX_DIM / 256;  // dim <= 32 lanes x NBL units x 16
+    __shared__ __attribute__((aligned(16))) float lx[NC * 256];
+    __shared__ __attribute__((aligned(16))) float lr[NC * 256];
+    __shared__ __attribute__((aligned(16))) float lg[NC * 256];
+    __shared__ __attribute__((aligned(16))) int8_t sq[NC * 256];
+    __shared__ float ssc[NC * 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 31, grp = lane >> 5;
     const int hd = a.head_dim, half = hd / 2, kvd = a.kv_heads * hd;
     const int nq = a.heads * half, nk = a.kv_heads * half;
     const int pu = blockIdx.x * 4 + wave;
-    const bool live = pu < nq + 2 * nk;
+    const bool live = wave < 4 && pu < nq + 2 * nk;
     const int region = pu < nq ? 0 : (pu < nq + nk ? 1 : 2);
     const int p = region == 0 ? pu : (region == 1 ? pu - nq : pu - nq - nk);
     const int h = p / half, j = p % half;
@@ -53,8 +56,13 @@ __global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
     const int rbase = region == 0 ? 0 : (region == 1 ? a.heads * hd : a.heads * hd + kvd);
     const int64_t nu = a.dim / Q8::UNIT;
     const WArgs w{a.w_qs, a.w_d, nullptr};
-    NqRegsFor<256, NBL * 32 * Q8::UNIT> nqv;  // dim <= 32 lanes x NBL units x 16
-    norm_quant_load<256>(a.nq, nqv);  // activations first: the prologue waits only for them
+    // Wave 4 holds no rows: it normalizes and quantizes the input (loads
+    // queued ahead of the weight loads by the issue barrier) while waves 0..3
+    // issue their row pairs' weight loads.
+    NormQuantWave<NC> nw;
+    if (wave == 4) nw.issue(a.nq, lx, lr, lg);
+    uq_issue_barrier();
+    if (wave == 4) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
     Q8::W wv[NBL];
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
@@ -75,7 +83,7 @@ __global__ __launch_bounds__(256) void k_qkv_rope(QkvArgs a) {
             sn = a.trig[(size_t)pos * hd + half + j];
         }
     }
-    norm_quant_finish<256>(a.nq, nqv, blockIdx.x == 0, sq, ssc, red);
+    __syncthreads();    // the quantized input in LDS
     if (!live) return;  // whole wave; no barrier follows
     double acc = 0.0;
 #pragma unroll
@@ -517,7 +525,8 @@ int step_lpr(int64_t k) { return k / Q8::UNIT <= 256 ? 32 : 64; }
 int launch_qkv_rope(const QkvArgs& a, hipStream_t s) {
     if (a.dim > MAX_DIM) return -1;
     const int units = (a.heads + 2 * a.kv_heads) * (a.head_dim / 2);
-    return pick_nbl<32, QkvRope>(a.dim / Q8::UNIT, dim3((units + 3) / 4), dim3(256), 0, s, a);
+    if (a.dim % 32 || a.nq.dim != a.dim) return -1;
+    return pick_nbl<32, QkvRope>(a.dim / Q8::UNIT, dim3((units + 3) / 4), dim3(320), 0, s, a);
 }
 int launch_attention_split(const AttSplitArgs& a, hipStream_t s) {
     const size_t lds = sizeof(float) * (size_t)a.max_seq;

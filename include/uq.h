@@ -34,6 +34,7 @@ extern "C" {
 #define UQ_ERR_TIMEOUT (-5)
 #define UQ_ERR_CONTEXT (-6)
 #define UQ_ERR_ARG (-7)
+#define UQ_ERR_FORMAT (-8) /* malformed GGUF file; detail in the gguf_error out-parameter */
 
 /* GGUF tensor kinds (ggml type ids, frontier_core.rs:53-58 plus Q3_K/Q4_K). */
 #define UQ_KIND_F32 0u
@@ -188,6 +189,57 @@ int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float
 /* `steps` tokens back to back on the library stream, device arrays x[steps][dim],
  * logits[steps][experts], out[steps][dim]; ms = HIP-event time of the launches. */
 int uq_moe_run(uq_moe_t m, const float* xs, const float* logits, float* outs, int steps, double* ms);
+
+/* ---------------------------------------------------------------- GGUF files */
+/* Bounded GGUF v3 directory parser, Shard::parse (driver/src/frontier_gguf.rs:
+ * 145-200): the directory must fit a 16 MiB prefix; tensor bodies stay on
+ * storage. Failures return UQ_ERR_FORMAT and one of the reference's error
+ * categories (frontier_gguf.rs:7-8) in *gguf_error. */
+#define UQ_GGUF_TRUNCATED 1
+#define UQ_GGUF_MAGIC 2
+#define UQ_GGUF_VERSION 3
+#define UQ_GGUF_LIMIT 4
+#define UQ_GGUF_TYPE 5
+#define UQ_GGUF_UTF8 6
+#define UQ_GGUF_ALIGNMENT 7
+#define UQ_GGUF_SHAPE 8
+#define UQ_GGUF_OVERFLOW 9
+#define UQ_GGUF_TENSOR_BOUNDS 10
+#define UQ_GGUF_OVERLAP 11
+#define UQ_GGUF_DUPLICATE 12
+#define UQ_GGUF_MISSING 13
+#define UQ_GGUF_SPLIT 14
+typedef struct uq_gguf* uq_gguf_t;
+/* Shard::parse(prefix, logical_bytes): directory from `len` bytes of a file of
+ * `logical_bytes` bytes (no file access; tensor offsets are absolute). */
+int uq_gguf_parse(const void* prefix, size_t len, uint64_t logical_bytes, uq_gguf_t* out, int* gguf_error);
+/* Opens a file: parses its first min(size, 16 MiB) bytes with logical_bytes =
+ * the file size, and keeps the path for uq_model_load_gguf. */
+int uq_gguf_open(const char* path, uq_gguf_t* out, int* gguf_error);
+int uq_gguf_free(uq_gguf_t g);
+int64_t uq_gguf_tensor_count(uq_gguf_t g);
+uint64_t uq_gguf_data_offset(uq_gguf_t g);
+/* split.no, split.count, split.tensors.count (defaults 0, 1, tensor count). */
+int uq_gguf_split_info(uq_gguf_t g, uint64_t* split_no, uint64_t* split_count, uint64_t* total_tensors);
+/* Tensor `index`: name (valid while g lives), ggml kind, rank, dims[4] (unused
+ * dims 1), absolute file offset and byte size (Tensor, frontier_gguf.rs:95-99). */
+int uq_gguf_tensor_info(uq_gguf_t g, int64_t index, const char** name, uint32_t* kind, int32_t* rank, uint64_t* dims,
+                        uint64_t* offset, uint64_t* bytes);
+/* Index of the tensor called `name`, or -1 (Shard::tensor). */
+int64_t uq_gguf_find_tensor(uq_gguf_t g, const char* name);
+/* Metadata values (Value::unsigned for u8/u16/u32/u64, Value::float, Value::string,
+ * frontier_gguf.rs:44-66); the string is not NUL-terminated. */
+int uq_gguf_meta_u64(uq_gguf_t g, const char* key, uint64_t* out);
+int uq_gguf_meta_f32(uq_gguf_t g, const char* key, float* out);
+int uq_gguf_meta_str(uq_gguf_t g, const char* key, const char** out, uint64_t* len);
+int uq_gguf_meta_array(uq_gguf_t g, const char* key, uint32_t* elem_kind, uint64_t* count);
+/* Qwen2 shape constants from qwen2.* metadata and token_embd.weight (the
+ * constants llm.rs:314-321 hard-codes); max_seq <= 0 takes context_length. */
+int uq_gguf_qwen2_config(uq_gguf_t g, int32_t max_seq, uq_qwen2_config* cfg);
+/* upload_weights (llm.rs:157-201) from a GGUF file: every blk.* tensor plus
+ * token_embd, output_norm and output (token_embd when the file ties them) into
+ * the model, read from the file the handle was opened from. */
+int uq_model_load_gguf(uq_model_t m, uq_gguf_t g);
 
 #ifdef __cplusplus
 }

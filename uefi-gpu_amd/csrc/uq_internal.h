@@ -16,6 +16,7 @@ enum Status : int {
     ERR_TIMEOUT = -5,     // llm.rs:267-269 bounded poll expired
     ERR_CONTEXT = -6,     // Error::Context (position beyond the cache)
     ERR_ARG = -7,         // null pointer / bad handle / wrong state
+    ERR_FORMAT = -8,      // malformed GGUF file (frontier_gguf.rs:7-8 Error)
 };
 
 enum Kind : uint32_t { KIND_F32 = 0, KIND_Q8_0 = 8, KIND_Q3_K = 11, KIND_Q4_K = 12 };

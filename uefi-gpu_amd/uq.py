@@ -30,6 +30,7 @@ class Error(enum.IntEnum):
     TIMEOUT = -5
     CONTEXT = -6
     ARG = -7
+    FORMAT = -8
 
 
 class UqError(RuntimeError):
@@ -98,6 +99,25 @@ _SIGS = {
     "uq_moe_ffn": (ctypes.c_int, [_vp, _c_f32p, _c_f32p, _c_f32p, _c_i32p, _c_f32p]),
     "uq_moe_ffn_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "uq_moe_run": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+    "uq_gguf_parse": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_uint64, ctypes.POINTER(_vp),
+                                     ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_free": (ctypes.c_int, [_vp]),
+    "uq_gguf_tensor_count": (_i64, [_vp]),
+    "uq_gguf_data_offset": (ctypes.c_uint64, [_vp]),
+    "uq_gguf_split_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                          ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_tensor_info": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint32),
+                                           ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_find_tensor": (_i64, [_vp, ctypes.c_char_p]),
+    "uq_gguf_meta_u64": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_meta_f32": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+    "uq_gguf_meta_str": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_meta_array": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                          ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_qwen2_config": (ctypes.c_int, [_vp, ctypes.c_int32, _vp]),
+    "uq_model_load_gguf": (ctypes.c_int, [_vp, _vp]),
     "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
     "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
     "uq_synth_tokens": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_uint32, _c_u32p]),
@@ -368,6 +388,19 @@ class Qwen2Model:
                 self.set_tensor(name, kind, n, rows, arr)
             self.prepare()
 
+    @classmethod
+    def from_gguf(cls, path, max_seq=0):
+        """A model with the shape constants and tensors of a Qwen2 GGUF file
+        (uq_gguf_qwen2_config + uq_model_load_gguf), prepared."""
+        g = Gguf.open(path)
+        try:
+            m = cls(g.qwen2_config(max_seq))
+            _check(lib().uq_model_load_gguf(m.handle, g.handle))
+            m.prepare()
+        finally:
+            g.free()
+        return m
+
     def set_tensor(self, name, kind, n, rows, arr):
         a = np.ascontiguousarray(arr)
         _check(lib().uq_model_set_tensor(self.handle, name.encode(), kind, n, rows, a.ctypes.data, a.nbytes))
@@ -503,3 +536,102 @@ class MoeLayer:
             self.free()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------- GGUF files
+class GgufError(UqError):
+    """A malformed GGUF directory; .gguf_error is the reference's error category
+    (frontier_gguf.rs:7-8): one of GGUF_ERRORS."""
+
+    def __init__(self, status, msg, gguf_error):
+        super().__init__(status, msg)
+        self.gguf_error = GGUF_ERRORS.get(gguf_error, gguf_error)
+
+
+GGUF_ERRORS = {1: "Truncated", 2: "Magic", 3: "Version", 4: "Limit", 5: "Type", 6: "Utf8", 7: "Alignment",
+               8: "Shape", 9: "Overflow", 10: "TensorBounds", 11: "Overlap", 12: "Duplicate", 13: "Missing",
+               14: "Split"}
+
+
+class Gguf:
+    """A parsed GGUF directory (Shard, frontier_gguf.rs:104-200): from bytes
+    with parse(), or from a file with open()."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @classmethod
+    def parse(cls, prefix, logical_bytes):
+        buf = bytes(prefix)
+        h, ge = _vp(), ctypes.c_int(0)
+        rc = lib().uq_gguf_parse(buf, len(buf), logical_bytes, ctypes.byref(h), ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        return cls(h)
+
+    @classmethod
+    def open(cls, path):
+        h, ge = _vp(), ctypes.c_int(0)
+        rc = lib().uq_gguf_open(os.fsencode(path), ctypes.byref(h), ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        return cls(h)
+
+    def free(self):
+        if self.handle:
+            lib().uq_gguf_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    @property
+    def data_offset(self):
+        return lib().uq_gguf_data_offset(self.handle)
+
+    def split(self):
+        a, b, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().uq_gguf_split_info(self.handle, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)))
+        return a.value, b.value, c.value
+
+    def tensors(self):
+        out = []
+        for i in range(lib().uq_gguf_tensor_count(self.handle)):
+            name, kind, rank = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_int32()
+            dims, off, nb = (ctypes.c_uint64 * 4)(), ctypes.c_uint64(), ctypes.c_uint64()
+            _check(lib().uq_gguf_tensor_info(self.handle, i, ctypes.byref(name), ctypes.byref(kind), ctypes.byref(rank),
+                                             dims, ctypes.byref(off), ctypes.byref(nb)))
+            out.append({"name": name.value.decode(), "kind": kind.value, "dims": list(dims)[:rank.value],
+                        "offset": off.value, "bytes": nb.value})
+        return out
+
+    def find(self, name):
+        return lib().uq_gguf_find_tensor(self.handle, name.encode())
+
+    def u64(self, key):
+        v = ctypes.c_uint64()
+        _check(lib().uq_gguf_meta_u64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def f32(self, key):
+        v = ctypes.c_float()
+        _check(lib().uq_gguf_meta_f32(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def string(self, key):
+        p, n = _vp(), ctypes.c_uint64()
+        _check(lib().uq_gguf_meta_str(self.handle, key.encode(), ctypes.byref(p), ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value).decode()
+
+    def array(self, key):
+        k, n = ctypes.c_uint32(), ctypes.c_uint64()
+        _check(lib().uq_gguf_meta_array(self.handle, key.encode(), ctypes.byref(k), ctypes.byref(n)))
+        return k.value, n.value
+
+    def qwen2_config(self, max_seq=0):
+        c = Qwen2Config()
+        _check(lib().uq_gguf_qwen2_config(self.handle, max_seq, ctypes.byref(c)))
+        return c.as_dict()

@@ -184,7 +184,8 @@ int uq_moe_set_shared(uq_moe_t m, uint32_t kind, const void* gate, const void* u
 /* Host-memory call: x (dim), router logits (experts) -> out (dim); optional
  * ids/weights (top_k) of the routing. Non-finite input -> UQ_ERR_NONFINITE. */
 int uq_moe_ffn(uq_moe_t m, const float* x, const float* router_logits, float* out, int32_t* ids, float* weights);
-/* Device-pointer form on `stream` (NULL: library stream), no synchronization. */
+/* Device-pointer form on `stream` (NULL: library stream), no synchronization;
+ * x must be 16-byte aligned (UQ_ERR_ARG otherwise). */
 int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float* out, void* stream);
 /* `steps` tokens back to back on the library stream, device arrays x[steps][dim],
  * logits[steps][experts], out[steps][dim]; ms = HIP-event time of the launches. */

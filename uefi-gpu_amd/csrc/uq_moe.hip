@@ -58,7 +58,6 @@ struct MoeDev {
 // status flag, workgroup (top_k, 0) the shared expert's sigmoid gate. The
 // shared slot's weight loads are issued before the routing work.
 constexpr int GU_WG = 512;
-constexpr int GU_PE = (MAX_EXPERTS + GU_WG - 1) / GU_WG, GU_C = 4;
 
 struct RouteLds {
     float p[MAX_EXPERTS];
@@ -69,9 +68,18 @@ struct RouteLds {
     unsigned bad;
 };
 
-// softmax (f32 running sum in expert order, frontier_forward.rs:47-51) and
-// stable top-k (score descending, id ascending) into L.sid; returns the sum.
-__device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& bad) {
+// Routing arithmetic (the oracle's, frontier_forward.rs:47-51): softmax with
+// max subtraction and an f32 running sum in expert order; stable top-k (score
+// descending, id ascending).
+
+// Routing by the whole workgroup, GU_PE experts per thread, five barriers:
+// max (DPP per wave, then across waves), exps to LDS, the f32 running sum in
+// expert order by lane 0 of wave 0 (eight float4 LDS reads in flight) while
+// waves 1.. run `side` (the input quant), p = e / sum in place, stable ranks
+// against LDS broadcast reads. Leaves p in L.p and the top-k ids in L.sid.
+constexpr int GU_PE = (MAX_EXPERTS + GU_WG - 1) / GU_WG;
+template <class Side>
+__device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsigned& bad, Side side) {
     const int t = threadIdx.x, E = a.E;
     float mx = -__builtin_inff();
 #pragma unroll
@@ -95,10 +103,24 @@ __device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& 
     // the status flag reports the input
     if (t < a.top_k) L.sid[t] = t;
     __syncthreads();
-    if (t == 0) {
+    if (t < 64) {
+        if (t == 0) {
         const float4* p4 = (const float4*)L.p;
         float s = 0.0f;
-        for (int q = 0; q < E / 4; q++) {
+        int q = 0;
+        for (; q + 8 <= E / 4; q += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = p4[q + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                s = s + v[u].x;
+                s = s + v[u].y;
+                s = s + v[u].z;
+                s = s + v[u].w;
+            }
+        }
+        for (; q < E / 4; q++) {
             const float4 v = p4[q];
             s = s + v.x;
             s = s + v.y;
@@ -107,6 +129,9 @@ __device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& 
         }
         for (int e = E & ~3; e < E; e++) s = s + L.p[e];
         L.sum = s;
+        }
+    } else {
+        side();
     }
     __syncthreads();
     const float sum = L.sum;
@@ -115,12 +140,7 @@ __device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& 
     for (int j = 0; j < GU_PE; j++) {
         const int e = j * GU_WG + t;
         pe[j] = e < E ? L.p[e] / sum : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < GU_PE; j++) {
-        const int e = j * GU_WG + t;
-        if (e < E) L.p[e] = pe[j];
+        if (e < E) L.p[e] = pe[j];  // each thread rewrites only its own entries
     }
     __syncthreads();
     const float4* p4 = (const float4*)L.p;
@@ -143,7 +163,6 @@ __device__ float route(const MoeDev& a, const float* lg, RouteLds& L, unsigned& 
             if (rank < a.top_k) L.sid[rank] = e;
         }
     }
-    __syncthreads();
     return sum;
 }
 
@@ -189,72 +208,71 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
     const int slot = blockIdx.x / blocks, rb = blockIdx.x % blocks;
     const bool shared = slot == a.top_k;
     const int D = a.D;
-    // global inputs up front
-    float lg[GU_PE], xv[GU_C];
+    // logits and x up front; waves 1..7 quantize x (4 values per lane, a
+    // 32-block = 8 lanes) while wave 0 forms the softmax sum
+    float lg[GU_PE];
 #pragma unroll
     for (int j = 0; j < GU_PE; j++) {
         const int e = j * GU_WG + t;
         lg[j] = e < a.E ? a.logits[e] : 0.0f;
     }
+    constexpr int QT = GU_WG - 64, QP = (MAX_D + 4 * QT - 1) / (4 * QT);
+    const int qt = t - 64;
+    float4 xv[QP];
 #pragma unroll
-    for (int j = 0; j < GU_C; j++) {
-        const int i = j * GU_WG + t;
-        xv[j] = i < D ? a.x[i] : 0.0f;
+    for (int j = 0; j < QP; j++) {
+        const int i = (j * QT + qt) * 4;
+        xv[j] = (qt >= 0 && i < D) ? *(const float4*)(a.x + i) : float4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     GuLane<KS, NS> sl;
     const int64_t srow = (int64_t)rb * 32 + wave * 4 + grp;
     if (shared) sl.load(sg, su, srow, D / KS::UNIT, sub);
     unsigned bad = 0;
-    const float sum = route(a, lg, L, bad);
-    // input quant (per 32) into LDS, GU_C elements per thread per pass
-    for (int base = 0; base < D; base += GU_C * GU_WG) {
-        if (base > 0) {
+    // i < D is uniform over each 8-lane block group (D is a multiple of 32)
+    auto quant_x = [&]() {
 #pragma unroll
-            for (int j = 0; j < GU_C; j++) {
-                const int i = base + j * GU_WG + t;
-                xv[j] = i < D ? a.x[i] : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < GU_C; j++) {
-            const int i = base + j * GU_WG + t;
+        for (int j = 0; j < QP; j++) {
+            const int i = (j * QT + qt) * 4;
             if (i < D) {
-                bad |= !isfinite(xv[j]);
-                float sc;
-                const int8_t q = uq_quant_lane(xv[j], &sc);
-                lxq[i] = q;
-                if ((t & 31) == 0) lxs[i >> 5] = sc;
+                const float v[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                bad |= !isfinite(v[0]) | !isfinite(v[1]) | !isfinite(v[2]) | !isfinite(v[3]);
+                uint32_t pk;
+                const float sc = uq_quant4_group8(v, &pk);
+                *(uint32_t*)(lxq + i) = pk;
+                if ((qt & 7) == 0) lxs[i >> 5] = sc;
             }
         }
-    }
-    bad = __syncthreads_or(bad);  // also publishes lxq/lxs
-    if (blockIdx.x == 0 && t == 0) {
-        float tot = 0.0f;
-        for (int k = 0; k < a.top_k; k++) tot = tot + L.p[L.sid[k]];
-        if (!(sum > 0.0f) || !isfinite(sum) || !(tot > 0.0f)) bad = 1;
-        for (int k = 0; k < a.top_k; k++) {
-            a.ids[k] = L.sid[k];
-            a.wts[k] = L.p[L.sid[k]] / tot;
-        }
-        a.status[0] = bad;
-    }
-    if (shared && rb == 0) {
-        // shared expert weight sigmoid(shexp_gate . x), dot in double
-        double dot = 0.0;
-        if (a.sh_gate)
-            for (int i = t; i < D; i += GU_WG) dot = __builtin_fma((double)a.sh_gate[i], (double)a.x[i], dot);
-        dot = block_sum_d<GU_WG>(dot, L.red);
-        if (t == 0) a.wts[a.top_k] = a.sh_gate ? uq_sigmoid((float)dot) : 1.0f;
-    }
+    };
+    const float sum = route_par(a, lg, L, bad, quant_x);
+    bad = __syncthreads_or(bad);  // publishes L.p / L.sid and lxq / lxs
     float v;
-    if (shared) {
-        v = sl.silu_mul(lxq, lxs, D / KS::UNIT, sub);
-    } else {
+    if (!shared) {
+        // routed expert: its weight loads go out before anything else waits
         const int e = L.sid[slot];
         const int ec = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
         GuLane<KR, NR> rl;
         rl.load(rg, ru, (int64_t)ec * a.F + srow, D / KR::UNIT, sub);
+        if (blockIdx.x == 0 && t == 0) {
+            float tot = 0.0f;
+            for (int k = 0; k < a.top_k; k++) tot = tot + L.p[L.sid[k]];
+            if (!(sum > 0.0f) || !isfinite(sum) || !(tot > 0.0f)) bad = 1;
+            for (int k = 0; k < a.top_k; k++) {
+                a.ids[k] = L.sid[k];
+                a.wts[k] = L.p[L.sid[k]] / tot;
+            }
+            a.status[0] = bad;
+        }
         v = rl.silu_mul(lxq, lxs, D / KR::UNIT, sub);
+    } else {
+        if (rb == 0) {
+            // shared expert weight sigmoid(shexp_gate . x), dot in double
+            double dot = 0.0;
+            if (a.sh_gate)
+                for (int i = t; i < D; i += GU_WG) dot = __builtin_fma((double)a.sh_gate[i], (double)a.x[i], dot);
+            dot = block_sum_d<GU_WG>(dot, L.red);
+            if (t == 0) a.wts[a.top_k] = a.sh_gate ? uq_sigmoid((float)dot) : 1.0f;
+        }
+        v = sl.silu_mul(lxq, lxs, D / KS::UNIT, sub);
     }
     if (sub == 0) ys[wave * 4 + grp] = v;
     __syncthreads();
@@ -541,6 +559,7 @@ extern "C" {
 
 int uq_moe_ffn_dev(uq_moe_t m, const float* x, const float* router_logits, float* out, void* stream) {
     if (!m || !x || !router_logits || !out) return set_error(ERR_ARG, "moe_ffn_dev: null pointer");
+    if ((uintptr_t)x & 15) return set_error(ERR_ARG, "moe_ffn_dev: x must be 16-byte aligned");
     if (int rc = moe_finalize(m)) return rc;
     MoeDev d{x, router_logits, m->sh_vec, m->xq, m->xs, m->ids, m->wts, m->status, m->midq, m->mids, out,
              m->D, m->F, m->E, m->K};

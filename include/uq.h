@@ -41,6 +41,11 @@ extern "C" {
 #define UQ_KIND_Q8_0 8u
 #define UQ_KIND_Q3_K 11u
 #define UQ_KIND_Q4_K 12u
+#define UQ_KIND_Q6_K 14u
+#define UQ_KIND_IQ3_XXS 18u
+#define UQ_KIND_IQ4_NL 20u
+#define UQ_KIND_IQ4_XS 23u
+#define UQ_KIND_BF16 30u
 
 /* ---------------------------------------------------------------- context */
 /* Replaces the GSP/RM channel bring-up that ends in llm::run's Gpu value
@@ -60,7 +65,9 @@ typedef struct uq_weight* uq_weight_t;
 /* Upload one GGUF tensor of m rows x n values (Tensor{n, m, typ}, llm.rs:63),
  * repack it on the device into the kernel layout, rebuild the GGUF bytes from
  * that layout and require a byte-for-byte match (llm.rs:187-200 upload
- * readback, gpu_prefill.rs:74-93 swizzle verify). kind: Q8_0, Q4_K, Q3_K. */
+ * readback, gpu_prefill.rs:74-93 swizzle verify). kind: Q8_0, Q4_K, Q3_K for
+ * the int8-activation linears below; F32, BF16, Q8_0, Q6_K, IQ3_XXS, IQ4_NL,
+ * IQ4_XS for the fp32-activation reader (F32/BF16: n % 8 == 0). */
 int uq_weight_upload(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, uq_weight_t* out);
 int uq_weight_free(uq_weight_t w);
 /* Device bytes held by the weight (repacked planes). */
@@ -100,6 +107,39 @@ int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t to
 /* Mean HIP-event time of the prefill GEMM on `tokens` synthetic activations
  * (w2 non-null: the fused gate/up pair), `reps` launches. Measurement aid. */
 int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps, double* ms);
+
+/* ---------------------------------------------------------------- fp32-activation reader
+ * The frontier backend's kernels (driver/kernels/frontier_quant.cu:12-93) for
+ * its seven kinds, with fp32 activations. Each output is the exact sum of the
+ * dequantized weights times x, rounded to f32 once; the reference's own check
+ * allows 2e-4 + 2e-5 |ref| against an f32 sequential sum (frontier_gpu.rs:111). */
+
+/* frontier_dequant (frontier_quant.cu:34-37) = dequantize (frontier_core.rs:73-106):
+ * the n values of one GGUF byte run (nbytes == row_bytes(kind, n)) as f32, bit
+ * for bit; host memory, synchronous. Q3_K/Q4_K -> UQ_ERR_QUANT_TYPE as there. */
+int uq_dequantize(uint32_t kind, const void* bytes, size_t nbytes, int64_t n, float* out);
+
+/* One entry of the FrontierJob table (frontier_quant.cu:71-78): weight, its
+ * input (n floats) and output (m floats). */
+typedef struct {
+    uq_weight_t weight;
+    const float* x;
+    float* y;
+} uq_linear_job;
+
+/* Weights::linear (frontier_forward.rs:17; frontier_backend.rs:243) over
+ * frontier_matvec (frontier_quant.cu:55-63): y = W x, host memory, synchronous.
+ * Non-finite input or output -> UQ_ERR_NONFINITE (frontier_backend.rs:222,272);
+ * Q3_K/Q4_K weights -> UQ_ERR_QUANT_TYPE. */
+int uq_linear(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m);
+/* Weights::batch (frontier_forward.rs:18; frontier_backend.rs:178-224): the jobs
+ * (host x and y) in ONE launch, the frontier_multi_matvec of
+ * frontier_quant.cu:79-93; bit-identical to uq_linear of each job. */
+int uq_linear_batch(const uq_linear_job* jobs, int count);
+/* Device forms on `stream` (NULL: library stream), no synchronization; x must
+ * be 16-byte aligned. */
+int uq_linear_dev(uq_weight_t w, const float* x, float* y, void* stream);
+int uq_linear_multi_dev(const uq_linear_job* jobs, int count, void* stream);
 
 /* ---------------------------------------------------------------- memory + timing
  * Small helpers so harnesses need no other GPU runtime binding. */

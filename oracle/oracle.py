@@ -13,6 +13,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, Q8_0, Q3_K, Q4_K = 0, 8, 11, 12
+Q6_K, IQ3_XXS, IQ4_NL, IQ4_XS, BF16 = 14, 18, 20, 23, 30
+FRONTIER_KINDS = (F32, BF16, Q8_0, Q6_K, IQ3_XXS, IQ4_NL, IQ4_XS)
 
 _lib = None
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -62,6 +64,11 @@ def lib():
             "uqo_expf": (ctypes.c_float, [ctypes.c_float]),
             "uqo_row_bytes": (_i64, [ctypes.c_uint32, _i64]),
             "uqo_dequantize": (ctypes.c_int, [ctypes.c_uint32, _u8p, _i64, _f32p]),
+            "uqo_iq3_grid": (ctypes.c_uint32, [ctypes.c_int]),
+            "uqo_iq4_value": (ctypes.c_int, [ctypes.c_int]),
+            "uqo_linear": (None, [ctypes.c_uint32, _u8p, _i64, _i64, _f32p, _f32p]),
+            "uqo_linear_f32seq": (None, [ctypes.c_uint32, _u8p, _i64, _i64, _f32p, _f32p]),
+            "uqo_frontier_fixture": (_i64, [ctypes.c_uint32, _i64, _u8p]),
             "uqo_quant_act": (None, [_f32p, _i64, _f32p, _i8p]),
             "uqo_q8_block_dots": (None, [_u8p, _i64, _i64, _i8p, _i32p]),
             "uqo_q4k_block_dots": (None, [_u8p, _i64, _i64, _i8p, _i32p]),
@@ -168,6 +175,44 @@ def dequantize(kind, w, n):
     rc = lib().uqo_dequantize(kind, p(w, _u8p), n, p(out, _f32p))
     if rc:
         raise ValueError("dequantize rc=%d" % rc)
+    return out
+
+
+def row_bytes(kind, n):
+    return lib().uqo_row_bytes(kind, n)
+
+
+def iq3_grid():
+    return np.array([lib().uqo_iq3_grid(i) for i in range(256)], np.uint32)
+
+
+def iq4_values():
+    return np.array([lib().uqo_iq4_value(i) for i in range(16)], np.int32)
+
+
+def linear(kind, w, n, m, x):
+    """fp32-activation matvec (frontier_matvec), exact double sum per row."""
+    y = np.empty(m, np.float32)
+    lib().uqo_linear(kind, p(np.ascontiguousarray(w, np.uint8), _u8p), n, m,
+                     p(np.ascontiguousarray(x, np.float32), _f32p), p(y, _f32p))
+    return y
+
+
+def linear_f32seq(kind, w, n, m, x):
+    """The reference's literal f32 sequential CPU check of frontier_matvec."""
+    y = np.empty(m, np.float32)
+    lib().uqo_linear_f32seq(kind, p(np.ascontiguousarray(w, np.uint8), _u8p), n, m,
+                            p(np.ascontiguousarray(x, np.float32), _f32p), p(y, _f32p))
+    return y
+
+
+def frontier_fixture(kind, n):
+    """The reference's synthetic quant bytes for `n` values (frontier_gpu.rs:37-50)."""
+    rb = row_bytes(kind, n)
+    if rb < 0:
+        raise ValueError("bad kind/n")
+    out = np.empty(rb, np.uint8)
+    lib().uqo_frontier_fixture(kind, n, p(out, _u8p))
     return out
 
 

@@ -23,6 +23,14 @@
  *                       it, frontier_core.rs:53-58); pinned by hand-worked
  *                       known-answer blocks, integer path == dequant path,
  *                       encode/decode round trips of the ggml layouts
+ *   dequantize, kinds   hand-worked known-answer blocks per kind (code book
+ *   BF16/Q6_K/IQ3_XXS/  and grid entries, sign parity, scale composition and
+ *   IQ4_NL/IQ4_XS       f32 multiply order), fp16-scale linearity, the IQ3
+ *                       grid's invariants; the grid and code book are data of
+ *                       the reference (frontier_tables.rs, frontier_core.rs:67)
+ *   uqo_linear          vs float64 numpy dot of uqo_dequantize values, and vs
+ *                       the reference's f32 check (frontier_gpu.rs:104-111)
+ *                       within its 2e-4 + 2e-5|ref| tolerance
  *   uqo_prefill_gemm    int64 brute force + float64 bound; sequential order
  *   uqo_rmsnorm/rope/attention/greedy  float64 textbook forms, invariants
  *                       (softmax sums to 1, pos 0 identity, norm-preserving
@@ -150,6 +158,12 @@ int64_t uqo_row_bytes(uint32_t kind, int64_t n) {
     case UQO_Q8_0: block = 32; bytes = 34; break;
     case UQO_Q4_K: block = 256; bytes = 144; break;
     case UQO_Q3_K: block = 256; bytes = 110; break;
+    /* the reference's remaining kinds, frontier_core.rs:53-58 */
+    case UQO_Q6_K: block = 256; bytes = 210; break;
+    case UQO_IQ3_XXS: block = 256; bytes = 98; break;
+    case UQO_IQ4_NL: block = 32; bytes = 18; break;
+    case UQO_IQ4_XS: block = 256; bytes = 136; break;
+    case UQO_BF16: block = 1; bytes = 2; break;
     default: return -1;
     }
     if (n <= 0 || n % block) return -2;
@@ -187,6 +201,79 @@ static inline int q4k_value(int i, const uint8_t* blk) {
 
 /* driver/src/frontier_core.rs:73-106 form (one value at a time, ggml's scale
  * multiplication order), for F32, Q8_0 and the Q4_K/Q3_K layouts. */
+/* The IQ4_NL/IQ4_XS code book (frontier_core.rs:67) and the IQ3_XXS grid
+ * (frontier_tables.rs:2-35, ggml's iq3xxs_grid). The grid is held here in a
+ * different encoding than the product's: entry i as four 3-bit digits (lowest
+ * byte first) into the eight byte levels below, expanded by uqo_iq3_grid();
+ * the tests check the expansion's invariants (256 distinct entries in
+ * ascending order, every byte one of the levels). */
+static const int8_t IQ4_BOOK[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+static const uint8_t IQ3_LEVEL[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+static const uint16_t IQ3_DIGITS[256] = {
+       0,    2,    4,    9,   11,   15,   16,   18,   25,   34,   59,   61,   65,   67,   72,   74,
+      81,   85,   88,   90,   97,  108,  120,  128,  130,  132,  137,  144,  146,  153,  155,  159,
+     169,  175,  189,  193,  199,  200,  202,  213,  248,  267,  287,  292,  303,  315,  317,  321,
+     327,  346,  362,  413,  436,  456,  460,  462,  483,  497,  513,  515,  520,  522,  529,  531,
+     536,  538,  540,  551,  552,  576,  578,  585,  592,  594,  641,  643,  648,  650,  657,  664,
+     698,  704,  706,  720,  729,  742,  758,  769,  773,  808,  848,  852,  870,  889,  901,  978,
+     992, 1024, 1026, 1033, 1035, 1040, 1042, 1046, 1049, 1058, 1089, 1091, 1093, 1096, 1098, 1105,
+    1112, 1139, 1143, 1144, 1152, 1154, 1161, 1167, 1168, 1170, 1183, 1184, 1197, 1217, 1224, 1228,
+    1272, 1276, 1309, 1323, 1347, 1367, 1377, 1404, 1473, 1475, 1486, 1509, 1537, 1544, 1546, 1553,
+    1555, 1576, 1589, 1594, 1600, 1602, 1616, 1625, 1636, 1638, 1665, 1667, 1672, 1685, 1706, 1722,
+    1737, 1755, 1816, 1831, 1850, 1856, 1862, 1874, 1901, 1932, 1950, 1971, 2011, 2032, 2052, 2063,
+    2077, 2079, 2091, 2095, 2172, 2192, 2207, 2208, 2224, 2230, 2247, 2277, 2308, 2345, 2356, 2389,
+    2403, 2424, 2501, 2504, 2506, 2520, 2570, 2593, 2616, 2624, 2630, 2646, 2669, 2700, 2714, 2746,
+    2754, 2795, 2824, 2835, 2839, 2874, 2882, 2905, 2984, 3028, 3042, 3092, 3108, 3110, 3124, 3153,
+    3185, 3215, 3252, 3288, 3294, 3364, 3397, 3434, 3483, 3523, 3537, 3587, 3589, 3591, 3592, 3610,
+    3626, 3670, 3680, 3722, 3749, 3754, 3776, 3789, 3803, 3824, 3857, 3873, 3904, 3906, 3924, 3992,
+};
+uint32_t uqo_iq3_grid(int i) {
+    uint32_t v = 0, d = IQ3_DIGITS[i & 255];
+    for (int k = 0; k < 4; k++) v |= (uint32_t)IQ3_LEVEL[(d >> (3 * k)) & 7] << (8 * k);
+    return v;
+}
+int uqo_iq4_value(int i) { return IQ4_BOOK[i & 15]; }
+static inline uint32_t rd32(const uint8_t* p) { return (uint32_t)rd16(p) | ((uint32_t)rd16(p + 2) << 16); }
+
+/* Exact decoded value i of a GGUF byte run: frontier_core.rs:73-106 (GPU twin
+ * frontier_quant.cu:12-33), with the same f32 multiplication order. */
+static float dequant_one(uint32_t kind, const uint8_t* in, int64_t i) {
+    switch (kind) {
+    case UQO_BF16: return f_from_bits((uint32_t)rd16(in + 2 * i) << 16);
+    case UQO_IQ4_NL: {
+        const uint8_t* p = in + (i / 32) * 18;
+        int j = (int)(i % 32), q = (p[2 + j % 16] >> (4 * (j / 16))) & 15;
+        return uqo_half(rd16(p)) * (float)IQ4_BOOK[q];
+    }
+    case UQO_IQ4_XS: {
+        const uint8_t* p = in + (i / 256) * 136;
+        int j = (int)(i % 256), sb = j / 32;
+        int sc = ((p[4 + sb / 2] >> (4 * (sb % 2))) & 15) | (((rd16(p + 2) >> (2 * sb)) & 3) << 4);
+        int q = (p[8 + sb * 16 + j % 16] >> (4 * ((j % 32) / 16))) & 15;
+        return (uqo_half(rd16(p)) * (float)(sc - 32)) * (float)IQ4_BOOK[q];
+    }
+    case UQO_Q6_K: {
+        const uint8_t* p = in + (i / 256) * 210;
+        int j = (int)(i % 256), sub = j / 128, l = j % 32, g = (j % 128) / 32;
+        int lo = p[sub * 64 + l + (g % 2) * 32], hi = p[128 + sub * 32 + l];
+        int q = (((lo >> (4 * (g / 2))) & 15) | (((hi >> (2 * g)) & 3) << 4)) - 32;
+        int sc = (int8_t)p[192 + sub * 8 + l / 16 + g * 2];
+        return (uqo_half(rd16(p + 208)) * (float)sc) * (float)q;
+    }
+    case UQO_IQ3_XXS: {
+        const uint8_t* p = in + (i / 256) * 98;
+        int j = (int)(i % 256), sb = j / 32, g = (j % 32) / 8;
+        uint32_t aux = rd32(p + 66 + sb * 4), s7 = (aux >> (7 * g)) & 127;
+        uint32_t sg = s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
+        int idx = p[2 + sb * 8 + g * 2 + (j % 8) / 4];
+        uint32_t q = (uqo_iq3_grid(idx) >> (8 * (j % 4))) & 255;
+        float scale = uqo_half(rd16(p)) * (0.5f + (float)(aux >> 28)) * 0.5f;
+        return (scale * (float)q) * ((sg & (1u << (j % 8))) ? -1.0f : 1.0f);
+    }
+    }
+    return NAN;
+}
+
 int uqo_dequantize(uint32_t kind, const uint8_t* in, int64_t n, float* out) {
     if (uqo_row_bytes(kind, n) < 0) return -1;
     for (int64_t i = 0; i < n; i++) {
@@ -212,6 +299,7 @@ int uqo_dequantize(uint32_t kind, const uint8_t* in, int64_t n, float* out) {
             out[i] = dl * (float)q3k_value(j, p);
             break;
         }
+        default: out[i] = dequant_one(kind, in, i); break;
         }
     }
     return 0;
@@ -782,3 +870,82 @@ int uqo_moe_ffn(const uqo_moe* mo, const float* x, const float* router_logits, f
     if (!rc && !all_finite(out, D)) rc = -3;
     return rc;
 }
+
+/* ---------------------------------------------------------------- fp32-activation reader
+ * frontier_matvec (frontier_quant.cu:55-63; host Weights::linear,
+ * frontier_backend.rs:243): y[r] = sum_i value(r, i) * x[i] with fp32 x. Each
+ * value is a dequantize() f32 whose products with x are exact in double; the
+ * sum runs in double in index order and is rounded to f32 once. */
+void uqo_linear(uint32_t kind, const uint8_t* w, int64_t n, int64_t m, const float* x, float* y) {
+    const int64_t rb = uqo_row_bytes(kind, n);
+    #pragma omp parallel
+    {
+        float* v = (float*)malloc(sizeof(float) * (size_t)n);
+        #pragma omp for schedule(static)
+        for (int64_t r = 0; r < m; r++) {
+            uqo_dequantize(kind, w + r * rb, n, v);
+            double acc = 0.0;
+            for (int64_t i = 0; i < n; i++) acc += (double)v[i] * (double)x[i];
+            y[r] = (float)acc;
+        }
+        free(v);
+    }
+}
+
+/* The reference's own CPU check of frontier_matvec (frontier_gpu.rs:104,
+ * :176-178): reference += dequant[j] * x[j] in f32, sequentially, multiply
+ * then add. Its tolerance is 2e-4 + 2e-5 |reference| (:111). */
+void uqo_linear_f32seq(uint32_t kind, const uint8_t* w, int64_t n, int64_t m, const float* x, float* y) {
+    const int64_t rb = uqo_row_bytes(kind, n);
+    float* v = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int64_t r = 0; r < m; r++) {
+        uqo_dequantize(kind, w + r * rb, n, v);
+        float acc = 0.0f;
+        for (int64_t i = 0; i < n; i++) {
+            float t = v[i] * x[i];
+            acc = acc + t;
+        }
+        y[r] = acc;
+    }
+    free(v);
+}
+
+/* The reference's synthetic quant bytes, frontier_gpu.rs:37-50: xorshift32
+ * bytes from state 0x13243546 (<<13, >>17, <<5, low byte), F32/BF16 values
+ * ((i % 127) - 63) / 64, and each block's fp16 scale field set to
+ * 0x2000, 0x2800, 0x3000, 0xb000 in turn. Returns bytes written or <0. */
+int64_t uqo_frontier_fixture(uint32_t kind, int64_t n, uint8_t* out) {
+    const int64_t rb = uqo_row_bytes(kind, n);
+    if (rb < 0) return -1;
+    uint32_t st = 0x13243546u;
+    for (int64_t i = 0; i < rb; i++) {
+        st ^= st << 13;
+        st ^= st >> 17;
+        st ^= st << 5;
+        out[i] = (uint8_t)st;
+    }
+    if (kind == UQO_F32 || kind == UQO_BF16) {
+        for (int64_t i = 0; i < n; i++) {
+            uint32_t bits = bits_from_f(((float)(i % 127) - 63.0f) / 64.0f);
+            if (kind == UQO_F32) memcpy(out + 4 * i, &bits, 4);
+            else { uint16_t h = (uint16_t)(bits >> 16); memcpy(out + 2 * i, &h, 2); }
+        }
+    } else {
+        int64_t block, size, off;
+        switch (kind) {
+        case UQO_Q8_0: block = 32; size = 34; off = 0; break;
+        case UQO_Q6_K: block = 256; size = 210; off = 208; break;
+        case UQO_IQ3_XXS: block = 256; size = 98; off = 0; break;
+        case UQO_IQ4_NL: block = 32; size = 18; off = 0; break;
+        case UQO_IQ4_XS: block = 256; size = 136; off = 0; break;
+        default: return -2;
+        }
+        static const uint16_t halves[4] = {0x2000, 0x2800, 0x3000, 0xb000};
+        for (int64_t b = 0; b < n / block; b++) {
+            uint16_t h = halves[b % 4];
+            memcpy(out + b * size + off, &h, 2);
+        }
+    }
+    return rb;
+}
+

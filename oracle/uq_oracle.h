@@ -32,7 +32,8 @@ extern "C" {
 #endif
 
 /* GGUF quant kinds used on this path (ggml type ids). */
-enum { UQO_F32 = 0, UQO_Q8_0 = 8, UQO_Q3_K = 11, UQO_Q4_K = 12 };
+enum { UQO_F32 = 0, UQO_Q8_0 = 8, UQO_Q3_K = 11, UQO_Q4_K = 12, UQO_Q6_K = 14, UQO_IQ3_XXS = 18,
+       UQO_IQ4_NL = 20, UQO_IQ4_XS = 23, UQO_BF16 = 30 };
 
 void     uqo_set_threads(int n);
 int      uqo_get_threads(void);
@@ -42,6 +43,11 @@ uint16_t uqo_f16_rne(float f);
 float    uqo_expf(float x);
 int64_t  uqo_row_bytes(uint32_t kind, int64_t n);
 int      uqo_dequantize(uint32_t kind, const uint8_t* in, int64_t n, float* out);
+uint32_t uqo_iq3_grid(int i);
+int      uqo_iq4_value(int i);
+void     uqo_linear(uint32_t kind, const uint8_t* w, int64_t n, int64_t m, const float* x, float* y);
+void     uqo_linear_f32seq(uint32_t kind, const uint8_t* w, int64_t n, int64_t m, const float* x, float* y);
+int64_t  uqo_frontier_fixture(uint32_t kind, int64_t n, uint8_t* out);
 
 void uqo_quant_act(const float* x, int64_t n, float* scale, int8_t* q);
 

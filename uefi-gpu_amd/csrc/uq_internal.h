@@ -19,7 +19,17 @@ enum Status : int {
     ERR_FORMAT = -8,      // malformed GGUF file (frontier_gguf.rs:7-8 Error)
 };
 
-enum Kind : uint32_t { KIND_F32 = 0, KIND_Q8_0 = 8, KIND_Q3_K = 11, KIND_Q4_K = 12 };
+enum Kind : uint32_t {
+    KIND_F32 = 0,
+    KIND_Q8_0 = 8,
+    KIND_Q3_K = 11,
+    KIND_Q4_K = 12,
+    KIND_Q6_K = 14,
+    KIND_IQ3_XXS = 18,
+    KIND_IQ4_NL = 20,
+    KIND_IQ4_XS = 23,
+    KIND_BF16 = 30,
+};
 
 int set_error(int status, const std::string& msg);
 #define UQ_CHECK_HIP(call)                                                        \
@@ -32,7 +42,9 @@ int set_error(int status, const std::string& msg);
 
 int64_t row_bytes(uint32_t kind, int64_t n);  // GGUF bytes of one row, <0 if invalid
 
-// Device-resident weight. Q8_0 is split into an int8 plane qs[m][n] and an
+// Device-resident weight. The frontier kinds (F32, BF16, Q6_K, IQ3_XXS,
+// IQ4_NL, IQ4_XS) use the planes of their FrontierLayout: qs = body units,
+// sc = aux bytes, d = fp16 block scales. Q8_0 is split into an int8 plane qs[m][n] and an
 // fp16 scale plane d[m][n/32]; Q4_K keeps the 144-byte superblocks (16-byte
 // aligned already); Q3_K is split into quants q[m][n/256][96] (hmask 32 B +
 // qs 64 B), packed 6-bit scales sc[m][n/256][12] and fp16 d[m][n/256].
@@ -51,6 +63,21 @@ struct Weight {
 int cu_count();
 
 int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank);
+
+// Split of one GGUF block of a frontier kind into three planes (body, aux,
+// fp16 scale): map[o] = plane << 12 | offset of source byte o within that
+// plane's per-block slice of plane_bytes[plane] bytes (uq_frontier.hip).
+struct FrontierLayout {
+    int block_vals, block_bytes;
+    int plane_bytes[3];
+    uint16_t map[256];
+};
+bool frontier_layout(uint32_t kind, FrontierLayout& L);
+void launch_layout_repack(const uint8_t* src, int64_t blocks, const FrontierLayout& L, uint8_t* const planes[3],
+                          hipStream_t s);
+void launch_layout_verify(const uint8_t* src, int64_t blocks, const FrontierLayout& L, uint8_t* const planes[3],
+                          unsigned* bad, hipStream_t s);
+void frontier_release();
 
 // ---- kernel launchers (uq_matvec.hip) ----
 void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s);

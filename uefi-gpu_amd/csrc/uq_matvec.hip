@@ -460,6 +460,8 @@ int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const flo
 }
 
 int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s) {
+    if (w.kind != KIND_Q8_0 && w.kind != KIND_Q4_K && w.kind != KIND_Q3_K)
+        return set_error(ERR_QUANT_TYPE, "block_dots: Q8_0, Q4_K or Q3_K only");
     const int bsz = w.kind == KIND_Q3_K ? 16 : 32;
     const int64_t items = w.m * (w.n / bsz);
     WArgs a{w.qs, w.d, w.sc};

@@ -7,6 +7,7 @@
 #include "uq_internal.h"
 #include "../../include/uq.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -48,6 +49,11 @@ int64_t row_bytes(uint32_t kind, int64_t n) {
     case KIND_Q8_0: block = 32; bytes = 34; break;
     case KIND_Q4_K: block = 256; bytes = 144; break;
     case KIND_Q3_K: block = 256; bytes = 110; break;
+    case KIND_Q6_K: block = 256; bytes = 210; break;
+    case KIND_IQ3_XXS: block = 256; bytes = 98; break;
+    case KIND_IQ4_NL: block = 32; bytes = 18; break;
+    case KIND_IQ4_XS: block = 256; bytes = 136; break;
+    case KIND_BF16: block = 1; bytes = 2; break;
     default: return ERR_QUANT_TYPE;
     }
     if (n <= 0 || n % block) return ERR_SHAPE;
@@ -102,6 +108,7 @@ int uq_init(int device) {
 int uq_shutdown(void) {
     if (!g_ctx.ready) return OK;
     hipStreamSynchronize(g_ctx.stream);
+    frontier_release();
     hipFree(g_ctx.dx);
     hipFree(g_ctx.dxq);
     hipFree(g_ctx.dxs);
@@ -125,17 +132,69 @@ int64_t uq_row_bytes(uint32_t kind, int64_t n) { return uq::row_bytes(kind, n); 
 }  // extern "C"
 
 namespace uq {
+// Frontier kinds: the GGUF blocks are split into their planes on the device
+// and every source byte is compared with its place in the planes.
+static int upload_split(uint32_t kind, int64_t n, int64_t m, const void* gguf, int64_t rb, const FrontierLayout& L,
+                        Weight& out) {
+    hipStream_t s = g_ctx.stream;
+    const int64_t blocks = n / L.block_vals * m;
+    size_t off[3], total = 0;
+    for (int p = 0; p < 3; p++) {
+        off[p] = total;
+        total += align256((size_t)(blocks * L.plane_bytes[p]));
+    }
+    Weight w;
+    w.kind = kind;
+    w.n = n;
+    w.m = m;
+    w.gguf_bytes = rb * m;
+    UQ_CHECK_HIP(hipMalloc(&w.alloc, std::max<size_t>(total, 256)));
+    w.alloc_bytes = total;
+    uint8_t* base = (uint8_t*)w.alloc;
+    uint8_t* planes[3] = {base + off[0], base + off[1], base + off[2]};
+    w.qs = (const int8_t*)planes[0];
+    w.sc = L.plane_bytes[1] ? planes[1] : nullptr;
+    w.d = L.plane_bytes[2] ? (const uint16_t*)planes[2] : nullptr;
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, (size_t)w.gguf_bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemsetAsync(g_ctx.dcount, 0, sizeof(unsigned), s);
+    if (e == hipSuccess) {
+        launch_layout_repack((const uint8_t*)staging, blocks, L, planes, s);
+        launch_layout_verify((const uint8_t*)staging, blocks, L, planes, g_ctx.dcount, s);
+        e = hipGetLastError();
+    }
+    unsigned bad = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&bad, g_ctx.dcount, sizeof(unsigned), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (staging) hipFree(staging);
+    int rc = OK;
+    if (e != hipSuccess) rc = set_error(ERR_DEVICE, std::string("weight_upload: ") + hipGetErrorString(e));
+    else if (bad) rc = set_error(ERR_DEVICE, "weight_upload: layout verify found " + std::to_string(bad) + " differing bytes");
+    if (rc != OK) {
+        hipFree(w.alloc);
+        return rc;
+    }
+    out = w;
+    return OK;
+}
+
 // Uploads, repacks and byte-verifies one GGUF tensor into w. bank = true lifts
 // the per-tensor row limit of llm.rs:248 (expert banks stack many tensors).
 int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank) {
     if (int rc = require_ctx()) return rc;
     if (!gguf) return set_error(ERR_ARG, "weight_upload: null pointer");
-    if (kind != KIND_Q8_0 && kind != KIND_Q4_K && kind != KIND_Q3_K)
-        return set_error(ERR_QUANT_TYPE, "weight_upload: kind must be Q8_0, Q4_K or Q3_K");
+    FrontierLayout fl;
+    const bool split = kind != KIND_Q8_0 && frontier_layout(kind, fl);
+    if (kind != KIND_Q8_0 && kind != KIND_Q4_K && kind != KIND_Q3_K && !split)
+        return set_error(ERR_QUANT_TYPE, "weight_upload: unsupported kind");
     const int64_t rb = uq::row_bytes(kind, n);
     if (rb < 0 || m <= 0 || n > MAX_N || (!bank && m > MAX_M) || m > (int64_t)1 << 26)
         return set_error(ERR_SHAPE, "weight_upload: bad shape");
+    if ((kind == KIND_F32 || kind == KIND_BF16) && n % 8)
+        return set_error(ERR_SHAPE, "weight_upload: F32/BF16 rows must hold a multiple of 8 values");
     if ((int64_t)bytes != rb * m) return set_error(ERR_SHAPE, "weight_upload: byte count != rows * row_bytes");
+    if (split) return upload_split(kind, n, m, gguf, rb, fl, out);
     hipStream_t s = g_ctx.stream;
     Weight w;
     w.kind = kind;

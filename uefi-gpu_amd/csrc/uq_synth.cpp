@@ -148,6 +148,31 @@ void gen_q3_k_row(Pcg32& g, int64_t n, uint8_t* out) {
     }
 }
 
+// The fp32-activation reader's kinds: uniform random code bytes with each
+// block's fp16 scale field lognormal (median 0.01, sigma 0.5); F32/BF16 rows
+// are 0.05 * N(0,1) (BF16 rounded to nearest even from the f32).
+void gen_frontier_row(Pcg32& g, uint32_t kind, int64_t n, uint8_t* out, int64_t rb) {
+    if (kind == 0 || kind == 30) {
+        for (int64_t i = 0; i < n; i++) {
+            const float v = (float)(0.05 * g.normal());
+            uint32_t b;
+            std::memcpy(&b, &v, 4);
+            if (kind == 0) std::memcpy(out + 4 * i, &b, 4);
+            else put16(out + 2 * i, (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16));
+        }
+        return;
+    }
+    for (int64_t i = 0; i < rb; i++) out[i] = (uint8_t)g.next();
+    int64_t block, size, off;
+    switch (kind) {
+    case 14: block = 256; size = 210; off = 208; break;
+    case 18: block = 256; size = 98; off = 0; break;
+    case 20: block = 32; size = 18; off = 0; break;
+    default: block = 256; size = 136; off = 0; break;  // 23
+    }
+    for (int64_t b = 0; b < n / block; b++) put16(out + b * size + off, lognormal_f16(g));
+}
+
 template <class F>
 void parallel_rows(int64_t rows, F&& f) {
     unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
@@ -169,18 +194,27 @@ void parallel_rows(int64_t rows, F&& f) {
 
 extern "C" {
 
-// GGUF-layout quantized rows (kind: 8 Q8_0, 11 Q3_K, 12 Q4_K); out holds
+// GGUF-layout quantized rows (kind: 8 Q8_0, 11 Q3_K, 12 Q4_K, and the
+// fp32-activation reader's 0 F32, 14 Q6_K, 18 IQ3_XXS, 20 IQ4_NL, 23 IQ4_XS,
+// 30 BF16); out holds
 // rows * row_bytes(kind, n). Returns 0, or -1 for an unknown kind / bad n.
 int uq_synth_quant(uint32_t kind, uint64_t seed, int64_t rows, int64_t n, uint8_t* out) {
     int64_t rb;
     if (kind == 8 && n > 0 && n % 32 == 0) rb = n / 32 * 34;
     else if (kind == 12 && n > 0 && n % 256 == 0) rb = n / 256 * 144;
     else if (kind == 11 && n > 0 && n % 256 == 0) rb = n / 256 * 110;
+    else if (kind == 14 && n > 0 && n % 256 == 0) rb = n / 256 * 210;
+    else if (kind == 18 && n > 0 && n % 256 == 0) rb = n / 256 * 98;
+    else if (kind == 20 && n > 0 && n % 32 == 0) rb = n / 32 * 18;
+    else if (kind == 23 && n > 0 && n % 256 == 0) rb = n / 256 * 136;
+    else if (kind == 0 && n > 0) rb = n * 4;
+    else if (kind == 30 && n > 0) rb = n * 2;
     else return -1;
     if (rows <= 0 || !out) return -1;
     parallel_rows(rows, [&](int64_t r) {
         Pcg32 g = Pcg32::row_stream(seed, (uint64_t)r);
-        if (kind == 8) gen_q8_0_row(g, n, out + r * rb);
+        if (kind != 8 && kind != 11 && kind != 12) gen_frontier_row(g, kind, n, out + r * rb, rb);
+        else if (kind == 8) gen_q8_0_row(g, n, out + r * rb);
         else if (kind == 12) gen_q4_k_row(g, n, out + r * rb);
         else gen_q3_k_row(g, n, out + r * rb);
     });

@@ -19,6 +19,9 @@ LIB_PATH = os.path.join(HERE, "libuq.so")
 
 OK = 0
 KIND_F32, KIND_Q8_0, KIND_Q3_K, KIND_Q4_K = 0, 8, 11, 12
+KIND_Q6_K, KIND_IQ3_XXS, KIND_IQ4_NL, KIND_IQ4_XS, KIND_BF16 = 14, 18, 20, 23, 30
+# kinds of the fp32-activation reader (frontier_core.rs:53-58)
+LINEAR_KINDS = (KIND_F32, KIND_BF16, KIND_Q8_0, KIND_Q6_K, KIND_IQ3_XXS, KIND_IQ4_NL, KIND_IQ4_XS)
 
 
 class Error(enum.IntEnum):
@@ -68,6 +71,11 @@ _SIGS = {
     "uq_gateup_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "uq_quant_act": (ctypes.c_int, [_c_f32p, _i64, _c_i8p, _c_f32p]),
     "uq_block_dots": (ctypes.c_int, [_vp, _c_f32p, _i64, _c_i32p, _i64]),
+    "uq_dequantize": (ctypes.c_int, [ctypes.c_uint32, _vp, ctypes.c_size_t, _i64, _c_f32p]),
+    "uq_linear": (ctypes.c_int, [_vp, _c_f32p, _i64, _c_f32p, _i64]),
+    "uq_linear_batch": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "uq_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "uq_linear_multi_dev": (ctypes.c_int, [_vp, ctypes.c_int, _vp]),
     "uq_dev_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "uq_dev_free": (ctypes.c_int, [_vp]),
     "uq_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
@@ -237,6 +245,37 @@ def batch(ws, x):
     yp = (_c_f32p * len(ws))(*[_p(y, _c_f32p) for y in ys])
     ms = (ctypes.c_int64 * len(ws))(*[w.m for w in ws])
     _check(lib().uq_batch(handles, len(ws), _p(x, _c_f32p), x.size, yp, ms))
+    return ys
+
+
+class LinearJob(ctypes.Structure):
+    """uq_linear_job: one entry of the FrontierJob table."""
+    _fields_ = [("weight", _vp), ("x", _vp), ("y", _vp)]
+
+
+def dequantize(kind, raw, n):
+    """frontier_dequant: the n values of a GGUF byte run as f32 (bit-exact)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(int(n), dtype=np.float32)
+    _check(lib().uq_dequantize(kind, raw.ctypes.data, raw.nbytes, int(n), _p(out, _c_f32p)))
+    return out
+
+
+def linear(w, x):
+    """Weights::linear over frontier_matvec: y = W x with fp32 x."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(w.m, dtype=np.float32)
+    _check(lib().uq_linear(w.handle, _p(x, _c_f32p), x.size, _p(y, _c_f32p), y.size))
+    return y
+
+
+def linear_batch(pairs):
+    """Weights::batch: [(weight, x), ...] in one launch; returns the outputs."""
+    xs = [np.ascontiguousarray(x, dtype=np.float32) for _, x in pairs]
+    ys = [np.empty(w.m, dtype=np.float32) for w, _ in pairs]
+    jobs = (LinearJob * len(pairs))(*[LinearJob(w.handle, x.ctypes.data, y.ctypes.data)
+                                      for (w, _), x, y in zip(pairs, xs, ys)])
+    _check(lib().uq_linear_batch(jobs, len(pairs)))
     return ys
 
 

@@ -187,6 +187,30 @@ def moe_bench(steps=64):
             "steps": steps, "bytes_per_step": step_bytes}
 
 
+LINEAR_NAMES = {uq.KIND_F32: "F32", uq.KIND_BF16: "BF16", uq.KIND_Q8_0: "Q8_0", uq.KIND_Q6_K: "Q6_K",
+                uq.KIND_IQ3_XXS: "IQ3_XXS", uq.KIND_IQ4_NL: "IQ4_NL", uq.KIND_IQ4_XS: "IQ4_XS"}
+
+
+def linear_sweep(n=2560, copies=3, reps=20):
+    """fp32-activation reader (the frontier backend's matvec): per kind one
+    m x 2560 weight of about 128 MB, 3 rotating copies (more than the 256 MB
+    MALL), one launch per copy in turn. Bytes per launch: the GGUF weight
+    bytes + 4n (x) + 4m (y)."""
+    out = {}
+    for kind in uq.LINEAR_KINDS:
+        rb = uq.row_bytes(kind, n)
+        m = min(160000, (128 << 20) // rb)
+        ws = [uq.Weight(kind, n, m, uq.synth_quant(kind, 0x5EED0020 + 16 * kind + c, m, n)) for c in range(copies)]
+        ms = uq.time_linear(ws, reps, 2)
+        for w in ws:
+            w.free()
+        nbytes = m * rb + 4 * n + 4 * m
+        gbs = nbytes * copies * reps / (ms / 1e3) / 1e9
+        out[LINEAR_NAMES[kind]] = {"rows": m, "bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3 / (copies * reps), 2),
+                                   "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,7 +219,7 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
-    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe"],
+    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe", "linear"],
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -206,7 +230,7 @@ def main():
     uq.init(0)
     if args.leg:
         leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "q4k": q4k_sweep, "q3k": q3k_sweep,
-               "moe": moe_bench}[args.leg]
+               "moe": moe_bench, "linear": linear_sweep}[args.leg]
         print(json.dumps({args.leg: leg()}), flush=True)
         return
     weights, pairs, shape_of = [], [], []

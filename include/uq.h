@@ -140,6 +140,10 @@ int uq_linear_batch(const uq_linear_job* jobs, int count);
  * be 16-byte aligned. */
 int uq_linear_dev(uq_weight_t w, const float* x, float* y, void* stream);
 int uq_linear_multi_dev(const uq_linear_job* jobs, int count, void* stream);
+/* Measurement aid (no reference counterpart): `reps` rounds, after `warmup`
+ * untimed ones, of one uq_linear_dev launch per weight in turn (zero x, each
+ * weight its own output); total_ms = HIP-event time of the timed rounds. */
+int uq_time_linear(const uq_weight_t* ws, int count, int reps, int warmup, double* total_ms);
 
 /* ---------------------------------------------------------------- memory + timing
  * Small helpers so harnesses need no other GPU runtime binding. */

@@ -80,6 +80,36 @@ def test_linear_random_shapes(gpu, kind, n, m):
     assert d.max() <= 1 and (d == 0).mean() > 0.999, (d.max(), (d == 0).mean())
 
 
+def wide_range_x(n, seed):
+    """x whose 32-blocks exercise the exact-integer staging: zeros, denormals,
+    a 2^20 range (double path), 1e30 beside 1e-30 (double path), small values
+    with zero low bits beside a large one (integer path), -0.0, ordinary."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    x[0:32] = 0
+    x[32:64] = (rng.normal(0, 1, 32) * 1e-41).astype(np.float32)          # denormals
+    x[64:96] = rng.normal(0, 1, 32).astype(np.float32) * np.float32(2.0) ** rng.integers(-20, 1, 32)
+    x[96:128] = rng.normal(0, 1, 32).astype(np.float32)
+    x[96], x[97] = 1e30, -1e-30
+    x[128:160] = (rng.integers(-8, 8, 32) * 2.0 ** -20).astype(np.float32)
+    x[128] = 3.0e3
+    x[160:192] = -0.0
+    return x
+
+
+@pytest.mark.parametrize("kind", [k for k in KINDS if k not in (uq.KIND_F32, uq.KIND_BF16)])
+def test_linear_wide_range_blocks(gpu, kind):
+    n, m = 2560, 300
+    raw = uq.synth_quant(kind, 0x71DE + kind, m, n)
+    x = wide_range_x(n, kind)
+    w = uq.Weight(kind, n, m, raw)
+    y = uq.linear(w, x)
+    ref = O.linear(kind, raw, n, m, x)
+    assert np.isfinite(y).all()
+    assert ulps(y, ref).max() <= 1
+    assert tol_ok(y, ref)
+
+
 def test_multi_format_job_table(gpu):
     # frontier_gpu.rs:281-307: all seven kinds in one dispatch, non-four-row tails
     n = 2560

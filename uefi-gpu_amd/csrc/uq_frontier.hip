@@ -74,6 +74,7 @@ __constant__ uint32_t c_iq3_grid[256] = {
 };
 
 constexpr int FWG = 256;
+constexpr int FL_WG = 512;  // workgroup of the linear kernel
 
 // ---------------------------------------------------------------- dequant
 // One value per thread from the GGUF bytes, the formulas and f32 multiply
@@ -173,27 +174,147 @@ struct FJob {
     float* y;
     int64_t m, pitch;
     int32_t kind, n;
-    int32_t wg0, pad;  // first workgroup of the job
+    int32_t wg0, wgs;  // first workgroup of the job, workgroups of the job
 };
 
-// Per-kind unit readers. A lane owns units u = sub, sub + LPR, ... of a row;
-// dot() returns sum over the unit's scale groups of scale * sum(code * x).
-// signed bit field (v_bfe_i32); the builtin takes the signedness of its first
-// operand, so the field is extracted from an int
-__device__ __forceinline__ int sbf(uint32_t v, int off, int width) {
-    return __builtin_amdgcn_sbfe((int)v, off, width);
+// ---- exact integer form of x
+// Each 32-block of x is staged in LDS as integers X_j with x_j = X_j *
+// 2^(E - XSHIFT), E = max(biased exponent of max|x_j|, 1): X_j = m_j *
+// 2^(e_j - E + 14) for the 24-bit significand m_j, |X_j| < 2^38, exact when
+// every element lies within 2^14 of the block maximum (or its dropped low bits
+// are zero). X_j is held as five balanced base-256 digits in five byte planes,
+// so sum(code * X) over a block is five v_dot4 sums recombined exactly in
+// double (|sum| < 2^51). A block that is not exact (wider range, or a
+// non-finite value) is marked and its dots run in double from x itself.
+constexpr int XSHIFT = 164, NLIMB = 5;
+
+struct XStage {
+    const uint32_t* limb;  // NLIMB planes of n/16 16-byte chunks (16 elements), in unit-major slots
+    const int* bexp;       // per 32-block: E, or -1 when the block takes the double path
+    const float* xg;       // x in global memory (double path)
+    const float* xf;       // F32 / BF16 weights: x as f32 in LDS
+    int n4;                // n / 4: dwords per plane
+};
+
+// Digit chunks are held unit-major: chunk k (elements 16k..16k+15) of the
+// job's kind sits in slot pos * NU + u, u its unit and pos its place in the
+// unit (NU units per row), so the lanes of a row group, which own
+// consecutive units, read consecutive 16-byte slots.
+__device__ __forceinline__ int chunk_slot(uint32_t kind, int k, int n) {
+    switch (kind) {
+    case KIND_Q6_K: {  // unit 4s + 2sub + h holds chunks 16s + 8sub + 2g + h, place g
+        const int u = 4 * (k >> 4) + 2 * ((k >> 3) & 1) + (k & 1);
+        return ((k >> 1) & 3) * (n / 64) + u;
+    }
+    case KIND_IQ3_XXS: return (k & 7) * (n / 128) + (k >> 3);
+    default: return (k & 1) * (n / 32) + (k >> 1);  // Q8_0, IQ4_NL, IQ4_XS: 2 chunks per unit
+    }
 }
-__device__ __forceinline__ int sx8(uint32_t v, int byte) { return sbf(v, 8 * byte, 8); }
-__device__ __forceinline__ double fx(const float* xl, int i) { return (double)xl[i]; }
+
+// sum(code * x) over NC chunks (4 dwords of packed signed codes each) in
+// slots slot0, slot0 + sstride, ...; e0 = first element (32-block exponent,
+// double path) and the chunks cover elements e0 + 16*c.
+template <int NC>
+__device__ __forceinline__ double seg_dot(const uint32_t (&c)[4 * NC], const XStage& xs, int e0, int slot0,
+                                          int sstride) {
+    const int E = xs.bexp[e0 >> 5];
+    if (E >= 0) {
+        int S[NLIMB];
+#pragma unroll
+        for (int l = 0; l < NLIMB; l++) {
+            int a = 0;
+#pragma unroll
+            for (int ch = 0; ch < NC; ch++) {
+                const uint4 p = ((const uint4*)xs.limb)[l * (xs.n4 >> 2) + slot0 + ch * sstride];
+                a = uq_dot4((int)c[4 * ch + 0], (int)p.x, a);
+                a = uq_dot4((int)c[4 * ch + 1], (int)p.y, a);
+                a = uq_dot4((int)c[4 * ch + 2], (int)p.z, a);
+                a = uq_dot4((int)c[4 * ch + 3], (int)p.w, a);
+            }
+            S[l] = a;
+        }
+        double t = (double)S[NLIMB - 1];
+#pragma unroll
+        for (int l = NLIMB - 2; l >= 0; l--) t = __builtin_fma(t, 256.0, (double)S[l]);
+        return __builtin_ldexp(t, E - XSHIFT);
+    }
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int q = 0; q < 4 * NC; q++)
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            s[k] = __builtin_fma((double)(int)(int8_t)(uint8_t)(c[q] >> (8 * k)), (double)xs.xg[e0 + 4 * q + k], s[k]);
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// Stages x of one job, 4 elements per thread (8 threads per 32-block): the
+// block's exponent from the 8-lane max of |x|, each X_j, and its five digits
+// packed 4 elements per dword into the five planes (byte l of X_j + 0x80 in
+// every digit position, minus 0x80: balanced digits in [-128, 127]).
+__device__ void stage_x(const float* __restrict__ x, int n, uint32_t kind, uint32_t* limb, int* bexp) {
+    const int n4 = n / 4;
+    for (int q = threadIdx.x; q < ((n4 + 7) & ~7); q += FL_WG) {
+        // q < n4 for the whole 8-lane group or for none of it (n % 32 == 0)
+        if (q < n4) {
+            const float4 v4 = ((const float4*)x)[q];
+            const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            amax = uq_group_max<8>(amax);
+            int E = (int)(__builtin_bit_cast(uint32_t, amax) >> 23);
+            bool ok = E < 255 && !(amax != amax);
+            E = E < 1 ? 1 : E;
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t bits = __builtin_bit_cast(uint32_t, v[k]);
+                const int eb = (int)((bits >> 23) & 255);
+                uint32_t m = bits & 0x7FFFFFu;
+                if (eb) m |= 0x800000u;
+                const int sh = (eb < 1 ? 1 : eb) - E + 14;
+                int64_t X = 0;
+                if (eb == 255) ok = false;
+                else if (sh >= 0) X = (int64_t)m << sh;
+                else if (sh > -24 && (m & ((1u << -sh) - 1u)) == 0) X = (int64_t)(m >> -sh);
+                else if (m != 0) ok = false;
+                if (bits >> 31) X = -X;
+                // offset binary: digit l = byte l of (X + 0x8080808080) - 0x80
+                const uint64_t Y = (uint64_t)(X + (int64_t)0x8080808080ll);
+                lo[k] = (uint32_t)Y ^ 0x80808080u;
+                hi[k] = (uint32_t)(Y >> 32) ^ 0x80u;
+            }
+            // 4x4 byte transpose of lo[] (plane l = byte l of each element), then plane 4
+            const uint32_t a01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x05010400u);
+            const uint32_t a23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x05010400u);
+            const uint32_t b01 = __builtin_amdgcn_perm(lo[1], lo[0], 0x07030602u);
+            const uint32_t b23 = __builtin_amdgcn_perm(lo[3], lo[2], 0x07030602u);
+            // a01 = [e0.b0, e1.b0, e0.b1, e1.b1], b01 = [e0.b2, e1.b2, e0.b3, e1.b3]
+            const int at = 4 * chunk_slot(kind, q >> 2, n) + (q & 3);  // dword within a plane
+            limb[0 * n4 + at] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+            limb[1 * n4 + at] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+            limb[2 * n4 + at] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+            limb[3 * n4 + at] = __builtin_amdgcn_perm(b23, b01, 0x07060302u);
+            const uint32_t h01 = __builtin_amdgcn_perm(hi[1], hi[0], 0x0C0C0400u);
+            const uint32_t h23 = __builtin_amdgcn_perm(hi[3], hi[2], 0x0C0C0400u);
+            limb[4 * n4 + at] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
+            const bool all_ok = uq_group_max<8>(ok ? 0.0f : 1.0f) == 0.0f;
+            if ((q & 7) == 0) bexp[q >> 3] = all_ok ? E : -1;
+        }
+    }
+}
+
+// ---- per-kind unit readers
+// A lane owns units u = sub, sub + LPR, ... of a row; dot() returns the unit's
+// sum over scale groups of scale * sum(code * x).
 
 // 4 IQ4 codes of the low nibbles of the 4 bytes of `nib` (upper nibbles
-// ignored), packed as signed bytes: v_perm_b32 over the two halves of the
-// code book, then the half picked by bit 3 of each nibble.
+// ignored), packed as signed bytes: v_perm_b32 over each half of the code
+// book, then a third v_perm_b32 takes byte k from the half picked by bit 3 of
+// nibble k (selector k, or k + 4 for the upper half).
 __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t nib, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
     const uint32_t sel = nib & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel), hi = __builtin_amdgcn_perm(t3, t2, sel);
-    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
-    return (hi & m) | (lo & ~m);
+    const uint32_t pick = ((nib >> 1) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(hi, lo, pick);
 }
 struct Iq4Book {
     uint32_t t0, t1, t2, t3;
@@ -205,29 +326,25 @@ struct Iq4Book {
         t3 = b[3];
     }
 };
-// sum of code * x over 32 IQ4 codes of one 16-byte unit (low nibbles -> x[0..15], high -> x[16..31])
-__device__ __forceinline__ double iq4_dot32(const uint4& w, const float* x, const Iq4Book& bk) {
+// the 32 codes of one 16-byte IQ4 unit (low nibbles -> elements 0..15, high -> 16..31)
+__device__ __forceinline__ double iq4_dot32(const uint4& w, const XStage& xs, int u, const Iq4Book& bk) {
     const uint32_t v[4] = {w.x, w.y, w.z, w.w};
-    double s = 0.0;
+    uint32_t c[8];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        const uint32_t lo = iq4_lookup4(v[q], bk.t0, bk.t1, bk.t2, bk.t3);
-        const uint32_t hi = iq4_lookup4(v[q] >> 4, bk.t0, bk.t1, bk.t2, bk.t3);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            s = __builtin_fma((double)sx8(lo, k), fx(x, 4 * q + k), s);
-            s = __builtin_fma((double)sx8(hi, k), fx(x, 16 + 4 * q + k), s);
-        }
+        c[q] = iq4_lookup4(v[q], bk.t0, bk.t1, bk.t2, bk.t3);
+        c[4 + q] = iq4_lookup4(v[q] >> 4, bk.t0, bk.t1, bk.t2, bk.t3);
     }
-    return s;
+    return seg_dot<2>(c, xs, 32 * u, u, xs.n4 / 8);
 }
 
 template <uint32_t K>
 struct FK;
 
+// F32 / BF16 weights are not small-integer codes: products in double from x.
 template <>
 struct FK<KIND_F32> {
-    static constexpr int WPU = 8, LPR = 16;
+    static constexpr int WPU = 8, LPR = 16, CH = 4;
     struct U {
         uint4 a, b;
     };
@@ -235,41 +352,45 @@ struct FK<KIND_F32> {
         const uint4* p = (const uint4*)(j.body + row * j.pitch) + 2 * u;
         return {p[0], p[1]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book&) {
-        const float* x = xl + 8 * u;
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book&) {
+        const float* x = xs.xf + 8 * u;
+        const float4 xa = ((const float4*)x)[0], xb = ((const float4*)x)[1];
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
         const uint32_t w[8] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w};
-        double s = 0.0;
+        double s[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int k = 0; k < 8; k++) s = __builtin_fma((double)uq_bits_f(w[k]), fx(x, k), s);
-        return s;
+        for (int k = 0; k < 8; k++) s[k & 3] = __builtin_fma((double)uq_bits_f(w[k]), (double)xv[k], s[k & 3]);
+        return (s[0] + s[1]) + (s[2] + s[3]);
     }
 };
 
 template <>
 struct FK<KIND_BF16> {
-    static constexpr int WPU = 8, LPR = 16;
+    static constexpr int WPU = 8, LPR = 16, CH = 4;
     struct U {
         uint4 a;
     };
     static __device__ U load(const FJob& j, int64_t row, int u) {
         return {((const uint4*)(j.body + row * j.pitch))[u]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book&) {
-        const float* x = xl + 8 * u;
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book&) {
+        const float* x = xs.xf + 8 * u;
+        const float4 xa = ((const float4*)x)[0], xb = ((const float4*)x)[1];
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
         const uint32_t w[4] = {v.a.x, v.a.y, v.a.z, v.a.w};
-        double s = 0.0;
+        double s[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            s = __builtin_fma((double)uq_bits_f(w[k] << 16), fx(x, 2 * k), s);
-            s = __builtin_fma((double)uq_bits_f(w[k] & 0xFFFF0000u), fx(x, 2 * k + 1), s);
+            s[k] = __builtin_fma((double)uq_bits_f(w[k] << 16), (double)xv[2 * k], s[k]);
+            s[k] = __builtin_fma((double)uq_bits_f(w[k] & 0xFFFF0000u), (double)xv[2 * k + 1], s[k]);
         }
-        return s;
+        return (s[0] + s[1]) + (s[2] + s[3]);
     }
 };
 
 template <>
 struct FK<KIND_Q8_0> {
-    static constexpr int WPU = 32, LPR = 16;
+    static constexpr int WPU = 32, LPR = 16, CH = 4;
     struct U {
         uint4 a, b;
         uint32_t d;
@@ -278,21 +399,15 @@ struct FK<KIND_Q8_0> {
         const uint4* p = (const uint4*)(j.body + row * j.pitch) + 2 * u;
         return {p[0], p[1], j.d[row * (j.n / 32) + u]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book&) {
-        const float* x = xl + 32 * u;
-        const uint32_t w[8] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w};
-        double s = 0.0;
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) s = __builtin_fma((double)sx8(w[q], k), fx(x, 4 * q + k), s);
-        return (double)uq_half((uint16_t)v.d) * s;
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book&) {
+        const uint32_t c[8] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w};
+        return (double)uq_half((uint16_t)v.d) * seg_dot<2>(c, xs, 32 * u, u, xs.n4 / 8);
     }
 };
 
 template <>
 struct FK<KIND_IQ4_NL> {
-    static constexpr int WPU = 32, LPR = 16;
+    static constexpr int WPU = 32, LPR = 16, CH = 4;
     struct U {
         uint4 a;
         uint32_t d;
@@ -300,14 +415,14 @@ struct FK<KIND_IQ4_NL> {
     static __device__ U load(const FJob& j, int64_t row, int u) {
         return {((const uint4*)(j.body + row * j.pitch))[u], j.d[row * (j.n / 32) + u]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book& bk) {
-        return (double)uq_half((uint16_t)v.d) * iq4_dot32(v.a, xl + 32 * u, bk);
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book& bk) {
+        return (double)uq_half((uint16_t)v.d) * iq4_dot32(v.a, xs, u, bk);
     }
 };
 
 template <>
 struct FK<KIND_IQ4_XS> {
-    static constexpr int WPU = 32, LPR = 16;
+    static constexpr int WPU = 32, LPR = 16, CH = 4;
     struct U {
         uint4 a;
         uint2 h;  // block head: d | scales_h << 16, scales_l
@@ -316,11 +431,11 @@ struct FK<KIND_IQ4_XS> {
         const uint2 h = ((const uint2*)j.aux)[row * (j.n / 256) + u / 8];
         return {((const uint4*)(j.body + row * j.pitch))[u], h};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book& bk) {
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book& bk) {
         const int sb = u & 7;
         const int sc = (int)((v.h.y >> (4 * sb)) & 15) | (int)(((v.h.x >> (16 + 2 * sb)) & 3) << 4);
         const float scale = uq_half((uint16_t)(v.h.x & 0xFFFF)) * (float)(sc - 32);
-        return (double)scale * iq4_dot32(v.a, xl + 32 * u, bk);
+        return (double)scale * iq4_dot32(v.a, xs, u, bk);
     }
 };
 
@@ -328,7 +443,7 @@ struct FK<KIND_IQ4_XS> {
 // qh[sub*32 + 16h ..] (16 bytes each) and the 4 group scales sc[sub*8 + h + 2g].
 template <>
 struct FK<KIND_Q6_K> {
-    static constexpr int WPU = 64, LPR = 8;
+    static constexpr int WPU = 64, LPR = 8, CH = 2;
     struct U {
         uint4 l0, l1, h;
         uint32_t sc, d;
@@ -338,26 +453,25 @@ struct FK<KIND_Q6_K> {
         const uint32_t sc = ((const uint32_t*)j.aux)[row * (j.n / 64) + u];
         return {p[0], p[1], p[2], sc, j.d[row * (j.n / 256) + u / 4]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t*, const Iq4Book&) {
-        const float* x = xl + 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1);
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t*, const Iq4Book&) {
+        const int e0 = 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1);
         const float d = uq_half((uint16_t)v.d);
         const uint32_t l0[4] = {v.l0.x, v.l0.y, v.l0.z, v.l0.w}, l1[4] = {v.l1.x, v.l1.y, v.l1.z, v.l1.w};
         const uint32_t hh[4] = {v.h.x, v.h.y, v.h.z, v.h.w};
         double r = 0.0;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            double s = 0.0;
+            uint32_t c[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const uint32_t lo = ((g & 1 ? l1[q] : l0[q]) >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
-                const uint32_t c = (lo | (((hh[q] >> (2 * g)) & 0x03030303u) << 4)) ^ 0x20202020u;
-                // 6-bit codes with bit 5 flipped, sign-extended: code - 32
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    s = __builtin_fma((double)sbf(c, 8 * k, 6), fx(x, 32 * g + 4 * q + k), s);
+                // 6-bit code with bit 5 flipped, its sign bit copied to bits 6-7: code - 32
+                const uint32_t t = (lo | (((hh[q] >> (2 * g)) & 0x03030303u) << 4)) ^ 0x20202020u;
+                const uint32_t s5 = t & 0x20202020u;
+                c[q] = t | (s5 << 1) | (s5 << 2);
             }
-            const float scale = d * (float)sx8(v.sc, g);
-            r = __builtin_fma((double)scale, s, r);
+            const float scale = d * (float)(int8_t)(uint8_t)(v.sc >> (8 * g));
+            r = __builtin_fma((double)scale, seg_dot<1>(c, xs, e0 + 32 * g, g * (xs.n4 / 16) + u, 0), r);
         }
         return r;
     }
@@ -367,7 +481,7 @@ struct FK<KIND_Q6_K> {
 // bytes) then their 4 sign/scale words (16 bytes).
 template <>
 struct FK<KIND_IQ3_XXS> {
-    static constexpr int WPU = 128, LPR = 4;
+    static constexpr int WPU = 128, LPR = 4, CH = 2;
     struct U {
         uint4 q0, q1, a;
         uint32_t d;
@@ -376,90 +490,217 @@ struct FK<KIND_IQ3_XXS> {
         const uint4* p = (const uint4*)(j.body + row * j.pitch) + 3 * u;
         return {p[0], p[1], p[2], j.d[row * (j.n / 256) + u / 2]};
     }
-    static __device__ double dot(const U& v, const float* xl, int u, const uint32_t* grid, const Iq4Book&) {
-        const float* x = xl + 128 * u;
+    // the 4 signs of `bits` (bit k -> byte k) applied to 4 unsigned bytes
+    static __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t bits) {
+        // bit k -> bit 8k (bits < 16, a 24-bit multiply; the shifted copies never overlap)
+        const uint32_t b = (uint32_t)__mul24((int)bits, 0x00204081) & 0x01010101u;
+        const uint32_t m = (b << 8) - b;  // 0xFF in each byte whose sign bit is set
+        return (g ^ m) + b;               // bytes of g are <= 62: no carry between bytes
+    }
+    static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t* grid, const Iq4Book&) {
         const float d = uq_half((uint16_t)v.d);
         const uint32_t qs[8] = {v.q0.x, v.q0.y, v.q0.z, v.q0.w, v.q1.x, v.q1.y, v.q1.z, v.q1.w};
         const uint32_t aux[4] = {v.a.x, v.a.y, v.a.z, v.a.w};
         double r = 0.0;
 #pragma unroll
         for (int l = 0; l < 4; l++) {
-            double s = 0.0;
+            uint32_t c[8];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const uint32_t s7 = (aux[l] >> (7 * g)) & 127u;
                 const uint32_t sg = s7 | ((uint32_t)(__popc(s7) & 1) << 7);
                 const uint32_t word = qs[2 * l + (g >> 1)];
                 const uint32_t g0 = grid[(word >> (16 * (g & 1))) & 255], g1 = grid[(word >> (16 * (g & 1) + 8)) & 255];
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const int q = (int)(((t < 4 ? g0 : g1) >> (8 * (t & 3))) & 255);
-                    const int c = (sg >> t) & 1 ? -q : q;
-                    s = __builtin_fma((double)c, fx(x, 32 * l + 8 * g + t), s);
-                }
+                c[2 * g] = apply_signs(g0, sg & 15u);
+                c[2 * g + 1] = apply_signs(g1, sg >> 4);
             }
             const float scale = d * (0.5f + (float)(aux[l] >> 28)) * 0.5f;
-            r = __builtin_fma((double)scale, s, r);
+            r = __builtin_fma((double)scale, seg_dot<2>(c, xs, 128 * u + 32 * l, 2 * l * (xs.n4 / 32) + u, xs.n4 / 32), r);
         }
         return r;
     }
 };
 
-// Rows of one job for this workgroup: LPR lanes per row, 64/LPR rows per
-// wave; a lane walks its units in order with the next unit's loads issued
-// before the current unit's dot; the lane group sums in double and rounds once.
+// Rows of one job for workgroup `wgi` of `wgc`: LPR lanes per row, 64/LPR
+// rows per wave, row blocks wgi, wgi + wgc, ... A lane owns units u = sub +
+// LPR*i of its row and walks them in chunks of CH units: the next chunk's
+// loads (the same row's or the next row block's) are issued before the
+// current chunk's dots. Per row the lane adds its units in order; the lane
+// group sums in double and rounds once.
 template <class T>
-__device__ void job_rows(const FJob& j, int wgi, const float* xl, const uint32_t* grid) {
-    constexpr int LPR = T::LPR, RPW = 64 / LPR, RPB = RPW * (FWG / 64);
+__device__ void job_rows(const FJob& j, int wgi, int wgc, const XStage& xs, const uint32_t* grid) {
+    constexpr int LPR = T::LPR, CH = T::CH, RPW = 64 / LPR, RPB = RPW * (FL_WG / 64);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane % LPR, grp = lane / LPR;
-    const int64_t row = (int64_t)wgi * RPB + wave * RPW + grp;
-    const int64_t rr = row < j.m ? row : j.m - 1;
     const int nu = j.n / T::WPU;
+    const int nb = (nu + LPR - 1) / LPR;    // unit slots per lane and row
+    const int nch = (nb + CH - 1) / CH;      // chunks per row
+    const int64_t rblocks = (j.m + RPB - 1) / RPB;
+    if (wgi >= rblocks) return;
     const Iq4Book bk;
+    typename T::U buf[2][CH];
+    // (row block, chunk) of the next fetch, advanced without division
+    int64_t frb = wgi;
+    int fc = 0;
+    auto fetch = [&](typename T::U (&b)[CH]) {
+        const int64_t row = frb * RPB + wave * RPW + grp;
+        const int64_t rr = row < j.m ? row : j.m - 1;
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int u = sub + LPR * (fc * CH + k);
+            if (fc * CH + k < nb) b[k] = T::load(j, rr, u < nu ? u : nu - 1);  // slot test is wave-uniform
+        }
+        if (++fc == nch) {
+            fc = 0;
+            frb += wgc;
+        }
+    };
+    fetch(buf[0]);
+    int64_t rb = wgi;
+    int c = 0;
     double acc = 0.0;
-    int u = sub;
-    typename T::U cur = T::load(j, rr, u < nu ? u : nu - 1);
-    for (; u < nu; u += LPR) {
-        const int un = u + LPR;
-        const typename T::U nxt = T::load(j, rr, un < nu ? un : nu - 1);
-        acc = acc + T::dot(cur, xl, u, grid, bk);
-        cur = nxt;
+    while (rb < rblocks) {
+        // two chunks per trip so the chunk buffers keep fixed registers
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            if (rb < rblocks) {
+                if (frb < rblocks) fetch(buf[h ^ 1]);
+#pragma unroll
+                for (int k = 0; k < CH; k++) {
+                    const int u = sub + LPR * (c * CH + k);
+                    if (c * CH + k < nb) {
+                        const double d = T::dot(buf[h][k], xs, u < nu ? u : nu - 1, grid, bk);
+                        acc = acc + (u < nu ? d : 0.0);
+                    }
+                }
+                if (++c == nch) {
+                    const int64_t row = rb * RPB + wave * RPW + grp;
+                    const double sum = uq_group_sum<LPR>(acc);
+                    if (row < j.m && sub == 0) j.y[row] = (float)sum;
+                    acc = 0.0;
+                    c = 0;
+                    rb += wgc;
+                }
+            }
+        }
     }
-    acc = uq_group_sum<LPR>(acc);
-    if (row < j.m && sub == 0) j.y[row] = (float)acc;
 }
 
 template <class T>
 constexpr int rows_per_wg() {
-    return (64 / T::LPR) * (FWG / 64);
+    return (64 / T::LPR) * (FL_WG / 64);
 }
 
-// One launch over a job table (wg0 ascending): the workgroup finds its job,
-// stages that job's x (n floats) and the IQ3 grid in LDS, and runs its rows.
-__global__ __launch_bounds__(FWG) void k_flinear(const FJob* __restrict__ jobs, int count) {
-    extern __shared__ __attribute__((aligned(16))) float fl_x[];
-    __shared__ uint32_t lgrid[256];
-    int lo = 0, hi = count;
+// Up to MAX_JOBS jobs per launch, passed by value in the kernel arguments
+// (no device table to copy before the launch); longer tables take several
+// launches, each row computed the same way.
+constexpr int MAX_JOBS = 32;
+struct JobArgs {
+    FJob job[MAX_JOBS];
+    int count;
+};
+
+// Shared front of the linear kernels: the workgroup's job (wg0 ascending)
+// and its staged x.
+__device__ __forceinline__ FJob find_job(const JobArgs& a) {
+    int lo = 0, hi = a.count;
     while (lo + 1 < hi) {
         const int mid = (lo + hi) >> 1;
-        if (jobs[mid].wg0 <= (int)blockIdx.x) lo = mid;
+        if (a.job[mid].wg0 <= (int)blockIdx.x) lo = mid;
         else hi = mid;
     }
-    const FJob j = jobs[lo];
-    for (int i = threadIdx.x; i < j.n / 4; i += FWG) ((float4*)fl_x)[i] = ((const float4*)j.x)[i];
-    lgrid[threadIdx.x] = c_iq3_grid[threadIdx.x];
+    return a.job[lo];
+}
+template <bool INTS>
+__device__ __forceinline__ XStage stage_job(const FJob& j, uint32_t* fl_lds, uint32_t* lgrid) {
+    XStage xs;
+    xs.limb = fl_lds;
+    xs.bexp = (const int*)(fl_lds + NLIMB * (j.n / 4));
+    xs.xg = j.x;
+    xs.xf = (const float*)fl_lds;
+    xs.n4 = j.n / 4;
+    if (INTS) stage_x(j.x, j.n, (uint32_t)j.kind, fl_lds, (int*)(fl_lds + NLIMB * (j.n / 4)));
+    else
+        for (int i = threadIdx.x; i < j.n / 4; i += FL_WG) ((float4*)fl_lds)[i] = ((const float4*)j.x)[i];
+    if (threadIdx.x < 256) lgrid[threadIdx.x] = c_iq3_grid[threadIdx.x];
     __syncthreads();
-    const int wgi = (int)blockIdx.x - j.wg0;
+    return xs;
+}
+
+// Jobs of one kind: registers sized for that kind alone.
+template <uint32_t K>
+__global__ __launch_bounds__(FL_WG) void k_flinear_kind(JobArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t fl_lds[];
+    __shared__ uint32_t lgrid[256];
+    const FJob j = find_job(a);
+    const XStage xs = stage_job<K != KIND_F32 && K != KIND_BF16>(j, fl_lds, lgrid);
+    job_rows<FK<K>>(j, (int)blockIdx.x - j.wg0, j.wgs, xs, lgrid);
+}
+
+// One launch over a job table of mixed kinds (wg0 ascending): the workgroup finds its job,
+// stages that job's x (integer digit planes and block exponents) and the IQ3
+// grid in LDS, and runs its rows. Dynamic LDS: NLIMB * n + 4 * (n / 32) bytes
+// (F32 / BF16 weights: x as 4 * n bytes of f32).
+__global__ __launch_bounds__(FL_WG) void k_flinear(JobArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t fl_lds[];
+    __shared__ uint32_t lgrid[256];
+    const FJob j = find_job(a);
+    const int wgi = (int)blockIdx.x - j.wg0, wgc = j.wgs;
+    if (j.kind == KIND_F32 || j.kind == KIND_BF16) {
+        const XStage xs = stage_job<false>(j, fl_lds, lgrid);
+        if (j.kind == KIND_F32) job_rows<FK<KIND_F32>>(j, wgi, wgc, xs, lgrid);
+        else job_rows<FK<KIND_BF16>>(j, wgi, wgc, xs, lgrid);
+        return;
+    }
+    const XStage xs = stage_job<true>(j, fl_lds, lgrid);
     switch (j.kind) {
-    case KIND_F32: job_rows<FK<KIND_F32>>(j, wgi, fl_x, lgrid); break;
-    case KIND_BF16: job_rows<FK<KIND_BF16>>(j, wgi, fl_x, lgrid); break;
-    case KIND_Q8_0: job_rows<FK<KIND_Q8_0>>(j, wgi, fl_x, lgrid); break;
-    case KIND_IQ4_NL: job_rows<FK<KIND_IQ4_NL>>(j, wgi, fl_x, lgrid); break;
-    case KIND_IQ4_XS: job_rows<FK<KIND_IQ4_XS>>(j, wgi, fl_x, lgrid); break;
-    case KIND_Q6_K: job_rows<FK<KIND_Q6_K>>(j, wgi, fl_x, lgrid); break;
-    case KIND_IQ3_XXS: job_rows<FK<KIND_IQ3_XXS>>(j, wgi, fl_x, lgrid); break;
+    case KIND_Q8_0: job_rows<FK<KIND_Q8_0>>(j, wgi, wgc, xs, lgrid); break;
+    case KIND_IQ4_NL: job_rows<FK<KIND_IQ4_NL>>(j, wgi, wgc, xs, lgrid); break;
+    case KIND_IQ4_XS: job_rows<FK<KIND_IQ4_XS>>(j, wgi, wgc, xs, lgrid); break;
+    case KIND_Q6_K: job_rows<FK<KIND_Q6_K>>(j, wgi, wgc, xs, lgrid); break;
+    case KIND_IQ3_XXS: job_rows<FK<KIND_IQ3_XXS>>(j, wgi, wgc, xs, lgrid); break;
     default: break;
     }
+}
+
+// The kernel for a job table: the kind's own kernel when every job has that kind.
+using FlKernel = void (*)(JobArgs);
+FlKernel kernel_for(const JobArgs& a) {
+    const int32_t k = a.job[0].kind;
+    for (int i = 1; i < a.count; i++)
+        if (a.job[i].kind != k) return k_flinear;
+    switch (k) {
+    case KIND_F32: return k_flinear_kind<KIND_F32>;
+    case KIND_BF16: return k_flinear_kind<KIND_BF16>;
+    case KIND_Q8_0: return k_flinear_kind<KIND_Q8_0>;
+    case KIND_IQ4_NL: return k_flinear_kind<KIND_IQ4_NL>;
+    case KIND_IQ4_XS: return k_flinear_kind<KIND_IQ4_XS>;
+    case KIND_Q6_K: return k_flinear_kind<KIND_Q6_K>;
+    case KIND_IQ3_XXS: return k_flinear_kind<KIND_IQ3_XXS>;
+    }
+    return k_flinear;
+}
+
+// Workgroups of a linear kernel resident per CU at `lds` dynamic bytes
+// (occupancy query, cached per kernel and size).
+int fl_resident(const void* kern, size_t lds) {
+    struct Entry {
+        const void* k;
+        size_t lds;
+        int n;
+    };
+    static Entry cache[64];
+    static int used = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].k == kern && cache[i].lds == lds) return cache[i].n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, FL_WG, lds) != hipSuccess || n <= 0) n = 1;
+    if (n > 8) n = 8;
+    if (used < 64) cache[used++] = Entry{kern, lds, n};
+    return n;
+}
+
+size_t stage_bytes(uint32_t kind, int n) {
+    return (kind == KIND_F32 || kind == KIND_BF16) ? 4 * (size_t)n : (size_t)NLIMB * n + 4 * (size_t)(n / 32);
 }
 
 int wg_rows(uint32_t kind) {
@@ -604,14 +845,6 @@ FJob make_job(const Weight& w, const float* x, float* y) {
     return j;
 }
 
-// Device job table of the multi form, grown on demand, kept until uq_shutdown.
-struct JobTable {
-    FJob* dev = nullptr;
-    int cap = 0;
-    std::vector<FJob> host;
-};
-JobTable g_jobs;
-
 int check_job_weight(const uq_weight_t w) {
     if (!w) return set_error(ERR_ARG, "linear: null weight");
     if (!linear_kind(w->w.kind))
@@ -622,37 +855,47 @@ int check_job_weight(const uq_weight_t w) {
 
 int enqueue_jobs(const uq_linear_job* jobs, int count, hipStream_t s) {
     if (!jobs || count <= 0) return set_error(ERR_ARG, "linear: empty job table");
-    g_jobs.host.resize((size_t)count);
-    int64_t wg = 0;
-    int max_n = 0;
     for (int i = 0; i < count; i++) {
         if (int rc = check_job_weight(jobs[i].weight)) return rc;
         if (!jobs[i].x || !jobs[i].y) return set_error(ERR_ARG, "linear: null x or y");
         if ((uintptr_t)jobs[i].x & 15) return set_error(ERR_ARG, "linear: x must be 16-byte aligned");
-        const Weight& w = jobs[i].weight->w;
-        FJob j = make_job(w, jobs[i].x, jobs[i].y);
-        j.wg0 = (int32_t)wg;
-        wg += (w.m + wg_rows(w.kind) - 1) / wg_rows(w.kind);
-        max_n = std::max(max_n, (int)w.n);
-        g_jobs.host[(size_t)i] = j;
     }
-    if (wg > 0x7fffffff) return set_error(ERR_SHAPE, "linear: job table too large for one launch");
-    if (count > g_jobs.cap) {
-        if (g_jobs.dev) {
-            UQ_CHECK_HIP(hipStreamSynchronize(s));
-            (void)hipFree(g_jobs.dev);
-            g_jobs.dev = nullptr;
-            g_jobs.cap = 0;
+    for (int c0 = 0; c0 < count; c0 += MAX_JOBS) {
+        JobArgs a{};
+        a.count = std::min(MAX_JOBS, count - c0);
+        size_t lds = 0;
+        for (int i = 0; i < a.count; i++) {
+            const Weight& w = jobs[c0 + i].weight->w;
+            a.job[i] = make_job(w, jobs[c0 + i].x, jobs[c0 + i].y);
+            lds = std::max(lds, stage_bytes(w.kind, (int)w.n));
         }
-        const int cap = std::max(count, 64);
-        UQ_CHECK_HIP(hipMalloc(&g_jobs.dev, sizeof(FJob) * (size_t)cap));
-        g_jobs.cap = cap;
+        // each job gets at most as many workgroups as fit on the chip at once
+        // (every workgroup loops over its row blocks)
+        const FlKernel kern = kernel_for(a);
+        const int64_t cap = (int64_t)cu_count() * fl_resident((const void*)kern, lds);
+        int64_t wg = 0;
+        for (int i = 0; i < a.count; i++) {
+            const Weight& w = jobs[c0 + i].weight->w;
+            const int64_t rblocks = (w.m + wg_rows(w.kind) - 1) / wg_rows(w.kind);
+            a.job[i].wg0 = (int32_t)wg;
+            a.job[i].wgs = (int32_t)std::min<int64_t>(rblocks, cap);
+            wg += a.job[i].wgs;
+        }
+        if (wg > 0x7fffffff) return set_error(ERR_SHAPE, "linear: job table too large for one launch");
+        static bool lds_set = false;
+        if (!lds_set) {
+            const FlKernel all[] = {k_flinear, k_flinear_kind<KIND_F32>, k_flinear_kind<KIND_BF16>,
+                                    k_flinear_kind<KIND_Q8_0>, k_flinear_kind<KIND_IQ4_NL>,
+                                    k_flinear_kind<KIND_IQ4_XS>, k_flinear_kind<KIND_Q6_K>,
+                                    k_flinear_kind<KIND_IQ3_XXS>};
+            for (FlKernel f : all)
+                UQ_CHECK_HIP(hipFuncSetAttribute((const void*)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)stage_bytes(KIND_Q8_0, 16384)));
+            lds_set = true;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)wg), dim3(FL_WG), lds, s, a);
+        UQ_CHECK_HIP(hipGetLastError());
     }
-    // the table is read by the launch that follows on the same stream
-    UQ_CHECK_HIP(hipMemcpyAsync(g_jobs.dev, g_jobs.host.data(), sizeof(FJob) * (size_t)count, hipMemcpyHostToDevice,
-                                s));
-    hipLaunchKernelGGL(k_flinear, dim3((unsigned)wg), dim3(FWG), (size_t)max_n * 4, s, g_jobs.dev, count);
-    UQ_CHECK_HIP(hipGetLastError());
     return OK;
 }
 
@@ -664,12 +907,6 @@ int check_finite(const float* v, int64_t n, const char* what) {
 
 }  // namespace
 
-namespace uq {
-void frontier_release() {
-    if (g_jobs.dev) (void)hipFree(g_jobs.dev);
-    g_jobs = JobTable{};
-}
-}  // namespace uq
 
 extern "C" {
 
@@ -751,6 +988,50 @@ int uq_linear_batch(const uq_linear_job* jobs, int count) {
         yo += m;
     }
     return check_finite(host.data(), ys, "linear_batch: output");
+}
+
+int uq_time_linear(const uq_weight_t* ws, int count, int reps, int warmup, double* total_ms) {
+    if (!uq_stream()) return set_error(ERR_ARG, "uq_init has not been called");
+    if (!ws || count <= 0 || reps <= 0 || warmup < 0 || !total_ms) return set_error(ERR_ARG, "time_linear: bad args");
+    int64_t xs = 0, ys = 0;
+    for (int i = 0; i < count; i++) {
+        if (int rc = check_job_weight(ws[i])) return rc;
+        xs += ws[i]->w.n;
+        ys += ws[i]->w.m;
+    }
+    hipStream_t s = (hipStream_t)uq_stream();
+    float *dx = nullptr, *dy = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&dx, sizeof(float) * (size_t)xs));
+    hipError_t e = hipMalloc(&dy, sizeof(float) * (size_t)ys);
+    if (e == hipSuccess) e = hipMemsetAsync(dx, 0, sizeof(float) * (size_t)xs, s);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    int rc = OK;
+    std::vector<uq_linear_job> jobs((size_t)count);
+    int64_t xo = 0, yo = 0;
+    for (int i = 0; i < count; i++) {
+        jobs[(size_t)i] = uq_linear_job{ws[i], dx + xo, dy + yo};
+        xo += ws[i]->w.n;
+        yo += ws[i]->w.m;
+    }
+    for (int r = 0; r < warmup + reps && e == hipSuccess && rc == OK; r++) {
+        if (r == warmup) e = hipEventRecord(e0, s);
+        for (int i = 0; i < count && rc == OK; i++) rc = enqueue_jobs(&jobs[(size_t)i], 1, s);
+    }
+    if (e == hipSuccess && rc == OK) e = hipEventRecord(e1, s);
+    if (e == hipSuccess && rc == OK) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess && rc == OK) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("time_linear: ") + hipGetErrorString(e));
+    if (rc != OK) return rc;
+    *total_ms = ms;
+    return OK;
 }
 
 int uq_linear(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m) {

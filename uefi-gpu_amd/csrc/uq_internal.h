@@ -77,7 +77,6 @@ void launch_layout_repack(const uint8_t* src, int64_t blocks, const FrontierLayo
                           hipStream_t s);
 void launch_layout_verify(const uint8_t* src, int64_t blocks, const FrontierLayout& L, uint8_t* const planes[3],
                           unsigned* bad, hipStream_t s);
-void frontier_release();
 
 // ---- kernel launchers (uq_matvec.hip) ----
 void launch_quant_act(const float* x, int64_t n, int8_t* xq, float* xs, hipStream_t s);

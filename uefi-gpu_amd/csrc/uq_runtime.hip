@@ -108,7 +108,6 @@ int uq_init(int device) {
 int uq_shutdown(void) {
     if (!g_ctx.ready) return OK;
     hipStreamSynchronize(g_ctx.stream);
-    frontier_release();
     hipFree(g_ctx.dx);
     hipFree(g_ctx.dxq);
     hipFree(g_ctx.dxs);

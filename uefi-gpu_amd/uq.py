@@ -76,6 +76,8 @@ _SIGS = {
     "uq_linear_batch": (ctypes.c_int, [_vp, ctypes.c_int]),
     "uq_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
     "uq_linear_multi_dev": (ctypes.c_int, [_vp, ctypes.c_int, _vp]),
+    "uq_time_linear": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_double)]),
     "uq_dev_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "uq_dev_free": (ctypes.c_int, [_vp]),
     "uq_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
@@ -277,6 +279,14 @@ def linear_batch(pairs):
                                       for (w, _), x, y in zip(pairs, xs, ys)])
     _check(lib().uq_linear_batch(jobs, len(pairs)))
     return ys
+
+
+def time_linear(weights, reps, warmup):
+    """HIP-event time (ms) of `reps` rounds of one fp32-activation linear per weight."""
+    handles = (_vp * len(weights))(*[w.handle for w in weights])
+    ms = ctypes.c_double()
+    _check(lib().uq_time_linear(handles, len(weights), reps, warmup, ctypes.byref(ms)))
+    return ms.value
 
 
 def quant_act(x):

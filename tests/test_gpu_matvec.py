@@ -155,7 +155,7 @@ def test_upload_rejects_bad_shapes(gpu):
         uq.Weight(uq.KIND_Q8_0, 64, 5, raw)
     assert e.value.status == uq.Error.SHAPE
     with pytest.raises(uq.UqError) as e:
-        uq.Weight(14, 256, 1, np.zeros(210, np.uint8))
+        uq.Weight(2, 256, 1, np.zeros(144, np.uint8))      # Q4_0: not a kind of this path
     assert e.value.status == uq.Error.QUANT_TYPE
     with pytest.raises(uq.UqError):
         uq.Weight(uq.KIND_Q8_0, 16416, 1, np.zeros(16416 // 32 * 34, np.uint8))   # n > 16384

@@ -203,6 +203,14 @@ int uq_prompt_tokens(uq_model_t m, const uint32_t* tokens, int count, int pos, u
  * the fp16 KV cache; next = greedy id after the last prompt token. The decode
  * step continues at pos = count. count <= min(max_seq, 1024). */
 int uq_prefill(uq_model_t m, const uint32_t* tokens, int count, uint32_t* next);
+/* generate_one (llm.rs:402-428): prefill of the prompt (count tokens), then
+ * up to max_new greedy steps. Before each step the current id is compared
+ * with the stop ids (the reference's 151645 / 151643); a stop id ends the
+ * run (*ended = 1) and is not emitted. out[0..*generated) are the emitted ids;
+ * count + max_new < max_seq. prefill_ms / decode_ms (optional): host-clock
+ * time of each phase, each ending with its ids on the host. */
+int uq_generate(uq_model_t m, const uint32_t* prompt, int count, int max_new, const uint32_t* stop, int nstop,
+                uint32_t* out, int* generated, int* ended, double* prefill_ms, double* decode_ms);
 /* LOGITS readback of verify_gpu_greedy (gpu_graph.rs:14-23). */
 int uq_model_logits(uq_model_t m, float* out, int64_t n);
 /* fp16 KV cache readback of positions [0, count) of one layer ([count][kv*hd]). */
@@ -278,6 +286,13 @@ int uq_gguf_meta_u64(uq_gguf_t g, const char* key, uint64_t* out);
 int uq_gguf_meta_f32(uq_gguf_t g, const char* key, float* out);
 int uq_gguf_meta_str(uq_gguf_t g, const char* key, const char** out, uint64_t* len);
 int uq_gguf_meta_array(uq_gguf_t g, const char* key, uint32_t* elem_kind, uint64_t* count);
+/* Element `index` of a string-array value (e.g. tokenizer.ggml.tokens):
+ * pointer into the parsed directory and its byte length. */
+int uq_gguf_meta_array_str(uq_gguf_t g, const char* key, uint64_t index, const char** out, uint64_t* len);
+/* Model::text (driver/src/llm.rs:87-99): the bytes of token `id` from the
+ * GPT-2 byte-level string in tokenizer.ggml.tokens. len = bytes needed; the
+ * call fails with UQ_ERR_ARG (len still set) when cap is smaller. */
+int uq_gguf_token_text(uq_gguf_t g, uint32_t id, uint8_t* out, uint64_t cap, uint64_t* len);
 /* Qwen2 shape constants from qwen2.* metadata and token_embd.weight (the
  * constants llm.rs:314-321 hard-codes); max_seq <= 0 takes context_length. */
 int uq_gguf_qwen2_config(uq_gguf_t g, int32_t max_seq, uq_qwen2_config* cfg);

@@ -175,6 +175,9 @@ struct uq_gguf {
     std::vector<TensorInfo> tensors;
     uint64_t data_offset = 0, logical_bytes = 0, split_no = 0, split_count = 1, total_tensors = 0;
     std::string path;  // set when opened from a file
+    // byte offsets of the elements of one string array, built on first use
+    std::string str_index_key;
+    std::vector<uint64_t> str_index;
 };
 
 namespace {
@@ -408,6 +411,75 @@ int uq_gguf_meta_array(uq_gguf_t g, const char* key, uint32_t* elem_kind, uint64
     if (m->kind != 9 || m->data.size() < 12) return fail_gguf(G_TYPE, nullptr, key);
     memcpy(elem_kind, m->data.data(), 4);
     memcpy(count, m->data.data() + 4, 8);
+    return UQ_OK;
+}
+
+int uq_gguf_meta_array_str(uq_gguf_t g, const char* key, uint64_t index, const char** out, uint64_t* len) {
+    if (!g || !key || !out || !len) return uq::set_error(UQ_ERR_ARG, "gguf_meta_array_str: null pointer");
+    const Meta* m = find_meta(g, key);
+    if (!m) return uq::set_error(UQ_ERR_FORMAT, std::string("gguf: missing key ") + key);
+    uint32_t elem = 0;
+    uint64_t count = 0;
+    if (m->kind != 9 || m->data.size() < 12) return fail_gguf(G_TYPE, nullptr, key);
+    memcpy(&elem, m->data.data(), 4);
+    memcpy(&count, m->data.data() + 4, 8);
+    if (elem != 8) return fail_gguf(G_TYPE, nullptr, key);
+    if (index >= count) return uq::set_error(UQ_ERR_ARG, "gguf_meta_array_str: index out of range");
+    if (g->str_index_key != key) {
+        // the parser checked every length against the value's bytes
+        g->str_index.clear();
+        g->str_index.reserve((size_t)count);
+        uint64_t pos = 12;
+        for (uint64_t i = 0; i < count; i++) {
+            uint64_t l;
+            memcpy(&l, m->data.data() + pos, 8);
+            g->str_index.push_back(pos);
+            pos += 8 + l;
+        }
+        g->str_index_key = key;
+    }
+    const uint64_t pos = g->str_index[(size_t)index];
+    memcpy(len, m->data.data() + pos, 8);
+    *out = (const char*)m->data.data() + pos + 8;
+    return UQ_OK;
+}
+
+// Model::text (driver/src/llm.rs:87-99): the GPT-2 byte-level string of token
+// `id` back to bytes. A character below 256 is that byte; character 256 + i
+// is the i-th byte (ascending) outside the printable ranges 33-126, 161-172
+// and 174-255; any other character is its own UTF-8 encoding.
+int uq_gguf_token_text(uq_gguf_t g, uint32_t id, uint8_t* out, uint64_t cap, uint64_t* len) {
+    if (!g || !len || (cap && !out)) return uq::set_error(UQ_ERR_ARG, "gguf_token_text: null pointer");
+    const char* s = nullptr;
+    uint64_t n = 0;
+    if (int rc = uq_gguf_meta_array_str(g, "tokenizer.ggml.tokens", id, &s, &n)) return rc;
+    uint8_t unprintable[68];
+    int nun = 0;
+    for (int b = 0; b < 256; b++)
+        if (!((b >= 33 && b <= 126) || (b >= 161 && b <= 172) || (b >= 174 && b <= 255))) unprintable[nun++] = (uint8_t)b;
+    uint64_t w = 0;
+    auto put = [&](uint8_t b) {
+        if (w < cap) out[w] = b;
+        w++;
+    };
+    const uint8_t* p = (const uint8_t*)s;
+    uint64_t i = 0;
+    while (i < n) {
+        // the parser checked the string is valid UTF-8
+        uint32_t c = p[i], extra = 0;
+        if (c >= 0xF0) { c &= 0x07; extra = 3; }
+        else if (c >= 0xE0) { c &= 0x0F; extra = 2; }
+        else if (c >= 0xC0) { c &= 0x1F; extra = 1; }
+        const uint64_t start = i;
+        i++;
+        for (uint32_t k = 0; k < extra; k++, i++) c = (c << 6) | (p[i] & 0x3F);
+        if (c < 256) put((uint8_t)c);
+        else if (c - 256 < (uint32_t)nun) put(unprintable[c - 256]);
+        else
+            for (uint64_t k = start; k < i; k++) put(p[k]);
+    }
+    *len = w;
+    if (w > cap) return uq::set_error(UQ_ERR_ARG, "gguf_token_text: buffer too small");
     return UQ_OK;
 }
 

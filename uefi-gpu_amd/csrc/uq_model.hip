@@ -14,6 +14,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <chrono>
 #include <cstring>
 #include <map>
 #include <string>
@@ -525,6 +526,48 @@ int uq_prefill(uq_model_t h, const uint32_t* tokens, int count, uint32_t* next) 
     if (!m || !tokens || !next) return set_error(ERR_ARG, "prefill: null pointer");
     if (!m->prepared) return set_error(ERR_ARG, "prefill: model not prepared");
     return m->prefill(tokens, count, next);
+}
+
+// generate_one (driver/src/llm.rs:402-428): the prompt through the prefill,
+// then greedy steps. Before each step the current id is checked against the
+// stop ids (end of generation); otherwise it is appended to the output and fed
+// to the next step at position count + i. Host clock per phase, each phase
+// ending with its result on the host.
+int uq_generate(uq_model_t h, const uint32_t* prompt, int count, int max_new, const uint32_t* stop, int nstop,
+                uint32_t* out, int* generated, int* ended, double* prefill_ms, double* decode_ms) {
+    Model* m = (Model*)h;
+    if (!m || !prompt || !out || !generated || !ended || (nstop > 0 && !stop))
+        return set_error(ERR_ARG, "generate: null pointer");
+    if (!m->prepared) return set_error(ERR_ARG, "generate: model not prepared");
+    if (count <= 0 || max_new < 0 || (int64_t)count + max_new >= m->cfg.max_seq)
+        return set_error(ERR_CONTEXT, "generate: prompt + new tokens must stay below max_seq");
+    auto is_stop = [&](uint32_t t) {
+        for (int k = 0; k < nstop; k++)
+            if (stop[k] == t) return true;
+        return false;
+    };
+    using clk = std::chrono::steady_clock;
+    const auto t0 = clk::now();
+    uint32_t next = 0;
+    if (int rc = m->prefill(prompt, count, &next)) return rc;
+    const auto t1 = clk::now();
+    int n = 0;
+    bool end = false;
+    for (int i = 0; i < max_new; i++) {
+        if (is_stop(next)) {
+            end = true;
+            break;
+        }
+        out[n++] = next;
+        if (int rc = uq_decode_step(h, next, count + i, &next)) return rc;
+    }
+    if (is_stop(next)) end = true;
+    const auto t2 = clk::now();
+    *generated = n;
+    *ended = end ? 1 : 0;
+    if (prefill_ms) *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    if (decode_ms) *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    return OK;
 }
 
 int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t tokens, float* y) {

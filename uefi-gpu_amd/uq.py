@@ -127,6 +127,12 @@ _SIGS = {
     "uq_gguf_meta_array": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
                                           ctypes.POINTER(ctypes.c_uint64)]),
     "uq_gguf_qwen2_config": (ctypes.c_int, [_vp, ctypes.c_int32, _vp]),
+    "uq_gguf_meta_array_str": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_vp),
+                                              ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_token_text": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_generate": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p, ctypes.c_int, _c_u32p,
+                                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                   ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "uq_model_load_gguf": (ctypes.c_int, [_vp, _vp]),
     "uq_synth_quant": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, _i64, _i64, _c_u8p]),
     "uq_synth_normal": (ctypes.c_int, [ctypes.c_uint64, _i64, ctypes.c_float, ctypes.c_float, _c_f32p]),
@@ -474,6 +480,19 @@ class Qwen2Model:
         _check(lib().uq_prefill(self.handle, _p(t, _c_u32p), t.size, ctypes.byref(nxt)))
         return nxt.value
 
+    def generate(self, prompt, max_new, stop=(151645, 151643)):
+        """generate_one (llm.rs:402-428): prefill, then greedy steps until a stop
+        id or max_new tokens. Returns (ids, ended, prefill_ms, decode_ms)."""
+        t = np.ascontiguousarray(prompt, np.uint32)
+        st = np.ascontiguousarray(stop, np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n, ended = ctypes.c_int(), ctypes.c_int()
+        pms, dms = ctypes.c_double(), ctypes.c_double()
+        _check(lib().uq_generate(self.handle, _p(t, _c_u32p), t.size, max_new, _p(st, _c_u32p), st.size,
+                                 _p(out, _c_u32p), ctypes.byref(n), ctypes.byref(ended), ctypes.byref(pms),
+                                 ctypes.byref(dms)))
+        return out[:n.value].copy(), bool(ended.value), pms.value, dms.value
+
     def prompt(self, tokens, pos=0):
         t = np.ascontiguousarray(tokens, np.uint32)
         nxt = ctypes.c_uint32()
@@ -679,6 +698,27 @@ class Gguf:
         k, n = ctypes.c_uint32(), ctypes.c_uint64()
         _check(lib().uq_gguf_meta_array(self.handle, key.encode(), ctypes.byref(k), ctypes.byref(n)))
         return k.value, n.value
+
+    def array_string(self, key, index):
+        """Element `index` of a string-array value, as bytes."""
+        p, n = _vp(), ctypes.c_uint64()
+        _check(lib().uq_gguf_meta_array_str(self.handle, key.encode(), index, ctypes.byref(p), ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value)
+
+    def token_bytes(self, token_id):
+        """Model::text (llm.rs:87-99) before the UTF-8 step: the token's bytes."""
+        n = ctypes.c_uint64()
+        buf = ctypes.create_string_buffer(256)
+        rc = lib().uq_gguf_token_text(self.handle, token_id, buf, 256, ctypes.byref(n))
+        if rc != 0 and n.value > 256:
+            buf = ctypes.create_string_buffer(n.value)
+            rc = lib().uq_gguf_token_text(self.handle, token_id, buf, n.value, ctypes.byref(n))
+        _check(rc)
+        return buf.raw[:n.value]
+
+    def text(self, token_id):
+        """Model::text: the token's bytes as text, invalid UTF-8 replaced (from_utf8_lossy)."""
+        return self.token_bytes(token_id).decode("utf-8", errors="replace")
 
     def qwen2_config(self, max_seq=0):
         c = Qwen2Config()

@@ -211,6 +211,64 @@ def linear_sweep(n=2560, copies=3, reps=20):
     return out
 
 
+def frontier_moe_bench(tokens=32, reps=3, experts=256, top_k=10, dim=2560, ff=640):
+    """Device work of the frontier MoE block (Forward::ffn) per token: the F32
+    router linear, then the 23-job table (10 routed experts' IQ3_XXS gate and
+    up, the shared Q8_0 gate and up, the F32 shared scale) and the 11-job
+    table (IQ4_NL routed down, Q8_0 shared down), one launch each. Experts are
+    drawn per token (seeded) from a bank of `experts` (about 557 MB for 256,
+    more than the MALL). The host arithmetic between the tables is not timed."""
+    import ctypes
+    rng = np.random.default_rng(0x5EED0005)
+    mk = lambda kind, n, m, seed: uq.Weight(kind, n, m, uq.synth_quant(kind, seed, m, n))
+    router = mk(uq.KIND_F32, dim, experts, 1)
+    sscale = mk(uq.KIND_F32, dim, 1, 2)
+    sgate, sup = mk(uq.KIND_Q8_0, dim, ff, 3), mk(uq.KIND_Q8_0, dim, ff, 4)
+    sdown = mk(uq.KIND_Q8_0, ff, dim, 5)
+    gate = [mk(uq.KIND_IQ3_XXS, dim, ff, 100 + e) for e in range(experts)]
+    up = [mk(uq.KIND_IQ3_XXS, dim, ff, 10000 + e) for e in range(experts)]
+    down = [mk(uq.KIND_IQ4_NL, ff, dim, 20000 + e) for e in range(experts)]
+    L = uq.lib()
+    nbuf = dim + experts + 23 * ff + 11 * ff + 11 * dim
+    buf = ctypes.c_void_p()
+    uq._check(L.uq_dev_alloc(4 * nbuf, ctypes.byref(buf)))
+    uq._check(L.uq_memcpy_h2d(buf, np.ascontiguousarray(rng.normal(0, 1, nbuf).astype(np.float32)).ctypes.data,
+                              4 * nbuf))
+    at = lambda off: buf.value + 4 * off
+    x, sc = at(0), at(dim)
+    proj = [at(dim + experts + i * ff) for i in range(23)]
+    mid = [at(dim + experts + (23 + i) * ff) for i in range(11)]
+    outs = [at(dim + experts + 34 * ff + i * dim) for i in range(11)]
+    jobs, sizes = [], []
+    for t in range(tokens):
+        ids = rng.choice(experts, top_k, replace=False)
+        jobs.append(uq.LinearJob(router.handle, x, sc))
+        sizes.append(1)
+        a = []
+        for e in ids:
+            a += [uq.LinearJob(gate[e].handle, x, proj[len(a)]), uq.LinearJob(up[e].handle, x, proj[len(a) + 1])]
+        a += [uq.LinearJob(sgate.handle, x, proj[20]), uq.LinearJob(sup.handle, x, proj[21]),
+              uq.LinearJob(sscale.handle, x, proj[22])]
+        jobs += a
+        sizes.append(len(a))
+        b = [uq.LinearJob(down[e].handle, mid[i], outs[i]) for i, e in enumerate(ids)]
+        b.append(uq.LinearJob(sdown.handle, mid[10], outs[10]))
+        jobs += b
+        sizes.append(len(b))
+    jt = (uq.LinearJob * len(jobs))(*jobs)
+    st = (ctypes.c_int * len(sizes))(*sizes)
+    ms = ctypes.c_double()
+    uq._check(L.uq_time_linear_tables(jt, st, len(sizes), reps, ctypes.byref(ms)))
+    L.uq_dev_free(buf)
+    for w in [router, sscale, sgate, sup, sdown] + gate + up + down:
+        w.free()
+    us = ms.value * 1e3 / (reps * tokens)
+    step_bytes = (experts * dim * 4 + top_k * (2 * ff * 980 + dim * (ff // 32) * 18) + 3 * ff * (dim // 32) * 34
+                  + dim * 4)
+    return {"us_per_token_layer": round(us, 2), "GBs": round(step_bytes / (us * 1e-6) / 1e9, 1),
+            "bytes_per_token_layer": step_bytes, "launches_per_token_layer": 3, "tokens": tokens, "experts": experts}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,7 +277,7 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
-    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe", "linear"],
+    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe", "linear", "frontier_moe"],
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -230,7 +288,7 @@ def main():
     uq.init(0)
     if args.leg:
         leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "q4k": q4k_sweep, "q3k": q3k_sweep,
-               "moe": moe_bench, "linear": linear_sweep}[args.leg]
+               "moe": moe_bench, "linear": linear_sweep, "frontier_moe": frontier_moe_bench}[args.leg]
         print(json.dumps({args.leg: leg()}), flush=True)
         return
     weights, pairs, shape_of = [], [], []

@@ -144,6 +144,11 @@ int uq_linear_multi_dev(const uq_linear_job* jobs, int count, void* stream);
  * untimed ones, of one uq_linear_dev launch per weight in turn (zero x, each
  * weight its own output); total_ms = HIP-event time of the timed rounds. */
 int uq_time_linear(const uq_weight_t* ws, int count, int reps, int warmup, double* total_ms);
+/* Measurement aid (no reference counterpart): the job tables jobs[0..sizes[0]),
+ * then the next sizes[1] jobs, ..., each one uq_linear_multi_dev launch
+ * (device x/y), repeated reps times after one untimed round; total_ms =
+ * HIP-event time of the timed rounds. */
+int uq_time_linear_tables(const uq_linear_job* jobs, const int* sizes, int ntables, int reps, double* total_ms);
 
 /* ---------------------------------------------------------------- memory + timing
  * Small helpers so harnesses need no other GPU runtime binding. */

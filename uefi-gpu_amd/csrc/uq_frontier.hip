@@ -481,7 +481,7 @@ struct FK<KIND_Q6_K> {
 // bytes) then their 4 sign/scale words (16 bytes).
 template <>
 struct FK<KIND_IQ3_XXS> {
-    static constexpr int WPU = 128, LPR = 4, CH = 2;
+    static constexpr int WPU = 128, LPR = 8, CH = 2;
     struct U {
         uint4 q0, q1, a;
         uint32_t d;
@@ -1029,6 +1029,34 @@ int uq_time_linear(const uq_weight_t* ws, int count, int reps, int warmup, doubl
     (void)hipFree(dx);
     if (dy) (void)hipFree(dy);
     if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("time_linear: ") + hipGetErrorString(e));
+    if (rc != OK) return rc;
+    *total_ms = ms;
+    return OK;
+}
+
+int uq_time_linear_tables(const uq_linear_job* jobs, const int* sizes, int ntables, int reps, double* total_ms) {
+    if (!uq_stream()) return set_error(ERR_ARG, "uq_init has not been called");
+    if (!jobs || !sizes || ntables <= 0 || reps <= 0 || !total_ms) return set_error(ERR_ARG, "time_linear_tables: bad args");
+    hipStream_t s = (hipStream_t)uq_stream();
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    UQ_CHECK_HIP(hipEventCreate(&e0));
+    hipError_t e = hipEventCreate(&e1);
+    int rc = OK;
+    for (int r = 0; r <= reps && e == hipSuccess && rc == OK; r++) {  // round 0 untimed
+        if (r == 1) e = hipEventRecord(e0, s);
+        int off = 0;
+        for (int t = 0; t < ntables && rc == OK; t++) {
+            rc = enqueue_jobs(jobs + off, sizes[t], s);
+            off += sizes[t];
+        }
+    }
+    if (e == hipSuccess && rc == OK) e = hipEventRecord(e1, s);
+    if (e == hipSuccess && rc == OK) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess && rc == OK) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("time_linear_tables: ") + hipGetErrorString(e));
     if (rc != OK) return rc;
     *total_ms = ms;
     return OK;

@@ -76,6 +76,8 @@ _SIGS = {
     "uq_linear_batch": (ctypes.c_int, [_vp, ctypes.c_int]),
     "uq_linear_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
     "uq_linear_multi_dev": (ctypes.c_int, [_vp, ctypes.c_int, _vp]),
+    "uq_time_linear_tables": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(ctypes.c_double)]),
     "uq_time_linear": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       ctypes.POINTER(ctypes.c_double)]),
     "uq_dev_alloc": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),

@@ -253,7 +253,7 @@ __device__ __forceinline__ double seg_dot(const uint32_t (&c)[4 * NC], const XSt
 // every digit position, minus 0x80: balanced digits in [-128, 127]).
 __device__ void stage_x(const float* __restrict__ x, int n, uint32_t kind, uint32_t* limb, int* bexp) {
     const int n4 = n / 4;
-    for (int q = threadIdx.x; q < ((n4 + 7) & ~7); q += FL_WG) {
+    for (int q = threadIdx.x; q < ((n4 + 7) & ~7); q += (int)blockDim.x) {
         // q < n4 for the whole 8-lane group or for none of it (n % 32 == 0)
         if (q < n4) {
             const float4 v4 = ((const float4*)x)[q];
@@ -344,7 +344,7 @@ struct FK;
 // F32 / BF16 weights are not small-integer codes: products in double from x.
 template <>
 struct FK<KIND_F32> {
-    static constexpr int WPU = 8, LPR = 16, CH = 4;
+    static constexpr int WPU = 8, LPR = 64, CH = 4;
     struct U {
         uint4 a, b;
     };
@@ -366,7 +366,7 @@ struct FK<KIND_F32> {
 
 template <>
 struct FK<KIND_BF16> {
-    static constexpr int WPU = 8, LPR = 16, CH = 4;
+    static constexpr int WPU = 8, LPR = 64, CH = 4;
     struct U {
         uint4 a;
     };
@@ -529,7 +529,8 @@ struct FK<KIND_IQ3_XXS> {
 // group sums in double and rounds once.
 template <class T>
 __device__ void job_rows(const FJob& j, int wgi, int wgc, const XStage& xs, const uint32_t* grid) {
-    constexpr int LPR = T::LPR, CH = T::CH, RPW = 64 / LPR, RPB = RPW * (FL_WG / 64);
+    constexpr int LPR = T::LPR, CH = T::CH, RPW = 64 / LPR;
+    const int RPB = RPW * (int)(blockDim.x / 64);  // rows per row block: the launch picks 256 or 512 threads
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane % LPR, grp = lane / LPR;
     const int nu = j.n / T::WPU;
     const int nb = (nu + LPR - 1) / LPR;    // unit slots per lane and row
@@ -586,8 +587,8 @@ __device__ void job_rows(const FJob& j, int wgi, int wgc, const XStage& xs, cons
 }
 
 template <class T>
-constexpr int rows_per_wg() {
-    return (64 / T::LPR) * (FL_WG / 64);
+constexpr int rows_per_wave() {
+    return 64 / T::LPR;
 }
 
 // Up to MAX_JOBS jobs per launch, passed by value in the kernel arguments
@@ -620,8 +621,8 @@ __device__ __forceinline__ XStage stage_job(const FJob& j, uint32_t* fl_lds, uin
     xs.n4 = j.n / 4;
     if (INTS) stage_x(j.x, j.n, (uint32_t)j.kind, fl_lds, (int*)(fl_lds + NLIMB * (j.n / 4)));
     else
-        for (int i = threadIdx.x; i < j.n / 4; i += FL_WG) ((float4*)fl_lds)[i] = ((const float4*)j.x)[i];
-    if (threadIdx.x < 256) lgrid[threadIdx.x] = c_iq3_grid[threadIdx.x];
+        for (int i = threadIdx.x; i < j.n / 4; i += (int)blockDim.x) ((float4*)fl_lds)[i] = ((const float4*)j.x)[i];
+    for (int i = threadIdx.x; i < 256; i += (int)blockDim.x) lgrid[i] = c_iq3_grid[i];
     __syncthreads();
     return xs;
 }
@@ -703,20 +704,20 @@ size_t stage_bytes(uint32_t kind, int n) {
     return (kind == KIND_F32 || kind == KIND_BF16) ? 4 * (size_t)n : (size_t)NLIMB * n + 4 * (size_t)(n / 32);
 }
 
-int wg_rows(uint32_t kind) {
+int wave_rows(uint32_t kind) {
     switch (kind) {
-    case KIND_F32: return rows_per_wg<FK<KIND_F32>>();
-    case KIND_BF16: return rows_per_wg<FK<KIND_BF16>>();
-    case KIND_Q8_0: return rows_per_wg<FK<KIND_Q8_0>>();
-    case KIND_IQ4_NL: return rows_per_wg<FK<KIND_IQ4_NL>>();
-    case KIND_IQ4_XS: return rows_per_wg<FK<KIND_IQ4_XS>>();
-    case KIND_Q6_K: return rows_per_wg<FK<KIND_Q6_K>>();
-    case KIND_IQ3_XXS: return rows_per_wg<FK<KIND_IQ3_XXS>>();
+    case KIND_F32: return rows_per_wave<FK<KIND_F32>>();
+    case KIND_BF16: return rows_per_wave<FK<KIND_BF16>>();
+    case KIND_Q8_0: return rows_per_wave<FK<KIND_Q8_0>>();
+    case KIND_IQ4_NL: return rows_per_wave<FK<KIND_IQ4_NL>>();
+    case KIND_IQ4_XS: return rows_per_wave<FK<KIND_IQ4_XS>>();
+    case KIND_Q6_K: return rows_per_wave<FK<KIND_Q6_K>>();
+    case KIND_IQ3_XXS: return rows_per_wave<FK<KIND_IQ3_XXS>>();
     }
     return 0;
 }
 
-bool linear_kind(uint32_t kind) { return wg_rows(kind) > 0; }
+bool linear_kind(uint32_t kind) { return wave_rows(kind) > 0; }
 
 }  // namespace
 
@@ -870,16 +871,25 @@ int enqueue_jobs(const uq_linear_job* jobs, int count, hipStream_t s) {
             lds = std::max(lds, stage_bytes(w.kind, (int)w.n));
         }
         // each job gets at most as many workgroups as fit on the chip at once
-        // (every workgroup loops over its row blocks)
+        // (every workgroup loops over its row blocks); a table that cannot fill
+        // the chip with 512-thread workgroups runs 256-thread ones, twice as many
         const FlKernel kern = kernel_for(a);
-        const int64_t cap = (int64_t)cu_count() * fl_resident((const void*)kern, lds);
+        const int64_t cu = cu_count();
+        int threads = FL_WG;
         int64_t wg = 0;
-        for (int i = 0; i < a.count; i++) {
-            const Weight& w = jobs[c0 + i].weight->w;
-            const int64_t rblocks = (w.m + wg_rows(w.kind) - 1) / wg_rows(w.kind);
-            a.job[i].wg0 = (int32_t)wg;
-            a.job[i].wgs = (int32_t)std::min<int64_t>(rblocks, cap);
-            wg += a.job[i].wgs;
+        for (int pass = 0; pass < 2; pass++) {
+            const int64_t cap = cu * fl_resident((const void*)kern, lds) * (FL_WG / threads);
+            wg = 0;
+            for (int i = 0; i < a.count; i++) {
+                const Weight& w = jobs[c0 + i].weight->w;
+                const int64_t rpb = (int64_t)wave_rows(w.kind) * (threads / 64);
+                const int64_t rblocks = (w.m + rpb - 1) / rpb;
+                a.job[i].wg0 = (int32_t)wg;
+                a.job[i].wgs = (int32_t)std::min<int64_t>(rblocks, cap);
+                wg += a.job[i].wgs;
+            }
+            if (pass == 0 && wg < 2 * cu) threads = FL_WG / 2;
+            else break;
         }
         if (wg > 0x7fffffff) return set_error(ERR_SHAPE, "linear: job table too large for one launch");
         static bool lds_set = false;
@@ -893,7 +903,7 @@ int enqueue_jobs(const uq_linear_job* jobs, int count, hipStream_t s) {
                                                  (int)stage_bytes(KIND_Q8_0, 16384)));
             lds_set = true;
         }
-        hipLaunchKernelGGL(kern, dim3((unsigned)wg), dim3(FL_WG), lds, s, a);
+        hipLaunchKernelGGL(kern, dim3((unsigned)wg), dim3(threads), lds, s, a);
         UQ_CHECK_HIP(hipGetLastError());
     }
     return OK;

@@ -490,13 +490,8 @@ struct FK<KIND_IQ3_XXS> {
         const uint4* p = (const uint4*)(j.body + row * j.pitch) + 3 * u;
         return {p[0], p[1], p[2], j.d[row * (j.n / 256) + u / 2]};
     }
-    // the 4 signs of `bits` (bit k -> byte k) applied to 4 unsigned bytes
-    static __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t bits) {
-        // bit k -> bit 8k (bits < 16, a 24-bit multiply; the shifted copies never overlap)
-        const uint32_t b = (uint32_t)__mul24((int)bits, 0x00204081) & 0x01010101u;
-        const uint32_t m = (b << 8) - b;  // 0xFF in each byte whose sign bit is set
-        return (g ^ m) + b;               // bytes of g are <= 62: no carry between bytes
-    }
+    // grid bytes (<= 62) negated where the sign mask byte is 0xFF: (g ^ m) + (m & 1),
+    // with no carry between bytes
     static __device__ double dot(const U& v, const XStage& xs, int u, const uint32_t* grid, const Iq4Book&) {
         const float d = uq_half((uint16_t)v.d);
         const uint32_t qs[8] = {v.q0.x, v.q0.y, v.q0.z, v.q0.w, v.q1.x, v.q1.y, v.q1.z, v.q1.w};
@@ -507,12 +502,11 @@ struct FK<KIND_IQ3_XXS> {
             uint32_t c[8];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const uint32_t s7 = (aux[l] >> (7 * g)) & 127u;
-                const uint32_t sg = s7 | ((uint32_t)(__popc(s7) & 1) << 7);
+                const uint4 sm = ((const uint4*)(grid + 256))[(aux[l] >> (7 * g)) & 127u];
                 const uint32_t word = qs[2 * l + (g >> 1)];
                 const uint32_t g0 = grid[(word >> (16 * (g & 1))) & 255], g1 = grid[(word >> (16 * (g & 1) + 8)) & 255];
-                c[2 * g] = apply_signs(g0, sg & 15u);
-                c[2 * g + 1] = apply_signs(g1, sg >> 4);
+                c[2 * g] = (g0 ^ sm.x) + sm.z;
+                c[2 * g + 1] = (g1 ^ sm.y) + sm.w;
             }
             const float scale = d * (0.5f + (float)(aux[l] >> 28)) * 0.5f;
             r = __builtin_fma((double)scale, seg_dot<2>(c, xs, 128 * u + 32 * l, 2 * l * (xs.n4 / 32) + u, xs.n4 / 32), r);
@@ -623,6 +617,20 @@ __device__ __forceinline__ XStage stage_job(const FJob& j, uint32_t* fl_lds, uin
     else
         for (int i = threadIdx.x; i < j.n / 4; i += (int)blockDim.x) ((float4*)fl_lds)[i] = ((const float4*)j.x)[i];
     for (int i = threadIdx.x; i < 256; i += (int)blockDim.x) lgrid[i] = c_iq3_grid[i];
+    // IQ3_XXS signs after the grid: entry s7 (7 stored sign bits, the 8th their
+    // parity) = byte masks of values 0-3 and 4-7 (0xFF = negative) and the
+    // masks' low bits
+    for (int i = threadIdx.x; i < 128; i += (int)blockDim.x) {
+        const uint32_t sg = (uint32_t)i | ((uint32_t)(__popc(i) & 1) << 7);
+        uint32_t m[2];
+        for (int h = 0; h < 2; h++) {
+            uint32_t v = 0;
+            for (int k = 0; k < 4; k++)
+                if ((sg >> (4 * h + k)) & 1) v |= 0xFFu << (8 * k);
+            m[h] = v;
+        }
+        ((uint4*)(lgrid + 256))[i] = make_uint4(m[0], m[1], m[0] & 0x01010101u, m[1] & 0x01010101u);
+    }
     __syncthreads();
     return xs;
 }
@@ -631,7 +639,7 @@ __device__ __forceinline__ XStage stage_job(const FJob& j, uint32_t* fl_lds, uin
 template <uint32_t K>
 __global__ __launch_bounds__(FL_WG) void k_flinear_kind(JobArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint32_t fl_lds[];
-    __shared__ uint32_t lgrid[256];
+    __shared__ __attribute__((aligned(16))) uint32_t lgrid[256 + 4 * 128];  // IQ3 grid, then the sign table
     const FJob j = find_job(a);
     const XStage xs = stage_job<K != KIND_F32 && K != KIND_BF16>(j, fl_lds, lgrid);
     job_rows<FK<K>>(j, (int)blockIdx.x - j.wg0, j.wgs, xs, lgrid);
@@ -643,7 +651,7 @@ __global__ __launch_bounds__(FL_WG) void k_flinear_kind(JobArgs a) {
 // (F32 / BF16 weights: x as 4 * n bytes of f32).
 __global__ __launch_bounds__(FL_WG) void k_flinear(JobArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint32_t fl_lds[];
-    __shared__ uint32_t lgrid[256];
+    __shared__ __attribute__((aligned(16))) uint32_t lgrid[256 + 4 * 128];  // IQ3 grid, then the sign table
     const FJob j = find_job(a);
     const int wgi = (int)blockIdx.x - j.wg0, wgc = j.wgs;
     if (j.kind == KIND_F32 || j.kind == KIND_BF16) {

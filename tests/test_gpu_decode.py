@@ -32,7 +32,8 @@ def build(cfg, seed):
 
 
 @pytest.mark.parametrize("cfg,steps", [(SMALL, 24), (dict(SMALL, layers=3, dim=512, hidden=1024, heads=8,
-                                                          kv_heads=2, head_dim=64, vocab=3000), 12)])
+                                                          kv_heads=2, head_dim=64, vocab=3000), 12),
+                                       (dict(SMALL, max_seq=4096), 24)])   # a long cache: attention LDS sized to max_seq
 def test_decode_steps_teacher_forced(gpu, cfg, steps):
     g, o = build(cfg, 0x5EED0002)
     toks = uq.synth_tokens(0x5EED0002, steps, cfg["vocab"])

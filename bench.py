@@ -309,6 +309,19 @@ def main():
     warm_rounds = max(1, args.warmup // args.copies)
     total_ms, _ = uq.time_matvecs(weights, pairs, 8960, rounds, warm_rounds, -1)
     value = step_bytes * steps / (total_ms / 1e3) / 1e9
+    # the same matvecs with each copy's weights of one input length in one
+    # job-table launch (q/o, k/v, gate+up pair, lm_head at K=1536; down at
+    # K=8960): the batch form of Gpu::batch, reported beside `value`
+    tw, tp = [], []
+    for c in range(args.copies):
+        chunk = list(range(c * per_copy, (c + 1) * per_copy))
+        for k in (1536, 8960):
+            for i in chunk:
+                if shape_of[i][2] == k:
+                    tw.append(weights[i])
+                    tp.append(pairs[i])
+    tables_ms = uq.time_matvec_tables(tw, tp, 8960, rounds, warm_rounds)
+    tables_gbs = step_bytes * steps / (tables_ms / 1e3) / 1e9
     # dominant kernel alone: lm_head launches back to back over the copies,
     # one event pair around all of them -> mean launch duration
     lm_ws = [w for w, sh in zip(weights, shape_of) if sh[0] == "lm_head"]
@@ -332,6 +345,11 @@ def main():
                      "kernel": "Q8_0 matvec, lm_head 151936x1536 (%d B per launch), mean of %d back-to-back "
                                "launches %.4f ms" % (lm_bytes, rounds * len(lm_ws), lm_ms)},
     }
+    result["sweep_job_tables"] = {
+        "GBs": round(tables_gbs, 2), "frac": round(tables_gbs / HBM_PEAK_GBS, 4),
+        "ms_per_step": round(tables_ms / steps, 5),
+        "note": "same weights and bytes; per step two launches (the four K=1536 matvecs as one job table, "
+                "down alone) instead of five"}
     read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
     result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
                            "note": "plain int4 streaming read / copy of 1 GiB, same box"}

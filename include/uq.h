@@ -90,6 +90,14 @@ int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, 
 /* gateup_dp4a (gpu_dp4a.cu:60-64): out[r] = silu(gate_r . x) * (up_r . x). */
 int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream);
 
+/* Gpu::batch as one launch (llm.rs:226-245; frontier_multi_matvec's job table,
+ * kernels/frontier_quant.cu:79-93): up to 8 Q8_0 weights of one input length
+ * over one quantized x; w2s (may be NULL, entries may be NULL) pairs weight i
+ * with an up matrix, ys[i] = silu(gate x) * (up x). Each output equals the
+ * single-weight launch's bit for bit. */
+int uq_matvec_table_dev(const uq_weight_t* ws, const uq_weight_t* w2s, int count, const int8_t* xq, const float* xs,
+                        float* const* ys, void* stream);
+
 /* Integer surfaces, host memory, synchronous. uq_quant_act: x (n floats) ->
  * q (n int8) + scale (n/32 floats) on the GPU (quant_act). uq_block_dots:
  * int32 per-block dots of W with the quantized x (Q8_0: m*(n/32) per 32-block,
@@ -164,6 +172,12 @@ int uq_memcpy_d2h(void* dst, const void* src, size_t bytes);
  * gate/up pair with weight i+1 (one fused launch). */
 int uq_time_matvecs(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
                     int probe, double* total_ms, double* probe_ms);
+
+/* The same measurement with consecutive Q8_0 weights of one input length (up
+ * to 8) launched as one job table (the batch of llm.rs:226-245); each output as
+ * uq_matvec_q_dev gives it. */
+int uq_time_matvec_tables(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
+                          double* total_ms);
 
 /* Achievable-bandwidth probe (no reference counterpart; measurement aid): a
  * streaming read of `bytes` and a copy of `bytes` (read + write counted),

@@ -159,3 +159,51 @@ def test_upload_rejects_bad_shapes(gpu):
     assert e.value.status == uq.Error.QUANT_TYPE
     with pytest.raises(uq.UqError):
         uq.Weight(uq.KIND_Q8_0, 16416, 1, np.zeros(16416 // 32 * 34, np.uint8))   # n > 16384
+
+
+def test_job_table_equals_single_launches(gpu):
+    """uq_matvec_table_dev (one launch over several weights sharing x) gives each
+    output bit for bit as uq_matvec_q_dev / uq_gateup_q_dev do; uq_batch uses it."""
+    import ctypes
+    L = uq.lib()
+    K = 1536
+    shapes = [(1536, None), (256, None), (8960, "pair"), (151936, None), (7, None)]
+    ws, w2s = [], []
+    for i, (N, pair) in enumerate(shapes):
+        ws.append(uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0x7AB0 + i, N, K)))
+        w2s.append(uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0x7AC0 + i, N, K)) if pair else None)
+    x = uq.synth_normal(0x7AD0, K)
+    q, s = uq.quant_act(x)
+    total = sum(N for N, _ in shapes)
+    bufs = [ctypes.c_void_p() for _ in range(5)]
+    sizes = [K, 4 * (K // 32), 4 * total, 4 * total, 0]
+    for b, n in zip(bufs, sizes[:4]):
+        assert L.uq_dev_alloc(n, ctypes.byref(b)) == 0
+    dq, ds, dy, dy1 = bufs[:4]
+    try:
+        assert L.uq_memcpy_h2d(dq, q.ctypes.data, K) == 0
+        assert L.uq_memcpy_h2d(ds, s.ctypes.data, 4 * (K // 32)) == 0
+        offs = np.cumsum([0] + [N for N, _ in shapes])
+        ys = (ctypes.c_void_p * 5)(*[dy.value + 4 * int(o) for o in offs[:5]])
+        hw = (ctypes.c_void_p * 5)(*[w.handle for w in ws])
+        h2 = (ctypes.c_void_p * 5)(*[(w.handle if w else None) for w in w2s])
+        assert L.uq_matvec_table_dev(hw, h2, 5, dq, ds, ys, None) == 0
+        for i, (w, w2) in enumerate(zip(ws, w2s)):
+            yi = ctypes.c_void_p(dy1.value + 4 * int(offs[i]))
+            if w2 is None:
+                assert L.uq_matvec_q_dev(w.handle, dq, ds, yi, None) == 0
+            else:
+                assert L.uq_gateup_q_dev(w.handle, w2.handle, dq, ds, yi, None) == 0
+        assert L.uq_sync() == 0
+        a = np.empty(total, np.float32)
+        b = np.empty(total, np.float32)
+        assert L.uq_memcpy_d2h(a.ctypes.data, dy, 4 * total) == 0
+        assert L.uq_memcpy_d2h(b.ctypes.data, dy1, 4 * total) == 0
+    finally:
+        for p in bufs[:4]:
+            L.uq_dev_free(p)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # uq_batch (q, k, v sharing x) equals three matvecs
+    ys = uq.batch(ws[:2] + [ws[4]], x)
+    for w, y in zip(ws[:2] + [ws[4]], ys):
+        assert np.array_equal(y.view(np.uint32), uq.matvec(w, x).view(np.uint32))

@@ -93,6 +93,10 @@ void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, con
 // y[m] = W x for any kind; gate/up fusion writes silu(gate)*up when w2 != null.
 int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s);
 int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s);
+// Up to 8 Q8_0 weights of one input length (w2s[i] non-null: gate/up pair) in
+// one launch over a shared quantized x; each output as launch_matvec gives it.
+int launch_matvec_multi(const Weight* const* ws, const Weight* const* w2s, float* const* ys, int count,
+                        const int8_t* xq, const float* xs, hipStream_t s);
 
 }  // namespace uq
 

@@ -216,6 +216,56 @@ __global__ __launch_bounds__(WG) void k_matvec(WArgs w, WArgs w2, const int8_t* 
     }
 }
 
+// Several weights with the same K and one shared x in one launch (the batch of
+// llm.rs:226-245 and frontier_multi_matvec's job table): workgroup -> job by
+// the ascending first-workgroup table, x loaded into registers once, then the
+// job's rows exactly as k_matvec computes them (identical results).
+constexpr int MV_MAX_JOBS = 8;
+struct MvJob {
+    WArgs w, w2;      // w2.qs != null: a gate/up pair writing silu(gate)*up
+    float* y;
+    int64_t rows, share;
+    int32_t wg0, wgs;
+};
+struct MvJobs {
+    MvJob job[MV_MAX_JOBS];
+    int count;
+};
+template <class KQ, int LPR, int NBL>
+__global__ __launch_bounds__(WG) void k_matvec_multi(MvJobs a, const int8_t* __restrict__ xq,
+                                                     const float* __restrict__ xs, int64_t K) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int RPB = RPW * (WG / 64);
+    int lo = 0, hi = a.count;
+    while (lo + 1 < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (a.job[mid].wg0 <= (int)blockIdx.x) lo = mid;
+        else hi = mid;
+    }
+    const MvJob& j = a.job[lo];
+    const int wgi = (int)blockIdx.x - j.wg0;
+    const int64_t nu = K / KQ::UNIT;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, grp = lane / LPR;
+    typename KQ::X xr[NBL];
+    load_xr<KQ, LPR, NBL>(xr, xq, xs, nu, sub);
+    const bool pair = j.w2.qs != nullptr;
+    if (j.rows <= (int64_t)j.wgs * RPB) {
+        // one pass: this workgroup's even share of the job's rows
+        const RowSpan sp = even_span_of(j.rows, j.share, wgi, j.wgs);
+        const int64_t row = sp.begin + wave * RPW + grp;
+        if (sp.begin + wave * RPW < sp.end) {
+            if (pair) matvec_row<KQ, LPR, NBL, true>(j.w, j.w2, xr, j.y, row, sp.end, nu, sub);
+            else matvec_row<KQ, LPR, NBL, false>(j.w, j.w2, xr, j.y, row, sp.end, nu, sub);
+        }
+    } else {
+        for (int64_t row0 = (int64_t)wgi * RPB; row0 < j.rows; row0 += (int64_t)j.wgs * RPB) {
+            if (pair) matvec_row<KQ, LPR, NBL, true>(j.w, j.w2, xr, j.y, row0 + wave * RPW + grp, j.rows, nu, sub);
+            else matvec_row<KQ, LPR, NBL, false>(j.w, j.w2, xr, j.y, row0 + wave * RPW + grp, j.rows, nu, sub);
+        }
+    }
+}
+
 // One row with the activation read from LDS (K-quant units), same order of
 // work as matvec_row.
 template <class KQ, int LPR, int NBL, bool GATEUP>
@@ -446,6 +496,64 @@ void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, int8_t* s
 void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
                        unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, sc, d, gguf, blocks, bad);
+}
+
+namespace {
+// The job table of weights sharing K: the resident workgroups of the chip are
+// split over the jobs in proportion to their rows (at least one each, at most
+// one row block per workgroup when the rows allow).
+template <class KQ, int LPR, int NBL>
+void launch_multi_t(const Weight* const* ws, const Weight* const* w2s, float* const* ys, int count,
+                    const int8_t* xq, const float* xs, hipStream_t s) {
+    constexpr int RPB = (64 / LPR) * (WG / 64);
+    const void* kern = (const void*)k_matvec_multi<KQ, LPR, NBL>;
+    const int64_t fit = (int64_t)cu_count() * resident_blocks(kern, 0);
+    int64_t total = 0;
+    for (int i = 0; i < count; i++) total += ws[i]->m;
+    MvJobs a{};
+    a.count = count;
+    int64_t wg = 0;
+    for (int i = 0; i < count; i++) {
+        const Weight& w = *ws[i];
+        const int64_t need = (w.m + RPB - 1) / RPB;
+        int64_t g = (fit * w.m + total / 2) / total;
+        if (g < 1) g = 1;
+        if (g > need) g = need;
+        MvJob& j = a.job[i];
+        j.w = WArgs{w.qs, w.d, w.sc};
+        j.w2 = w2s && w2s[i] ? WArgs{w2s[i]->qs, w2s[i]->d, w2s[i]->sc} : WArgs{nullptr, nullptr, nullptr};
+        j.y = ys[i];
+        j.rows = w.m;
+        j.wgs = (int32_t)g;
+        j.share = w.m / g;
+        j.wg0 = (int32_t)wg;
+        wg += g;
+    }
+    hipLaunchKernelGGL((k_matvec_multi<KQ, LPR, NBL>), dim3((unsigned)wg), dim3(WG), 0, s, a, xq, xs, ws[0]->n);
+}
+}  // namespace
+
+int launch_matvec_multi(const Weight* const* ws, const Weight* const* w2s, float* const* ys, int count,
+                        const int8_t* xq, const float* xs, hipStream_t s) {
+    if (count < 1 || count > MV_MAX_JOBS) return set_error(ERR_ARG, "matvec job table: 1..8 weights");
+    for (int i = 0; i < count; i++) {
+        if (ws[i]->kind != KIND_Q8_0 || ws[i]->n != ws[0]->n)
+            return set_error(ERR_SHAPE, "matvec job table: Q8_0 weights of one input length");
+        if (w2s && w2s[i] && (w2s[i]->kind != ws[i]->kind || w2s[i]->n != ws[i]->n || w2s[i]->m != ws[i]->m))
+            return set_error(ERR_SHAPE, "gate/up pair: shapes differ");
+    }
+    // the same lane geometry as launch_kind<Q8> picks for one weight of this K
+    const int64_t nu = ws[0]->n / Q8::UNIT;
+#define UQ_TRYM(L, B) \
+    if (nu <= (int64_t)(L) * (B)) { launch_multi_t<Q8, L, B>(ws, w2s, ys, count, xq, xs, s); return OK; }
+    UQ_TRYM(4, 1) UQ_TRYM(4, 2)
+    UQ_TRYM(8, 1) UQ_TRYM(8, 2) UQ_TRYM(8, 3)
+    UQ_TRYM(16, 2) UQ_TRYM(16, 3) UQ_TRYM(16, 4)
+    UQ_TRYM(32, 3) UQ_TRYM(32, 4)
+    UQ_TRYM(64, 3) UQ_TRYM(64, 4) UQ_TRYM(64, 5) UQ_TRYM(64, 6) UQ_TRYM(64, 7) UQ_TRYM(64, 8)
+    UQ_TRYM(64, 9) UQ_TRYM(64, 10) UQ_TRYM(64, 12) UQ_TRYM(64, 14) UQ_TRYM(64, 16)
+#undef UQ_TRYM
+    return set_error(ERR_SHAPE, "matvec: input length too large");
 }
 
 int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {

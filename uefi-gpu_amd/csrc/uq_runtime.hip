@@ -307,6 +307,22 @@ int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, 
     return OK;
 }
 
+int uq_matvec_table_dev(const uq_weight_t* ws, const uq_weight_t* w2s, int count, const int8_t* xq, const float* xs,
+                        float* const* ys, void* stream) {
+    if (int rc = require_ctx()) return rc;
+    if (!ws || !xq || !xs || !ys || count < 1 || count > 8) return set_error(ERR_ARG, "matvec_table_dev: 1..8 weights");
+    const Weight* wl[8];
+    const Weight* w2l[8];
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !ys[i]) return set_error(ERR_ARG, "matvec_table_dev: null weight or output");
+        wl[i] = &ws[i]->w;
+        w2l[i] = w2s && w2s[i] ? &w2s[i]->w : nullptr;
+    }
+    if (int rc = launch_matvec_multi(wl, w2l, ys, count, xq, xs, pick(stream))) return rc;
+    UQ_CHECK_HIP(hipGetLastError());
+    return OK;
+}
+
 int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream) {
     if (int rc = require_ctx()) return rc;
     if (!gate || !up || !xq || !xs || !out) return set_error(ERR_ARG, "gateup_q_dev: null pointer");
@@ -331,9 +347,23 @@ int uq_batch(const uq_weight_t* ws, int count, const float* x, int64_t n, float*
     UQ_CHECK_HIP(hipMemcpyAsync(g_ctx.dx, x, sizeof(float) * n, hipMemcpyHostToDevice, s));
     launch_quant_act(g_ctx.dx, n, g_ctx.dxq, g_ctx.dxs, s);
     int64_t off = 0;
-    for (int i = 0; i < count; i++) {
-        if (int rc = launch_matvec(ws[i]->w, nullptr, g_ctx.dxq, g_ctx.dxs, g_ctx.dy + off, s)) return rc;
-        off += ms[i];
+    bool q8 = true;
+    for (int i = 0; i < count; i++) q8 = q8 && ws[i]->w.kind == KIND_Q8_0;
+    if (q8 && count > 1) {
+        // one launch for the batch (the reference's QKV job batch)
+        const Weight* wl[3];
+        float* yl[3];
+        for (int i = 0; i < count; i++) {
+            wl[i] = &ws[i]->w;
+            yl[i] = g_ctx.dy + off;
+            off += ms[i];
+        }
+        if (int rc = launch_matvec_multi(wl, nullptr, yl, count, g_ctx.dxq, g_ctx.dxs, s)) return rc;
+    } else {
+        for (int i = 0; i < count; i++) {
+            if (int rc = launch_matvec(ws[i]->w, nullptr, g_ctx.dxq, g_ctx.dxs, g_ctx.dy + off, s)) return rc;
+            off += ms[i];
+        }
     }
     UQ_CHECK_HIP(hipGetLastError());
     std::vector<float> host((size_t)total);
@@ -481,6 +511,66 @@ int uq_time_matvecs(const uq_weight_t* ws, const int* pairs, int count, int64_t 
     hipFree(xs);
     hipFree(y);
     return rc;
+}
+
+int uq_time_matvec_tables(const uq_weight_t* ws, const int* pairs, int count, int64_t max_n, int reps, int warmup,
+                          double* total_ms) {
+    if (int rc = require_ctx()) return rc;
+    if (!ws || count <= 0 || reps <= 0 || warmup < 0 || !total_ms) return set_error(ERR_ARG, "time_matvec_tables: bad args");
+    hipStream_t s = g_ctx.stream;
+    int64_t ysum = 0;
+    for (int i = 0; i < count; i++) {
+        if (!ws[i]) return set_error(ERR_ARG, "time_matvec_tables: null weight");
+        if (ws[i]->w.n > max_n) return set_error(ERR_SHAPE, "time_matvec_tables: weight n > max_n");
+        ysum += ws[i]->w.m;
+    }
+    // consecutive weights of one input length form one table; pairs[i] marks a gate/up pair (i, i+1)
+    struct Table { std::vector<const Weight*> w, w2; std::vector<float*> y; };
+    std::vector<Table> tables;
+    float *x = nullptr, *y = nullptr, *xs = nullptr;
+    int8_t* xq = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&x, sizeof(float) * max_n));
+    UQ_CHECK_HIP(hipMalloc(&xq, max_n));
+    UQ_CHECK_HIP(hipMalloc(&xs, sizeof(float) * (max_n / 32)));
+    UQ_CHECK_HIP(hipMalloc(&y, sizeof(float) * ysum));
+    std::vector<float> hx((size_t)max_n);
+    for (int64_t i = 0; i < max_n; i++) hx[i] = (float)((i * 37) % 251) / 125.0f - 1.0f;
+    UQ_CHECK_HIP(hipMemcpyAsync(x, hx.data(), sizeof(float) * max_n, hipMemcpyHostToDevice, s));
+    launch_quant_act(x, max_n, xq, xs, s);
+    int64_t yo = 0;
+    for (int i = 0; i < count; i++) {
+        const bool pair = pairs && pairs[i] && i + 1 < count;
+        if (tables.empty() || tables.back().w.back()->n != ws[i]->w.n || tables.back().w.size() == 8) tables.emplace_back();
+        tables.back().w.push_back(&ws[i]->w);
+        tables.back().w2.push_back(pair ? &ws[i + 1]->w : nullptr);
+        tables.back().y.push_back(y + yo);
+        yo += ws[i]->w.m;
+        if (pair) i++;
+    }
+    hipEvent_t t0, t1;
+    UQ_CHECK_HIP(hipEventCreate(&t0));
+    UQ_CHECK_HIP(hipEventCreate(&t1));
+    int rc = OK;
+    for (int r = 0; r < warmup + reps && rc == OK; r++) {
+        if (r == warmup) UQ_CHECK_HIP(hipEventRecord(t0, s));
+        for (const Table& t : tables) {
+            rc = launch_matvec_multi(t.w.data(), t.w2.data(), t.y.data(), (int)t.w.size(), xq, xs, s);
+            if (rc) break;
+        }
+    }
+    UQ_CHECK_HIP(hipEventRecord(t1, s));
+    UQ_CHECK_HIP(hipEventSynchronize(t1));
+    float ms = 0;
+    UQ_CHECK_HIP(hipEventElapsedTime(&ms, t0, t1));
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    hipFree(x);
+    hipFree(xq);
+    hipFree(xs);
+    hipFree(y);
+    if (rc) return rc;
+    *total_ms = ms;
+    return OK;
 }
 
 }  // extern "C"

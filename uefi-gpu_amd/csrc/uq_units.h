@@ -283,10 +283,15 @@ struct Q3K {
 struct RowSpan {
     int64_t begin, end, step;
 };
-__device__ __forceinline__ RowSpan even_span(int64_t rows, int64_t share) {
-    const int64_t b = blockIdx.x, extra = rows - share * (int64_t)gridDim.x;
+// Rows [begin, end) of workgroup b of g when `rows` are split evenly (share =
+// rows / g, the first rows - share*g workgroups take one more).
+__device__ __forceinline__ RowSpan even_span_of(int64_t rows, int64_t share, int64_t b, int64_t g) {
+    const int64_t extra = rows - share * g;
     const int64_t begin = b * share + (b < extra ? b : extra);
     return RowSpan{begin, begin + share + (b < extra ? 1 : 0), share + 1};
+}
+__device__ __forceinline__ RowSpan even_span(int64_t rows, int64_t share) {
+    return even_span_of(rows, share, blockIdx.x, gridDim.x);
 }
 template <int RPB>
 __device__ __forceinline__ RowSpan row_span(int64_t rows, int64_t share) {

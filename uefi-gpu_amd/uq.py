@@ -69,6 +69,8 @@ _SIGS = {
     "uq_quant_act_dev": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "uq_matvec_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "uq_gateup_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "uq_matvec_table_dev": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int, _vp, _vp,
+                                           ctypes.POINTER(_vp), _vp]),
     "uq_quant_act": (ctypes.c_int, [_c_f32p, _i64, _c_i8p, _c_f32p]),
     "uq_block_dots": (ctypes.c_int, [_vp, _c_f32p, _i64, _c_i32p, _i64]),
     "uq_dequantize": (ctypes.c_int, [ctypes.c_uint32, _vp, ctypes.c_size_t, _i64, _c_f32p]),
@@ -84,6 +86,8 @@ _SIGS = {
     "uq_dev_free": (ctypes.c_int, [_vp]),
     "uq_memcpy_h2d": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
     "uq_memcpy_d2h": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t]),
+    "uq_time_matvec_tables": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int), ctypes.c_int, _i64,
+                                             ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "uq_time_matvecs": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int), ctypes.c_int, _i64,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -333,6 +337,15 @@ def probe_bandwidth(nbytes=1 << 30, reps=10):
     r, c = ctypes.c_double(), ctypes.c_double()
     _check(lib().uq_probe_bandwidth(nbytes, reps, ctypes.byref(r), ctypes.byref(c)))
     return r.value, c.value
+
+
+def time_matvec_tables(weights, pairs, max_n, reps, warmup):
+    """HIP-event ms of `reps` rounds, consecutive same-K weights as one job-table launch."""
+    handles = (_vp * len(weights))(*[w.handle for w in weights])
+    pr = (ctypes.c_int * len(weights))(*pairs)
+    ms = ctypes.c_double()
+    _check(lib().uq_time_matvec_tables(handles, pr, len(weights), max_n, reps, warmup, ctypes.byref(ms)))
+    return ms.value
 
 
 def time_matvecs(weights, pairs, max_n, reps, warmup, probe):

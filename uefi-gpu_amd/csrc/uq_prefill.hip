@@ -75,7 +75,11 @@ __global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, i
 // reference's order; that work, not the MFMA, bounds this kernel.
 constexpr int GK_BLK = 4;                  // 32-blocks per stage
 constexpr int GBM = 32, GBN = 64;          // rows, tokens per workgroup tile
-constexpr int GR = 4;                      // ring depth (stages)
+// Ring depth 2: one stage in flight while one is computed. The kernel is
+// VALU-bound (the per-block f32 rescale), so occupancy hides more than ring
+// depth: 2 stages fit four gate/up workgroups per CU where 4 stages fit two
+// (gate+up 104 -> 76 us at 512 tokens; 3 stages changed nothing).
+constexpr int GR = 2;
 
 template <bool GU>
 struct GemmStageLds {

@@ -17,6 +17,7 @@
 #include "uq_device.h"
 #include "uq_blockops.h"
 #include "uq_prefill.h"
+#include "uq_internal.h"
 
 namespace uq {
 namespace {
@@ -74,25 +75,31 @@ __global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, i
 // Per output and block the VALU does (float)c, dw*dx and the fmaf in the
 // reference's order; that work, not the MFMA, bounds this kernel.
 constexpr int GK_BLK = 4;                  // 32-blocks per stage
-constexpr int GBM = 32, GBN = 64;          // rows, tokens per workgroup tile
+constexpr int GBM = 32;                    // rows per workgroup tile
 // Ring depth 2: one stage in flight while one is computed. The kernel is
 // VALU-bound (the per-block f32 rescale), so occupancy hides more than ring
 // depth: 2 stages fit four gate/up workgroups per CU where 4 stages fit two
 // (gate+up 104 -> 76 us at 512 tokens; 3 stages changed nothing).
 constexpr int GR = 2;
 
-template <bool GU>
+// WM = MFMA row tiles per wave: WM 2 gives waves of 32 rows x 16 tokens
+// (workgroup 32 x 64), WM 1 waves of 16 rows x 16 tokens in a 2 x 2 grid
+// (workgroup 32 x 32): twice the waves for the narrow projections, whose
+// 32 x 64 grids leave SIMDs with one or two waves.
+template <int WM>
+constexpr int gemm_bn() { return WM == 2 ? 64 : 32; }
+template <bool GU, int WM>
 struct GemmStageLds {
     int8_t a[GBM * 128];
     int8_t a2[GU ? GBM * 128 : 16];
-    int8_t b[GBN * 128];
+    int8_t b[gemm_bn<WM>() * 128];
     float sw[GK_BLK * GBM];
     float sw2[GU ? GK_BLK * GBM : 4];
-    float sx[GK_BLK * GBN];
+    float sx[GK_BLK * gemm_bn<WM>()];
 };
-// loads per wave per stage: A (1), A2 (1), B (2), scales sw, sw2, sx
-template <bool GU>
-constexpr int gemm_lps() { return GU ? 7 : 5; }
+// loads per wave per stage: A (1), A2 (1), B (WM), scales sw, sw2, sx
+template <bool GU, int WM>
+constexpr int gemm_lps() { return (GU ? 5 : 3) + WM; }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) { uq_lds_load16(g, lds_wave_base); }
@@ -105,16 +112,16 @@ struct GemmSrc {
     const int8_t *a, *a2, *b0, *b1;
     const float *sw, *sw2, *sx;
 };
-template <bool GU>
+template <bool GU, int WM>
 __device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int64_t r0, int64_t t0, int wave, int lane) {
     const int64_t K = p.k, N = p.n;
     const int slot = lane & 7, row = 8 * wave + (lane >> 3);
-    const int tk0 = 16 * wave + (lane >> 3), tk1 = tk0 + 8;
+    const int tk0 = 8 * WM * wave + (lane >> 3), tk1 = tk0 + 8;
     GemmSrc g;
     g.a = p.w_qs + (r0 + row) * K + 16 * (slot ^ swz(row));
     g.a2 = GU ? p.w2_qs + (r0 + row) * K + 16 * (slot ^ swz(row)) : nullptr;
     g.b0 = p.xq + (t0 + tk0) * K + 16 * (slot ^ swz(tk0));
-    g.b1 = p.xq + (t0 + tk1) * K + 16 * (slot ^ swz(tk1));
+    g.b1 = WM == 2 ? p.xq + (t0 + tk1) * K + 16 * (slot ^ swz(tk1)) : nullptr;
     g.sw = p.w_ds + (int64_t)wave * N + r0 + 4 * (lane & 7);
     g.sw2 = GU ? p.w2_ds + (int64_t)wave * N + r0 + 4 * (lane & 7) : nullptr;
     g.sx = p.xst + (int64_t)wave * p.mp + t0 + 4 * (lane & 15);
@@ -124,14 +131,15 @@ __device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int64_t r0, int
 // Issue the global->LDS loads of one stage (first block kb). A full stage
 // offsets the precomputed pointers; a partial last stage (nblk < 4) re-reads
 // its last valid block in place of the missing ones (values unused).
-template <bool GU>
-__device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g, GemmStageLds<GU>& S,
+template <bool GU, int WM>
+__device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g, GemmStageLds<GU, WM>& S,
                                            int64_t kb, int nblk, int wave, int lane) {
+    constexpr int BN = gemm_bn<WM>();
     const int slot = lane & 7;
     int64_t da = kb * 32, db0 = da, db1 = da, dsw = kb * p.n, dsx = kb * (int64_t)p.mp;
     if (nblk < GK_BLK) {
         // chunk c = slot ^ swz(row) of block c/2; clamp the block, keep the half
-        const int row = 8 * wave + (lane >> 3), tk0 = 16 * wave + (lane >> 3), tk1 = tk0 + 8;
+        const int row = 8 * wave + (lane >> 3), tk0 = 8 * WM * wave + (lane >> 3), tk1 = tk0 + 8;
         auto shift = [&](int r) {
             const int c = slot ^ swz(r), blk = c >> 1, cb = blk < nblk ? blk : nblk - 1;
             return (int64_t)(cb - blk) * 32;
@@ -145,13 +153,13 @@ __device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g
     }
     lds_load16(g.a + da, S.a + wave * 1024);
     if (GU) lds_load16(g.a2 + da, S.a2 + wave * 1024);
-    lds_load16(g.b0 + db0, S.b + (2 * wave) * 1024);
-    lds_load16(g.b1 + db1, S.b + (2 * wave + 1) * 1024);
+    lds_load16(g.b0 + db0, S.b + (WM * wave) * 1024);
+    if (WM == 2) lds_load16(g.b1 + db1, S.b + (2 * wave + 1) * 1024);
     if (lane < GBM / 4) {
         lds_load16(g.sw + dsw, S.sw + wave * GBM);
         if (GU) lds_load16(g.sw2 + dsw, S.sw2 + wave * GBM);
     }
-    if (lane < GBN / 4) lds_load16(g.sx + dsx, S.sx + wave * GBN);
+    if (lane < BN / 4) lds_load16(g.sx + dsx, S.sx + wave * BN);
 }
 
 // Wait until at most `n` vector-memory ops of this wave are outstanding
@@ -174,19 +182,20 @@ __device__ __forceinline__ void stage_barrier() {
 
 // NB consecutive 32-blocks (from j0) of a stage: every MFMA of the group is
 // issued first, then the f32 rescale runs block by block in order.
-template <bool GU, int NB>
-__device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU>& S, int j0, int wc, int lane,
-                                            float (&f)[2][4], float (&g)[2][4]) {
+template <bool GU, int WM, int NB>
+__device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU, WM>& S, int j0, int wc, int rb, int lane,
+                                            float (&f)[WM][4], float (&g)[WM][4]) {
+    constexpr int BN = gemm_bn<WM>();
     const int li = lane & 15, lm = (lane >> 4) * 4, sub = ((lane >> 4) & 1) * 8, hi = lane >> 5;
     const v4i z = {0, 0, 0, 0};
-    v4i c[NB][2], c2[NB][2];
+    v4i c[NB][WM], c2[NB][WM];
 #pragma unroll
     for (int jj = 0; jj < NB; jj++) {
         const int j = j0 + jj, gc = 2 * j + hi;
-        long av[2], a2v[2], bv;
+        long av[WM], a2v[WM], bv;
 #pragma unroll
-        for (int m = 0; m < 2; m++) {
-            const int row = 16 * m + li;
+        for (int m = 0; m < WM; m++) {
+            const int row = rb + 16 * m + li;
             const int off = row * 128 + ((gc ^ swz(row)) << 4) + sub;
             av[m] = *(const long*)(S.a + off);
             if (GU) a2v[m] = *(const long*)(S.a2 + off);
@@ -196,7 +205,7 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU>& S, int j0, i
             bv = *(const long*)(S.b + tok * 128 + ((gc ^ swz(tok)) << 4) + sub);
         }
 #pragma unroll
-        for (int m = 0; m < 2; m++) {
+        for (int m = 0; m < WM; m++) {
             c[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[m], bv, z, 0, 0, 0);
             if (GU) c2[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2v[m], bv, z, 0, 0, 0);
         }
@@ -204,12 +213,12 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU>& S, int j0, i
 #pragma unroll
     for (int jj = 0; jj < NB; jj++) {
         const int j = j0 + jj;
-        const float x = S.sx[j * GBN + wc + li];
+        const float x = S.sx[j * BN + wc + li];
 #pragma unroll
-        for (int m = 0; m < 2; m++) {
-            const v4f w = *(const v4f*)(S.sw + j * GBM + 16 * m + lm);
+        for (int m = 0; m < WM; m++) {
+            const v4f w = *(const v4f*)(S.sw + j * GBM + rb + 16 * m + lm);
             v4f w2;
-            if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + 16 * m + lm);
+            if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + rb + 16 * m + lm);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 f[m][q] = fmaf((float)c[jj][m][q], w[q] * x, f[m][q]);
@@ -219,26 +228,27 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU>& S, int j0, i
     }
 }
 
-template <bool GU>
+template <bool GU, int WM>
 __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) GemmStageLds<GU> ring[GR];
-    constexpr int LPS = gemm_lps<GU>();
+    __shared__ __attribute__((aligned(16))) GemmStageLds<GU, WM> ring[GR];
+    constexpr int LPS = gemm_lps<GU, WM>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wc = wave * 16;
-    const int64_t r0 = (int64_t)blockIdx.x * GBM, t0 = (int64_t)blockIdx.y * GBN;
+    // the wave's tile: tokens wc.. of the workgroup's, rows rb..
+    const int wc = WM == 2 ? wave * 16 : (wave >> 1) * 16, rb = WM == 2 ? 0 : (wave & 1) * 16;
+    const int64_t r0 = (int64_t)blockIdx.x * GBM, t0 = (int64_t)blockIdx.y * gemm_bn<WM>();
     const int64_t nb = a.k / 32, nst = (nb + GK_BLK - 1) / GK_BLK;
     auto nblk_of = [&](int64_t s) { return (int)(nb - s * GK_BLK < GK_BLK ? nb - s * GK_BLK : GK_BLK); };
-    float f[2][4], g[2][4];
+    float f[WM][4], g[WM][4];
 #pragma unroll
-    for (int m = 0; m < 2; m++)
+    for (int m = 0; m < WM; m++)
 #pragma unroll
         for (int q = 0; q < 4; q++) f[m][q] = g[m][q] = 0.0f;
-    const GemmSrc src = gemm_src<GU>(a, r0, t0, wave, lane);
+    const GemmSrc src = gemm_src<GU, WM>(a, r0, t0, wave, lane);
     // prologue: stages 0 .. GR-2 in flight
 #pragma unroll
     for (int s = 0; s < GR - 1; s++)
-        if (s < nst) gemm_issue<GU>(a, src, ring[s], (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
+        if (s < nst) gemm_issue<GU, WM>(a, src, ring[s], (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
     for (int64_t s = 0; s < nst; s++) {
         // stage s landed for this wave: the stages issued after it may stay in flight
         const int64_t later = (nst - 1 - s < GR - 2) ? nst - 1 - s : GR - 2;
@@ -247,20 +257,20 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
         else wait_vm<0>();
         stage_barrier();  // every wave's loads of stage s landed; stage s-1 fully consumed
         const int64_t sn = s + GR - 1;
-        if (sn < nst) gemm_issue<GU>(a, src, ring[sn % GR], sn * GK_BLK, nblk_of(sn), wave, lane);
-        const GemmStageLds<GU>& S = ring[s % GR];
+        if (sn < nst) gemm_issue<GU, WM>(a, src, ring[sn % GR], sn * GK_BLK, nblk_of(sn), wave, lane);
+        const GemmStageLds<GU, WM>& S = ring[s % GR];
         const int nblk = nblk_of(s);
         if (nblk == GK_BLK) {
-            gemm_blocks<GU, GU ? 2 : 4>(S, 0, wc, lane, f, g);
-            if (GU) gemm_blocks<GU, 2>(S, 2, wc, lane, f, g);
+            gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
+            if (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
         } else {
-            for (int j = 0; j < nblk; j++) gemm_blocks<GU, 1>(S, j, wc, lane, f, g);
+            for (int j = 0; j < nblk; j++) gemm_blocks<GU, WM, 1>(S, j, wc, rb, lane, f, g);
         }
     }
     const int li = lane & 15, lm = (lane >> 4) * 4;
 #pragma unroll
-    for (int m = 0; m < 2; m++) {
-        const int64_t t = t0 + wc + li, r = r0 + 16 * m + lm;
+    for (int m = 0; m < WM; m++) {
+        const int64_t t = t0 + wc + li, r = r0 + rb + 16 * m + lm;
         float4 o;
         if (GU) {
             o = make_float4(uq_silu_mul(f[m][0], g[m][0]), uq_silu_mul(f[m][1], g[m][1]),
@@ -518,10 +528,19 @@ void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, 
     hipLaunchKernelGGL(k_pf_quant, dim3((unsigned)((k + 255) / 256), tokens), dim3(256), 0, s, x, k, mp, xq, xst);
 }
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s) {
-    if (a.n % 64 || a.mp % GBN || a.k % 32 || a.k <= 0) return -1;
-    const dim3 grid((unsigned)(a.n / GBM), (unsigned)(a.mp / GBN));
-    if (a.w2_qs) hipLaunchKernelGGL(k_pf_gemm<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(k_pf_gemm<false>, grid, dim3(256), 0, s, a);
+    if (a.n % 64 || a.mp % 64 || a.k % 32 || a.k <= 0) return -1;
+    // 32 x 64 workgroup tiles unless that grid gives fewer than four
+    // workgroups per CU; then 32 x 32 tiles of 16 x 16 waves
+    const bool narrow = (a.n / GBM) * (a.mp / 64) < 4 * (int64_t)cu_count();
+    if (narrow) {
+        const dim3 grid((unsigned)(a.n / GBM), (unsigned)(a.mp / gemm_bn<1>()));
+        if (a.w2_qs) hipLaunchKernelGGL((k_pf_gemm<true, 1>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_pf_gemm<false, 1>), grid, dim3(256), 0, s, a);
+    } else {
+        const dim3 grid((unsigned)(a.n / GBM), (unsigned)(a.mp / gemm_bn<2>()));
+        if (a.w2_qs) hipLaunchKernelGGL((k_pf_gemm<true, 2>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_pf_gemm<false, 2>), grid, dim3(256), 0, s, a);
+    }
     return 0;
 }
 void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s) {

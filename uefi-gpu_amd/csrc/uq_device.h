@@ -206,19 +206,21 @@ UQ_DEV int8_t uq_quant_lane(float v, float* scale_out) {
 // returns the block scale and packs the 4 int8 codes (lowest value in the low
 // byte). The amax is an fmaxf tree like uq_quant_lane's (a NaN is dropped
 // unless the whole block is NaN), so both give the same codes and scale.
+// The code of one value given its block's 127/amax (0 for an all-zero or
+// all-NaN block), as uq_quant_lane computes it.
+UQ_DEV uint32_t uq_quant_code(float v, float inv) {
+    float r = __builtin_rintf(v * inv);
+    if (r != r) r = 0.0f;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (uint32_t)(uint8_t)(int8_t)(int)r;
+}
 UQ_DEV float uq_quant4_group8(const float v[4], uint32_t* packed) {
     float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     a = uq_group_max<8>(a);
     const float inv = a > 0.0f ? 127.0f / a : 0.0f;
     uint32_t p = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const float t = v[c] * inv;
-        float r = __builtin_rintf(t);
-        if (r != r) r = 0.0f;
-        r = fminf(fmaxf(r, -127.0f), 127.0f);
-        p |= ((uint32_t)(uint8_t)(int8_t)(int)r) << (8 * c);
-    }
+    for (int c = 0; c < 4; c++) p |= uq_quant_code(v[c], inv) << (8 * c);
     *packed = p;
     return a / 127.0f;
 }

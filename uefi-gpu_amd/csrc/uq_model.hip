@@ -378,8 +378,13 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
         na.mp = mp;
         launch_pf_norm(na, n, s);
     };
-    auto gemm = [&](const Weight& w, const float* dt, const Weight* w2, const float* dt2, float* y) {
-        PfGemmArgs ga{w.qs, dt, w2 ? w2->qs : nullptr, dt2, PXQ, PXST, y, w.m, w.n, mp};
+    // the gate/up GEMM quantizes SiLU(gate)*up into the arena of PG (codes,
+    // then scales) for the down GEMM
+    int8_t* const hq = (int8_t*)PG;
+    float* const hst = (float*)((char*)PG + (((size_t)pcap * c.hidden + 255) & ~(size_t)255));
+    auto gemm = [&](const Weight& w, const float* dt, const Weight* w2, const float* dt2, float* y,
+                    const int8_t* xq = nullptr, const float* xst = nullptr, int8_t* yq = nullptr, float* yst = nullptr) {
+        PfGemmArgs ga{w.qs, dt, w2 ? w2->qs : nullptr, dt2, xq ? xq : PXQ, xst ? xst : PXST, y, w.m, w.n, mp, yq, yst};
         return launch_pf_gemm(ga, s);
     };
     for (int l = 0; l < c.layers; l++) {
@@ -396,10 +401,10 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
         if (gemm(*weight(lname(l, "attn_output.weight")), L.o_dt, nullptr, nullptr, PTMP))
             return fail(ERR_SHAPE, "prefill: o rows not a multiple of 64");
         norm(l, vec(lname(l, "ffn_norm.weight")), false);
-        if (gemm(*weight(lname(l, "ffn_gate.weight")), L.g_dt, weight(lname(l, "ffn_up.weight")), L.u_dt, PG))
+        if (gemm(*weight(lname(l, "ffn_gate.weight")), L.g_dt, weight(lname(l, "ffn_up.weight")), L.u_dt, nullptr,
+                 nullptr, nullptr, hq, hst))
             return fail(ERR_SHAPE, "prefill: ffn rows not a multiple of 64");
-        launch_pf_quant(PG, c.hidden, n, mp, PXQ, PXST, s);
-        if (gemm(*weight(lname(l, "ffn_down.weight")), L.d_dt, nullptr, nullptr, PTMP))
+        if (gemm(*weight(lname(l, "ffn_down.weight")), L.d_dt, nullptr, nullptr, PTMP, hq, hst))
             return fail(ERR_SHAPE, "prefill: down rows not a multiple of 64");
     }
     // the last prompt token through the decode output head (gpu_prefill.rs:138-148)

@@ -29,6 +29,10 @@ struct PfGemmArgs {
     float* y;                // [mp][n]
     int64_t n, k;
     int mp;
+    // gate/up only, instead of y: SiLU(gate)*up quantized per 32 rows, codes
+    // [mp][n] and scales [n/32][mp] (the next GEMM's input planes), or null
+    int8_t* yq;
+    float* yst;
 };
 
 struct PfRopeArgs {

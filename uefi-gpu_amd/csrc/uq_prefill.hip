@@ -268,6 +268,33 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
         }
     }
     const int li = lane & 15, lm = (lane >> 4) * 4;
+    if (GU && WM == 2 && a.yq) {
+        // SiLU(gate)*up quantized per 32-block into the next GEMM's planes:
+        // the workgroup's 32 rows are one block of each token, held by lanes
+        // li, li+16, li+32, li+48 (8 values each) of one wave
+        float o[WM][4];
+        float am = 0.0f;
+#pragma unroll
+        for (int m = 0; m < WM; m++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                o[m][q] = uq_silu_mul(f[m][q], g[m][q]);
+                am = (m | q) ? fmaxf(am, fabsf(o[m][q])) : fabsf(o[m][q]);
+            }
+        am = fmaxf(am, __shfl_xor(am, 16, 64));
+        am = fmaxf(am, __shfl_xor(am, 32, 64));
+        const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+        const int64_t t = t0 + wc + li;
+#pragma unroll
+        for (int m = 0; m < WM; m++) {
+            uint32_t p = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) p |= uq_quant_code(o[m][q], inv) << (8 * q);
+            *(uint32_t*)(a.yq + t * a.n + r0 + 16 * m + lm) = p;
+        }
+        if (lane < 16) a.yst[(r0 / 32) * a.mp + t] = am / 127.0f;
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < WM; m++) {
         const int64_t t = t0 + wc + li, r = r0 + rb + 16 * m + lm;
@@ -531,7 +558,9 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s) {
     if (a.n % 64 || a.mp % 64 || a.k % 32 || a.k <= 0) return -1;
     // 32 x 64 workgroup tiles unless that grid gives fewer than four
     // workgroups per CU; then 32 x 32 tiles of 16 x 16 waves
-    const bool narrow = (a.n / GBM) * (a.mp / 64) < 4 * (int64_t)cu_count();
+    if (a.yq && (!a.w2_qs || !a.yst)) return -1;
+    // the quantizing gate/up epilogue needs a wave's tile to hold whole blocks (wide tiles)
+    const bool narrow = !a.yq && (a.n / GBM) * (a.mp / 64) < 4 * (int64_t)cu_count();
     if (narrow) {
         const dim3 grid((unsigned)(a.n / GBM), (unsigned)(a.mp / gemm_bn<1>()));
         if (a.w2_qs) hipLaunchKernelGGL((k_pf_gemm<true, 1>), grid, dim3(256), 0, s, a);

@@ -394,10 +394,13 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
         PfRopeArgs ra{PY, nqkv, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")), vec(lname(l, "attn_v.bias")),
                       trig, kcache + l * kvl, vcache + l * kvl, 0, c.heads, c.kv_heads, c.head_dim};
         launch_pf_rope_kv(ra, n, s);
+        // head_dim 128: the attention epilogue quantizes its output for the o GEMM
+        const bool fused_quant = c.head_dim == 128;
         PfAttnArgs aa{PY, nqkv, kcache + l * kvl, vcache + l * kvl, PATT, n, 0, pcap, c.heads, c.kv_heads, c.head_dim,
-                      (float)(1.0 / std::sqrt((double)c.head_dim))};
+                      (float)(1.0 / std::sqrt((double)c.head_dim)), fused_quant ? PXQ : nullptr,
+                      fused_quant ? PXST : nullptr, mp};
         if (launch_pf_attention(aa, s)) return fail(ERR_SHAPE, "prefill: attention head_dim unsupported");
-        launch_pf_quant(PATT, c.dim, n, mp, PXQ, PXST, s);
+        if (!fused_quant) launch_pf_quant(PATT, c.dim, n, mp, PXQ, PXST, s);
         if (gemm(*weight(lname(l, "attn_output.weight")), L.o_dt, nullptr, nullptr, PTMP))
             return fail(ERR_SHAPE, "prefill: o rows not a multiple of 64");
         norm(l, vec(lname(l, "ffn_norm.weight")), false);

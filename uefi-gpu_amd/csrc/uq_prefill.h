@@ -54,6 +54,11 @@ struct PfAttnArgs {
     int n, p0, kcap;         // queries, first position, key capacity (>= p0 + n)
     int heads, kv_heads, head_dim;
     float qscale;
+    // head_dim 128 only, instead of out: the output quantized per 32 dims
+    // (codes [n][heads*hd], scales [heads*hd/32][mp]: the o GEMM's input planes), or null
+    int8_t* xq;
+    float* xst;
+    int mp;
 };
 
 void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float* dt, hipStream_t s);

@@ -532,6 +532,31 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
             k0 += 4 * SU;
         }
     }
+    if (DT * 16 == 32 && a.xq) {
+        // this wave's 32 dims of head h are one quant block of each query: the
+        // block's values sit in the 16 lanes of group g (DT each)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int qi = 4 * r + g;
+            float v[DT];
+            float am = 0.0f;
+#pragma unroll
+            for (int j = 0; j < DT; j++) {
+                v[j] = (float)(o[j][r] + o2[j][r]);
+                am = j ? fmaxf(am, fabsf(v[j])) : fabsf(v[j]);
+            }
+            am = uq_group_max<16>(am);
+            const float inv = am > 0.0f ? 127.0f / am : 0.0f;
+            if (qi < nq) {
+                const size_t col = (size_t)h * HD + wave * DT * 16;
+                int8_t* q = a.xq + (size_t)(tq0 + qi) * (a.heads * HD) + col + c;
+#pragma unroll
+                for (int j = 0; j < DT; j++) q[j * 16] = (int8_t)uq_quant_code(v[j], inv);
+                if (c == 0) a.xst[(col / 32) * a.mp + tq0 + qi] = am / 127.0f;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int qi = 4 * r + g;

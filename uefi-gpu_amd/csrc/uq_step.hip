@@ -315,18 +315,20 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
 }
 
 // ------------------------------------------------------------------ decode FFN
-// Both FFN launches use one 1024-thread workgroup per CU with the rows split
-// evenly over the grid: a CU's share of a weight stream is bounded by its
-// share of HBM bandwidth, so a CU holding two workgroups would finish last and
-// set the kernel's duration. Waves that hold no rows do the prologue work
-// meanwhile: a wave stalls at issue while its CU's weight stream drains, so a
-// wave that also streams weights could not start its prologue until then.
+// The rows are split evenly over the grid, and in every workgroup the waves
+// that hold no rows do the prologue work meanwhile: a wave stalls at issue
+// while its CU's weight stream drains, so a wave that also streams weights
+// could not start its prologue until then. Down uses one 1024-thread
+// workgroup per CU (two 512-thread ones measured slower); gate/up four
+// 256-thread workgroups per CU, each with its own prologue wave (1016 ->
+// 1041 tok/s against one 1024-thread workgroup; 2 x 512 gave 1027, 8 x 256
+// and 8 x 128 were slower).
 
-// Gate/up: 4 rows per wave (16 lanes per row), waves 0..14 hold rows, wave 15
-// runs the RMSNorm + quant prologue of the input.
-constexpr int GH_RPW = 4, GH_ROWS_MAX = 15 * GH_RPW;
+// Gate/up: 4 rows per wave (16 lanes per row), waves 0..GH_NW-2 hold rows,
+// the last wave runs the RMSNorm + quant prologue of the input.
+constexpr int GH_RPW = 4, GH_NW = 4, GH_ROWS_MAX = (GH_NW - 1) * GH_RPW;
 template <int NBL>
-__global__ __launch_bounds__(1024) void k_gateup_h(GateArgs a) {
+__global__ __launch_bounds__(GH_NW * 64) void k_gateup_h(GateArgs a) {
     constexpr int NC = NBL < MAX_DIM / 256 ? NBL : MAX_DIM / 256;  // dim <= 16 lanes x NBL units x 16
     __shared__ __attribute__((aligned(16))) float lx[NC * 256];
     __shared__ __attribute__((aligned(16))) float lr[NC * 256];
@@ -337,13 +339,13 @@ __global__ __launch_bounds__(1024) void k_gateup_h(GateArgs a) {
     const int64_t nu = a.k / Q8::UNIT;
     const RowSpan sp = even_span(a.rows, a.share);
     const int64_t lo = sp.begin, hi = sp.end;
-    const bool rows_wave = wave < 15 && wave * GH_RPW < hi - lo;  // wave-uniform
+    const bool rows_wave = wave < GH_NW - 1 && wave * GH_RPW < hi - lo;  // wave-uniform
     const int64_t row = lo + wave * GH_RPW + grp, rr = row < hi ? row : hi - 1;
     const WArgs wg{a.g_qs, a.g_d, nullptr}, wu{a.u_qs, a.u_d, nullptr};
     NormQuantWave<NC> nw;
-    if (wave == 15) nw.issue(a.nq, lx, lr, lg);
-    uq_issue_barrier();  // the prologue's loads are queued before any weight load of this CU
-    if (wave == 15) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
+    if (wave == GH_NW - 1) nw.issue(a.nq, lx, lr, lg);
+    uq_issue_barrier();  // the prologue's loads are queued before any weight load of this workgroup
+    if (wave == GH_NW - 1) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
     Q8::W gw[NBL], uw[NBL];
     if (rows_wave) {
 #pragma unroll
@@ -564,12 +566,12 @@ int launch_wo_acc(const WoArgs& a, hipStream_t s) {
 }
 int launch_gateup_h(const GateArgs& a, hipStream_t s) {
     if (a.k > MAX_DIM || a.k % 32 || a.nq.dim != a.k || a.rows <= 0) return -1;
-    int64_t g = cu_count();
+    int64_t g = 4 * cu_count();
     if (g > a.rows) g = a.rows;
     if ((a.rows + g - 1) / g > GH_ROWS_MAX) g = (a.rows + GH_ROWS_MAX - 1) / GH_ROWS_MAX;
     GateArgs b = a;
     b.share = a.rows / g;
-    return pick_nbl<16, GateUpH>(a.k / Q8::UNIT, dim3((unsigned)g), dim3(1024), 0, s, b);
+    return pick_nbl<16, GateUpH>(a.k / Q8::UNIT, dim3((unsigned)g), dim3(GH_NW * 64), 0, s, b);
 }
 int launch_down_h(const DownArgs& a, hipStream_t s) {
     if (a.k % 32 || a.k > 9 * 64 * Q8::UNIT || a.rows <= 0) return -1;

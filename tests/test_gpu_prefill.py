@@ -27,8 +27,10 @@ def quant_rows(X):
     return np.stack([q for q, _ in qs]), np.stack([s for _, s in qs])
 
 
+# (4096, 1536, 512) runs the 32 x 64 workgroup tiles; the others give grids
+# of under four workgroups per CU and run the 32 x 32 tiles
 @pytest.mark.parametrize("N,K,T", [(1536, 1536, 512), (256, 1536, 77), (8960, 1536, 64), (1536, 8960, 40),
-                                   (64, 32, 1), (128, 64, 130)])
+                                   (64, 32, 1), (128, 64, 130), (4096, 1536, 512)])
 def test_prefill_gemm_bit_exact(gpu, N, K, T):
     raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0003 + N, N, K)
     X = np.stack([uq.synth_normal(0x5EED0003 + t, K) for t in range(T)])

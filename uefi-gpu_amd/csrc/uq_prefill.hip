@@ -249,23 +249,32 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
     for (int s = 0; s < GR - 1; s++)
         if (s < nst) gemm_issue<GU, WM>(a, src, ring[s], (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
-    for (int64_t s = 0; s < nst; s++) {
-        // stage s landed for this wave: the stages issued after it may stay in flight
+    // stage s landed for this wave (the stages issued after it may stay in
+    // flight), then every wave's loads of stage s landed and stage s-1 is
+    // fully consumed; the next stage's loads go out
+    auto enter = [&](int64_t s) {
         const int64_t later = (nst - 1 - s < GR - 2) ? nst - 1 - s : GR - 2;
         if (later >= 2) wait_vm<2 * LPS>();
         else if (later == 1) wait_vm<LPS>();
         else wait_vm<0>();
-        stage_barrier();  // every wave's loads of stage s landed; stage s-1 fully consumed
+        stage_barrier();
         const int64_t sn = s + GR - 1;
         if (sn < nst) gemm_issue<GU, WM>(a, src, ring[sn % GR], sn * GK_BLK, nblk_of(sn), wave, lane);
+    };
+    // full stages in a loop with no other path, so the accumulators stay in
+    // their registers across iterations; a partial last stage after it
+    const int64_t nfull = nb / GK_BLK;
+    for (int64_t s = 0; s < nfull; s++) {
+        enter(s);
         const GemmStageLds<GU, WM>& S = ring[s % GR];
-        const int nblk = nblk_of(s);
-        if (nblk == GK_BLK) {
-            gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
-            if (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
-        } else {
-            for (int j = 0; j < nblk; j++) gemm_blocks<GU, WM, 1>(S, j, wc, rb, lane, f, g);
-        }
+        gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
+        if (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
+    }
+    if (nst > nfull) {
+        enter(nfull);
+        const GemmStageLds<GU, WM>& S = ring[nfull % GR];
+        const int nblk = nblk_of(nfull);
+        for (int j = 0; j < nblk; j++) gemm_blocks<GU, WM, 1>(S, j, wc, rb, lane, f, g);
     }
     const int li = lane & 15, lm = (lane >> 4) * 4;
     if (GU && WM == 2 && a.yq) {

@@ -106,61 +106,68 @@ __device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) {
 // rows r and r+16 (read by one ds_read2 of the two MFMA row tiles) get different slots
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
 
-// Per-lane source pointers of the stage loads at k = 0 (a full stage adds
-// kb * 32 bytes to the quantized planes and kb block rows to the scale planes).
+// Per-lane byte offsets of the stage loads from wave-uniform bases: each load
+// is a uniform 64-bit base (scalar registers, advanced once per stage by
+// scalar arithmetic) plus a 32-bit per-lane offset computed once, so the
+// loads take the scalar-base addressing form and a stage costs no per-lane
+// 64-bit address arithmetic. The offsets stay far below 2^32 (rows of the
+// tile times K <= 16384, or 16-byte scale chunks).
 struct GemmSrc {
-    const int8_t *a, *a2, *b0, *b1;
-    const float *sw, *sw2, *sx;
+    uint32_t a, b0, b1, sw, sx;
 };
 template <bool GU, int WM>
-__device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int64_t r0, int64_t t0, int wave, int lane) {
-    const int64_t K = p.k, N = p.n;
+__device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int wave, int lane) {
+    const int K = (int)p.k;
     const int slot = lane & 7, row = 8 * wave + (lane >> 3);
     const int tk0 = 8 * WM * wave + (lane >> 3), tk1 = tk0 + 8;
     GemmSrc g;
-    g.a = p.w_qs + (r0 + row) * K + 16 * (slot ^ swz(row));
-    g.a2 = GU ? p.w2_qs + (r0 + row) * K + 16 * (slot ^ swz(row)) : nullptr;
-    g.b0 = p.xq + (t0 + tk0) * K + 16 * (slot ^ swz(tk0));
-    g.b1 = WM == 2 ? p.xq + (t0 + tk1) * K + 16 * (slot ^ swz(tk1)) : nullptr;
-    g.sw = p.w_ds + (int64_t)wave * N + r0 + 4 * (lane & 7);
-    g.sw2 = GU ? p.w2_ds + (int64_t)wave * N + r0 + 4 * (lane & 7) : nullptr;
-    g.sx = p.xst + (int64_t)wave * p.mp + t0 + 4 * (lane & 15);
+    g.a = (uint32_t)(row * K + 16 * (slot ^ swz(row)));
+    g.b0 = (uint32_t)(tk0 * K + 16 * (slot ^ swz(tk0)));
+    g.b1 = (uint32_t)(tk1 * K + 16 * (slot ^ swz(tk1)));
+    g.sw = (uint32_t)(16 * (lane & 7));
+    g.sx = (uint32_t)(16 * (lane & 15));
     return g;
 }
+__device__ __forceinline__ const void* at(const void* base, uint32_t off) {
+    return (const char*)base + (uint64_t)off;
+}
 
-// Issue the global->LDS loads of one stage (first block kb). A full stage
-// offsets the precomputed pointers; a partial last stage (nblk < 4) re-reads
-// its last valid block in place of the missing ones (values unused).
+// Issue the global->LDS loads of one stage (first block kb) of the tile at
+// rows r0, tokens t0. A partial last stage (nblk < 4) re-reads its last valid
+// block in place of the missing ones (values unused).
 template <bool GU, int WM>
 __device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g, GemmStageLds<GU, WM>& S,
-                                           int64_t kb, int nblk, int wave, int lane) {
+                                           int64_t r0, int64_t t0, int64_t kb, int nblk, int wave, int lane) {
     constexpr int BN = gemm_bn<WM>();
     const int slot = lane & 7;
-    int64_t da = kb * 32, db0 = da, db1 = da, dsw = kb * p.n, dsx = kb * (int64_t)p.mp;
+    uint32_t oa = g.a, ob0 = g.b0, ob1 = g.b1;
+    int jw = wave;  // the scale block row this wave loads
     if (nblk < GK_BLK) {
         // chunk c = slot ^ swz(row) of block c/2; clamp the block, keep the half
+        // (the shift is -32 * (blocks past the end) >= -(the chunk's own offset))
         const int row = 8 * wave + (lane >> 3), tk0 = 8 * WM * wave + (lane >> 3), tk1 = tk0 + 8;
         auto shift = [&](int r) {
             const int c = slot ^ swz(r), blk = c >> 1, cb = blk < nblk ? blk : nblk - 1;
-            return (int64_t)(cb - blk) * 32;
+            return (uint32_t)((cb - blk) * 32);
         };
-        da += shift(row);
-        db0 += shift(tk0);
-        db1 += shift(tk1);
-        const int j = wave < nblk ? wave : nblk - 1;
-        dsw += (int64_t)(j - wave) * p.n;
-        dsx += (int64_t)(j - wave) * p.mp;
+        oa += shift(row);
+        ob0 += shift(tk0);
+        ob1 += shift(tk1);
+        jw = wave < nblk ? wave : nblk - 1;
     }
-    lds_load16(g.a + da, S.a + wave * 1024);
-    if (GU) lds_load16(g.a2 + da, S.a2 + wave * 1024);
-    lds_load16(g.b0 + db0, S.b + (WM * wave) * 1024);
-    if (WM == 2) lds_load16(g.b1 + db1, S.b + (2 * wave + 1) * 1024);
+    const int64_t K = p.k, wa = r0 * K + kb * 32, wb = t0 * K + kb * 32;
+    lds_load16(at(p.w_qs + wa, oa), S.a + wave * 1024);
+    if (GU) lds_load16(at(p.w2_qs + wa, oa), S.a2 + wave * 1024);
+    lds_load16(at(p.xq + wb, ob0), S.b + (WM * wave) * 1024);
+    if (WM == 2) lds_load16(at(p.xq + wb, ob1), S.b + (2 * wave + 1) * 1024);
     if (lane < GBM / 4) {
-        lds_load16(g.sw + dsw, S.sw + wave * GBM);
-        if (GU) lds_load16(g.sw2 + dsw, S.sw2 + wave * GBM);
+        const int64_t ws = r0 + (kb + jw) * p.n;
+        lds_load16(at(p.w_ds + ws, g.sw), S.sw + wave * GBM);
+        if (GU) lds_load16(at(p.w2_ds + ws, g.sw), S.sw2 + wave * GBM);
     }
-    if (lane < BN / 4) lds_load16(g.sx + dsx, S.sx + wave * BN);
+    if (lane < BN / 4) lds_load16(at(p.xst + t0 + (kb + jw) * (int64_t)p.mp, g.sx), S.sx + wave * BN);
 }
+
 
 // Wait until at most `n` vector-memory ops of this wave are outstanding
 // (s_waitcnt vmcnt(n); expcnt and lgkmcnt left at their maxima).
@@ -244,11 +251,11 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
     for (int m = 0; m < WM; m++)
 #pragma unroll
         for (int q = 0; q < 4; q++) f[m][q] = g[m][q] = 0.0f;
-    const GemmSrc src = gemm_src<GU, WM>(a, r0, t0, wave, lane);
+    const GemmSrc src = gemm_src<GU, WM>(a, wave, lane);
     // prologue: stages 0 .. GR-2 in flight
 #pragma unroll
     for (int s = 0; s < GR - 1; s++)
-        if (s < nst) gemm_issue<GU, WM>(a, src, ring[s], (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
+        if (s < nst) gemm_issue<GU, WM>(a, src, ring[s], r0, t0, (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
     // stage s landed for this wave (the stages issued after it may stay in
     // flight), then every wave's loads of stage s landed and stage s-1 is
     // fully consumed; the next stage's loads go out
@@ -259,7 +266,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
         else wait_vm<0>();
         stage_barrier();
         const int64_t sn = s + GR - 1;
-        if (sn < nst) gemm_issue<GU, WM>(a, src, ring[sn % GR], sn * GK_BLK, nblk_of(sn), wave, lane);
+        if (sn < nst) gemm_issue<GU, WM>(a, src, ring[sn % GR], r0, t0, sn * GK_BLK, nblk_of(sn), wave, lane);
     };
     // full stages in a loop with no other path, so the accumulators stay in
     // their registers across iterations; a partial last stage after it

@@ -30,7 +30,7 @@ HBM_PEAK_GBS = 8000.0
 # over this script: FETCH_SIZE 121,105.3 KiB x 2.0 + WRITE_SIZE 593.5 KiB x 1.0,
 # factors from 1 GiB read/copy probe kernels in the same runs
 # (profiles/q8_matvec_lm_head_pmc.md).
-LM_HEAD_TRAFFIC_BYTES = 248_625_130
+LM_HEAD_TRAFFIC_BYTES = 248_624_996
 
 # (name, N rows, K, fused pair)
 SHAPES = [("attn_q/o", 1536, 1536, False), ("attn_k/v", 256, 1536, False),

@@ -1,6 +1,6 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-Headline (BASELINE metric "Q8_0 matvec HBM GB/s (% peak)"): a step is one bs=1
+Headline metric "Q8_0 matvec HBM GB/s (% peak)": a step is one bs=1
 pass of the Q8_0 matvec over the Qwen2.5-1.5B projection shapes
 (N x K) 1536x1536 (q/o), 256x1536 (k/v), 8960x1536 gate+up as one fused
 launch, 1536x8960 (down) and 151936x1536 (lm_head), weights resident in HBM.

@@ -56,7 +56,7 @@ def test_block_dots_bit_exact(gpu, kind, n, m):
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
-def test_q8_matvec_baseline_shapes(gpu, N, K):
+def test_q8_matvec_qwen_shapes(gpu, N, K):
     raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0001 + N, N, K)
     x = uq.synth_normal(0x5EED0001 + K, K)
     w = uq.Weight(uq.KIND_Q8_0, K, N, raw)
@@ -68,7 +68,7 @@ def test_q8_matvec_baseline_shapes(gpu, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151936, 1536)])
-def test_q4k_matvec_baseline_shapes(gpu, N, K):
+def test_q4k_matvec_qwen_shapes(gpu, N, K):
     raw = uq.synth_quant(uq.KIND_Q4_K, 0x5EED0001 + N, N, K)
     x = uq.synth_normal(0x5EED0011 + K, K)
     w = uq.Weight(uq.KIND_Q4_K, K, N, raw)

@@ -74,13 +74,17 @@ int uq_weight_free(uq_weight_t w);
 int64_t uq_weight_bytes(uq_weight_t w);
 
 /* ---------------------------------------------------------------- linears */
-/* Gpu::matvec (llm.rs:246-273): y = W x, x of n floats, y of m floats, host
- * memory, synchronous. Activations are quantized per 32 to int8 (quant_act,
- * gpu_dp4a.cu:23-31) and the dot runs on int8 (linear_dp4a, gpu_dp4a.cu:40-52).
- * Shape rule of llm.rs:248: n % 32 == 0, n <= 16384, m <= 160000 (per kind
- * block size for K-quants). Non-finite x -> UQ_ERR_NONFINITE. */
+/* graph_quant + graph_linear (gpu_graph.rs:70-80) as one host call: y = W x,
+ * x of n floats, y of m floats, host memory, synchronous. x is quantized per
+ * 32 to int8 (quant_act, gpu_dp4a.cu:23-31) and the dot runs on int8
+ * (linear_dp4a, gpu_dp4a.cu:40-52), the decode graph's arithmetic. Q8_0, Q4_K,
+ * Q3_K weights; n % 32 == 0 (K-quants: % 256), n <= 16384, m <= 160000.
+ * Non-finite x -> UQ_ERR_NONFINITE. The reference's Gpu::matvec computes on
+ * fp32 x instead: its drop-in is uq_linear with a Q8_0 weight. */
 int uq_matvec(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m);
-/* Gpu::batch (llm.rs:226-245): 1..3 tensors sharing one input x. */
+/* graph_linear over 1..3 weights sharing one quantized x (the decode graph's
+ * q/k/v and gate/up groups, gpu_graph.rs:137-162), host memory. All-Q8_0
+ * groups run as one job-table launch. */
 int uq_batch(const uq_weight_t* ws, int count, const float* x, int64_t n, float* const* ys, const int64_t* ms);
 
 /* Device forms (graph_quant / graph_linear, gpu_graph.rs:70-80). stream may be
@@ -90,8 +94,9 @@ int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, 
 /* gateup_dp4a (gpu_dp4a.cu:60-64): out[r] = silu(gate_r . x) * (up_r . x). */
 int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream);
 
-/* Gpu::batch as one launch (llm.rs:226-245; frontier_multi_matvec's job table,
- * kernels/frontier_quant.cu:79-93): up to 8 Q8_0 weights of one input length
+/* graph_linear over several weights as one launch (gpu_graph.rs:74-80, in the
+ * job-table form of frontier_multi_matvec, kernels/frontier_quant.cu:79-93):
+ * up to 8 Q8_0 weights of one input length
  * over one quantized x; w2s (may be NULL, entries may be NULL) pairs weight i
  * with an up matrix, ys[i] = silu(gate x) * (up x). Each output equals the
  * single-weight launch's bit for bit. */
@@ -138,11 +143,18 @@ typedef struct {
 /* Weights::linear (frontier_forward.rs:17; frontier_backend.rs:243) over
  * frontier_matvec (frontier_quant.cu:55-63): y = W x, host memory, synchronous.
  * Non-finite input or output -> UQ_ERR_NONFINITE (frontier_backend.rs:222,272);
- * Q3_K/Q4_K weights -> UQ_ERR_QUANT_TYPE. */
+ * Q3_K/Q4_K weights -> UQ_ERR_QUANT_TYPE.
+ * With a Q8_0 weight this is also Gpu::matvec (llm.rs:246-273): matvec_q8 on
+ * fp32 x (llm.rs:294-297), gated against the fp32 dequant dot at abs 0.002
+ * (llm.rs:302-309). Its shape rule (llm.rs:248: typ 8, n % 32 == 0,
+ * n <= 16384, m <= 160000) is the caller's check there and here.
+ * Device staging is one library buffer grown to the largest call so far. */
 int uq_linear(uq_weight_t w, const float* x, int64_t n, float* y, int64_t m);
 /* Weights::batch (frontier_forward.rs:18; frontier_backend.rs:178-224): the jobs
  * (host x and y) in ONE launch, the frontier_multi_matvec of
- * frontier_quant.cu:79-93; bit-identical to uq_linear of each job. */
+ * frontier_quant.cu:79-93; bit-identical to uq_linear of each job.
+ * With 1..3 Q8_0 jobs sharing one x this is Gpu::batch (llm.rs:226-245), whose
+ * prebuilt jobs copy the fp32 matvec_q8 launch (llm.rs:202-214). */
 int uq_linear_batch(const uq_linear_job* jobs, int count);
 /* Device forms on `stream` (NULL: library stream), no synchronization; x must
  * be 16-byte aligned. */

@@ -109,3 +109,80 @@ def test_decode_qwen25_shapes_two_layers(gpu):
         rc, onxt, olg = o.decode(int(toks[pos]), pos, want_logits=True)
         assert rc == 0 and nxt == onxt
         assert ulps(g.logits(), olg).max() <= 1
+
+
+def _replace(tensors, name, raw):
+    kind, n, rows, _ = tensors[name]
+    out = dict(tensors)
+    out[name] = (kind, n, rows, raw)
+    return out
+
+
+@pytest.mark.parametrize("cfg", [SMALL, dict(uq.QWEN25_15B, layers=1, max_seq=64)])
+def test_greedy_tie_takes_lowest_id(gpu, cfg):
+    """Two byte-identical lm_head rows give bit-identical logits; the greedy id
+    is the lower of the two (gpu_greedy.cu:1-27, gpu_graph.rs:14-23), whether
+    the twin row sits in the same argmax workgroup or in another one."""
+    t = uq.synth_qwen2(cfg, 41)
+    o = O.Model(cfg, {k: v[3] for k, v in t.items()})
+    rc, a, olg = o.decode(5, 0, want_logits=True)
+    assert rc == 0 and (olg == olg[a]).sum() == 1          # a unique maximum to start from
+    rb = cfg["dim"] // 32 * 34
+    vocab = cfg["vocab"]
+    for b in sorted({a - 1, a + 1, 0, vocab - 1} - {a}):
+        if not 0 <= b < vocab:
+            continue
+        raw = t["output.weight"][3].copy()
+        raw[b * rb:(b + 1) * rb] = raw[a * rb:(a + 1) * rb]
+        t2 = _replace(t, "output.weight", raw)
+        g = uq.Qwen2Model(cfg, t2)
+        try:
+            nxt = g.decode_step(5, 0)
+            lg = g.logits()
+            assert lg[a].view(np.uint32) == lg[b].view(np.uint32)
+            assert nxt == min(a, b), (a, b, nxt)
+            o2 = O.Model(cfg, {k: v[3] for k, v in t2.items()})
+            assert o2.decode(5, 0)[1] == min(a, b)
+            # the tie survives into the device-fed loop: the second step starts from min(a, b)
+            ids, _ = g.decode_run(5, 0, 2)
+            assert ids[0] == min(a, b) and ids[1] == o2.decode(min(a, b), 1)[1]
+        finally:
+            g.free()
+
+
+def test_nonfinite_logit_fails_the_step(gpu):
+    """One fp16 NaN (then +inf) scale in one lm_head row: that logit is
+    non-finite and every greedy entry point returns UQ_ERR_NONFINITE (the bad
+    flag of gpu_greedy.cu:1-27). An infinite output-norm weight makes one
+    activation infinite: its block quantizes to codes 0 with scale inf, and
+    0 * inf makes every logit NaN. The run still fails with NONFINITE, and the
+    id fed back on the device between steps stays inside the vocabulary."""
+    t = uq.synth_qwen2(SMALL, 43)
+    rb = SMALL["dim"] // 32 * 34
+    toks = uq.synth_tokens(43, 9, SMALL["vocab"])
+    for scale in (b"\x00\x7e", b"\x00\x7c"):          # fp16 0x7E00 NaN, 0x7C00 +inf (little endian)
+        raw = t["output.weight"][3].copy()
+        row = 123
+        raw[row * rb + 34 * 2:row * rb + 34 * 2 + 2] = np.frombuffer(scale, np.uint8)   # block 2 of row 123
+        g = uq.Qwen2Model(SMALL, _replace(t, "output.weight", raw))
+        try:
+            for call in (lambda: g.decode_step(5, 0), lambda: g.decode_run(5, 0, 3), lambda: g.prefill(toks)):
+                with pytest.raises(uq.UqError) as e:
+                    call()
+                assert e.value.status == uq.Error.NONFINITE
+            assert not np.isfinite(g.logits()[row])
+        finally:
+            g.free()
+    gamma = t["output_norm.weight"][3].copy()
+    gamma[7] = np.inf
+    g = uq.Qwen2Model(SMALL, _replace(t, "output_norm.weight", gamma))
+    try:
+        with pytest.raises(uq.UqError) as e:
+            g.decode_run(5, 0, 4)
+        assert e.value.status == uq.Error.NONFINITE
+        assert np.isnan(g.logits()).all()
+        with pytest.raises(uq.UqError) as e:
+            g.decode_step(5, 4)
+        assert e.value.status == uq.Error.NONFINITE
+    finally:
+        g.free()

@@ -97,13 +97,18 @@ def test_q8_matvec_ragged_shapes(gpu, m, n):
     assert ulps(uq.matvec(w, x), O.matvec(O.Q8_0, raw, n, m, x)).max() <= 1
 
 
-def test_gateup_fused_silu(gpu):
+# the fused gate/up pair: Q8_0 and Q4_K at the Qwen2.5-1.5B FFN (2 x 8960 x
+# 1536), Q3_K at the MoE expert FFN (2 x 768 x 2048), plus ragged row counts
+# that leave a partial row block in the last workgroup
+@pytest.mark.parametrize("kind,N,K", [(uq.KIND_Q8_0, 8960, 1536), (uq.KIND_Q4_K, 8960, 1536),
+                                      (uq.KIND_Q3_K, 768, 2048), (uq.KIND_Q4_K, 37, 512),
+                                      (uq.KIND_Q3_K, 45, 768)])
+def test_gateup_fused_silu(gpu, kind, N, K):
     import ctypes
-    N, K = 8960, 1536
-    rg = uq.synth_quant(uq.KIND_Q8_0, 71, N, K)
-    ru = uq.synth_quant(uq.KIND_Q8_0, 72, N, K)
-    x = uq.synth_normal(73, K)
-    wg, wu = uq.Weight(uq.KIND_Q8_0, K, N, rg), uq.Weight(uq.KIND_Q8_0, K, N, ru)
+    rg = uq.synth_quant(kind, 71 + N, N, K)
+    ru = uq.synth_quant(kind, 72 + N, N, K)
+    x = uq.synth_normal(73 + K, K)
+    wg, wu = uq.Weight(kind, K, N, rg), uq.Weight(kind, K, N, ru)
     L = uq.lib()
     buf = {}
     for name, size in (("x", 4 * K), ("xq", K), ("xs", 4 * K // 32), ("out", 4 * N)):
@@ -119,13 +124,15 @@ def test_gateup_fused_silu(gpu):
     finally:
         for p in buf.values():
             L.uq_dev_free(p)
-    g = O.matvec(O.Q8_0, rg, K, N, x)
-    u = O.matvec(O.Q8_0, ru, K, N, x)
+    g = O.matvec(kind, rg, K, N, x)
+    u = O.matvec(kind, ru, K, N, x)
     ref = np.array([O.silu_mul(float(a), float(b)) for a, b in zip(g, u)], np.float32)
     assert ulps(out, ref).max() <= 1
 
 
 def test_batch_and_reference_surface(gpu):
+    """Gpu::batch / Gpu::matvec (llm.rs:226-273) run matvec_q8 on fp32 x: the
+    fp32-activation reader with Q8_0 weights, exact double sum per row."""
     K = 1536
     raws = [uq.synth_quant(uq.KIND_Q8_0, 90 + i, m, K) for i, m in enumerate((1536, 256, 256))]
     ts = [uq.Tensor("blk.0.attn_%s.weight" % s, K, m, uq.KIND_Q8_0, r)
@@ -137,7 +144,7 @@ def test_batch_and_reference_surface(gpu):
     ys = [np.zeros(t.m, np.float32) for t in ts]
     assert g.batch(ts, x, ys)
     for t, y, r in zip(ts, ys, raws):
-        assert ulps(y, O.matvec(O.Q8_0, r, K, t.m, x)).max() <= 1
+        assert ulps(y, O.linear(O.Q8_0, r, K, t.m, x)).max() <= 1
     y1 = np.zeros(1536, np.float32)
     assert g.matvec(ts[0], x, y1) and np.array_equal(y1, ys[0])
     # failure modes return False like the reference (llm.rs:227,248)
@@ -147,6 +154,32 @@ def test_batch_and_reference_surface(gpu):
     bad = x.copy()
     bad[5] = np.nan
     assert not g.matvec(ts[0], bad, y1) and "NONFINITE" in g.last_error
+
+
+def test_reference_matvec_gate(gpu):
+    """The reference's Gpu::matvec gate (llm.rs:301-309) restated through the C
+    ABI: blk.0.attn_q.weight (1536 x 1536 Q8_0), x[i] = ((i % 17) - 8) / 16,
+    rows 0, 1, 17, 127, DIM-1 against the f32 sequential dequant dot, abs error
+    < 0.002, every output finite. The int8-activation form (uq_matvec) is not
+    this call: it misses the gate by ~0.07 on these rows."""
+    K = N = 1536
+    raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0001, N, K)
+    t = uq.Tensor("blk.0.attn_q.weight", K, N, uq.KIND_Q8_0, raw)
+    g = uq.Gpu(0)
+    g.upload(t)
+    x = ((np.arange(K) % 17).astype(np.float32) - np.float32(8.0)) / np.float32(16.0)
+    y = np.zeros(N, np.float32)
+    assert g.matvec(t, x, y)
+    expect = O.q8_dequant_dot(raw, K, N, x)
+    rows = [0, 1, 17, 127, N - 1]
+    err = np.abs(y[rows] - expect[rows])
+    assert np.isfinite(y).all() and err.max() < 0.002, err
+    # the whole output sits within 1 ulp of the exact sum as well
+    assert ulps(y, O.linear(O.Q8_0, raw, K, N, x)).max() <= 1
+    # the shape rule of llm.rs:248 returns False as there
+    k4 = uq.Tensor("k4", 256, 1, uq.KIND_Q4_K, uq.synth_quant(uq.KIND_Q4_K, 3, 1, 256))
+    g.upload(k4)
+    assert not g.matvec(k4, np.zeros(256, np.float32), np.zeros(1, np.float32))   # typ != 8
 
 
 def test_upload_rejects_bad_shapes(gpu):

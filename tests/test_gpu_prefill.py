@@ -60,6 +60,23 @@ def test_prefill_matches_oracle(gpu, n):
         assert np.array_equal(k, o.keys(layer, n)) and np.array_equal(v, o.values(layer, n))
 
 
+# KV capacities that are not a multiple of the 64-token GEMM tile: the prompt
+# fills the cache to its last position, so every attention key read must stay
+# inside [0, n) of the allocation
+@pytest.mark.parametrize("max_seq,n", [(100, 100), (97, 97), (97, 50), (65, 65)])
+def test_prefill_kv_capacity_not_tile_multiple(gpu, max_seq, n):
+    cfg = dict(SMALL, max_seq=max_seq)
+    g, o = build(cfg, 57)
+    toks = uq.synth_tokens(57 + n, n, cfg["vocab"])
+    nxt = g.prefill(toks)
+    rc, onxt, olg = o.prefill(toks, want_logits=True)
+    assert rc == 0 and nxt == onxt
+    assert ulps(g.logits(), olg).max() <= 1
+    for layer in range(cfg["layers"]):
+        k, v = g.kv(layer, n)
+        assert np.array_equal(k, o.keys(layer, n)) and np.array_equal(v, o.values(layer, n))
+
+
 def test_prefill_then_decode(gpu):
     g, o = build(SMALL, 33)
     toks = uq.synth_tokens(33, 50, SMALL["vocab"])

@@ -387,3 +387,92 @@ def test_moe_route_vs_stable_sort():
         assert abs(float(w.astype(np.float64).sum()) - 1) < 1e-6
     _, ids, _ = O.moe_route(np.zeros(128, np.float32), 8)
     assert list(ids) == list(range(8))
+
+
+# ---------------------------------------------------------------- byte-literal K-quant known answers
+# Literal superblocks written from ggml's published block structs and
+# dequantize_row_q4_K / dequantize_row_q3_K (ggml-quants.c), independent of
+# tests/ggml_layouts.py. Expected values are listed as 2*w (integers).
+#
+# Q4_K (block_q4_K: fp16 d, fp16 dmin, scales[12], qs[128]): d = 1.0, dmin =
+# 0.5; 6-bit (scale, min) of the eight 32-value sub-blocks
+# (3,9) (11,2) (7,12) (14,5) (17,44) (38,58) (53,6) (61,27): for j >= 4 the
+# scale's high two bits sit in scales[j-4] >> 6 and the min's in scales[j] >> 6,
+# and the two differ for every such j. qs[32k + l] holds sub-block 2k in its
+# low nibble and 2k+1 in its high nibble; w = d*sc*q - dmin*m. The bytes are
+# chosen so that swapping the two high-bit fields changes 128 of the 256
+# values, and reading a byte's two nibbles as consecutive values changes 236.
+Q4K_BLOCK = bytes.fromhex(
+    "003c0038438bc7ce89c20c45c1a665bd00871e952ca33ab148cf56dd64eb72f9"
+    "81089f16ad24bb32c940d75ee56cf37a35bc43ca51d86fe67df48b029910a72e"
+    "b63dc44bd259e067fe750c831a9128af6ae178ff860d941ba229b037ce45dc53"
+    "eb62f970078e159c23aa31b84fc65dd49f16ad24bb32c940d75ee56cf37a0188"
+    "10972ea53cb34ac158df66ed74fb8209"
+)
+Q4K_2W = [
+    -9, 33, 75, 21, 63, 9, 51, -3, 39, 81, 27, 69, 15, 57, 3, 45,
+    -3, 39, 81, 27, 69, 15, 57, 3, 45, -9, 33, 75, 21, 63, 9, 51,
+    -2, 174, 20, 196, 42, 218, 64, 240, 86, 262, 108, 284, 130, 306, 152, 328,
+    174, -2, 196, 20, 218, 42, 240, 64, 262, 86, 284, 108, 306, 130, 328, 152,
+    58, 156, 30, 128, 2, 100, 198, 72, 170, 44, 142, 16, 114, -12, 86, 184,
+    72, 170, 44, 142, 16, 114, -12, 86, 184, 58, 156, 30, 128, 2, 100, 198,
+    79, 303, 107, 331, 135, 359, 163, 387, 191, 415, 219, -5, 247, 23, 275, 51,
+    303, 79, 331, 107, 359, 135, 387, 163, 415, 191, -5, 219, 23, 247, 51, 275,
+    296, -10, 228, 466, 160, 398, 92, 330, 24, 262, -44, 194, 432, 126, 364, 58,
+    330, 24, 262, -44, 194, 432, 126, 364, 58, 296, -10, 228, 466, 160, 398, 92,
+    398, 1006, 474, 1082, 550, -58, 626, 18, 702, 94, 778, 170, 854, 246, 930, 322,
+    1006, 398, 1082, 474, -58, 550, 18, 626, 94, 702, 170, 778, 246, 854, 322, 930,
+    1584, 630, 1372, 418, 1160, 206, 948, -6, 736, 1478, 524, 1266, 312, 1054, 100, 842,
+    -6, 736, 1478, 524, 1266, 312, 1054, 100, 842, 1584, 630, 1372, 418, 1160, 206, 948,
+    1071, 95, 1193, 217, 1315, 339, 1437, 461, 1559, 583, 1681, 705, 1803, 827, -27, 949,
+    95, 1071, 217, 1193, 339, 1315, 461, 1437, 583, 1559, 705, 1681, 827, 1803, 949, -27,
+]
+
+# Q3_K (block_q3_K: hmask[32], qs[64], scales[12], fp16 d): d = 0.5; the 16
+# 6-bit scales 5 37 22 60 0 49 18 33 63 12 41 26 54 3 30 47 (value - 32 on
+# decode), low four bits in scales[s] (s < 8) or scales[s-8] >> 4, high two
+# bits in scales[8 + s%4] >> 2*(s/4). Value 128c + 32j + 16h + l reads bits
+# 2j of qs[32c + 16h + l] and bit 4c+j of hmask[16h + l]; a clear hmask bit
+# subtracts 4. The bytes are chosen so that an inverted hmask test changes
+# all 256 values, taking the high bits from scales[8 + s/4] >> 2*(s%4)
+# changes 112, and exchanging j and h for j < 2 changes 64.
+Q3K_BLOCK = bytes.fromhex(
+    "aa56a56a55a95a9595aa56a56a55a95a5a95aa56a56a55a9a95a95aa56a56a55"
+    "500ffaa5500ffaa5a5500ffaa5500ffafaa5500ffaa5500f0ffaa5500ffaa550"
+    "faa5500ffaa5500f0ffaa5500ffaa550500ffaa5500ffaa5a5500ffaa5500ffa"
+    "f5c596ac6031e2f1f00e659b0038"
+)
+Q3K_2W = [
+    108, 27, -54, 81, 0, -81, 54, -27, -27, 108, 27, -54, 81, 0, -81, 54,
+    -10, 5, -20, -5, 10, -15, 0, 15, 15, -10, 5, -20, -5, 10, -15, 0,
+    0, -30, 20, -10, 40, 10, -20, 30, 30, 0, -30, 20, -10, 40, 10, -20,
+    56, -84, 0, 84, -56, 28, -112, -28, -28, 56, -84, 0, 84, -56, 28, -112,
+    96, 0, -96, 64, -32, 128, 32, -64, -64, 96, 0, -96, 64, -32, 128, 32,
+    -17, 34, -51, 0, 51, -34, 17, -68, -68, -17, 34, -51, 0, 51, -34, 17,
+    -14, 56, 14, -28, 42, 0, -42, 28, 28, -14, 56, 14, -28, 42, 0, -42,
+    3, -2, 1, -4, -1, 2, -3, 0, 0, 3, -2, 1, -4, -1, 2, -3,
+    -62, 31, -124, -31, 62, -93, 0, 93, 93, -62, 31, -124, -31, 62, -93, 0,
+    0, -60, 40, -20, 80, 20, -40, 60, 60, 0, -60, 40, -20, 80, 20, -40,
+    18, -27, 0, 27, -18, 9, -36, -9, -9, 18, -27, 0, 27, -18, 9, -36,
+    24, 6, -12, 18, 0, -18, 12, -6, -6, 24, 6, -12, 18, 0, -18, 12,
+    -22, 44, -66, 0, 66, -44, 22, -88, -88, -22, 44, -66, 0, 66, -44, 22,
+    -29, 116, 29, -58, 87, 0, -87, 58, 58, -29, 116, 29, -58, 87, 0, -87,
+    -6, 4, -2, 8, 2, -4, 6, 0, 0, -6, 4, -2, 8, 2, -4, 6,
+    -45, 0, 45, -30, 15, -60, -15, 30, 30, -45, 0, 45, -30, 15, -60, -15,
+]
+
+
+@pytest.mark.parametrize("kind,block,twice", [(O.Q4_K, Q4K_BLOCK, Q4K_2W), (O.Q3_K, Q3K_BLOCK, Q3K_2W)])
+def test_kquant_byte_literal_known_answers(kind, block, twice):
+    raw = np.frombuffer(block, np.uint8)
+    assert raw.size == O.row_bytes(kind, 256)
+    exp = (np.array(twice, np.float64) / 2).astype(np.float32)
+    assert np.array_equal(O.dequantize(kind, raw, 256), exp)
+    # the integer path sees the same codes: one-hot activations pick each value
+    qx = np.zeros(256, np.int8)
+    xs = np.ones(8, np.float32)
+    for i in (0, 17, 31, 32, 63, 100, 127, 128, 200, 255):
+        qx[:] = 0
+        qx[i] = 1
+        y = O.matvec_q(kind, raw, 256, 1, xs, qx)
+        assert y[0] == exp[i], (i, y[0], exp[i])

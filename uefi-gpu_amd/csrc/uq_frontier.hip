@@ -937,19 +937,18 @@ int uq_dequantize(uint32_t kind, const void* bytes, size_t nbytes, int64_t n, fl
     if (rb < 0) return set_error(ERR_SHAPE, "dequantize: n is not a whole number of blocks");
     if ((int64_t)nbytes != rb) return set_error(ERR_SHAPE, "dequantize: byte count != row_bytes(kind, n)");
     hipStream_t s = (hipStream_t)uq_stream();
-    uint8_t* din = nullptr;
-    float* dout = nullptr;
-    UQ_CHECK_HIP(hipMalloc(&din, (size_t)rb));
-    hipError_t e = hipMalloc(&dout, sizeof(float) * (size_t)n);
-    if (e == hipSuccess) e = hipMemcpyAsync(din, bytes, (size_t)rb, hipMemcpyHostToDevice, s);
+    const size_t in_bytes = ((size_t)rb + 255) & ~(size_t)255;
+    void* stage = nullptr;
+    if (int rc = staging_buffer(in_bytes + sizeof(float) * (size_t)n, &stage)) return rc;
+    uint8_t* const din = (uint8_t*)stage;
+    float* const dout = (float*)((char*)stage + in_bytes);
+    hipError_t e = hipMemcpyAsync(din, bytes, (size_t)rb, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) {
         hipLaunchKernelGGL(k_dequant, dim3(grid_blocks(n)), dim3(FWG), 0, s, din, dout, kind, n);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipMemcpyAsync(out, dout, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    (void)hipFree(din);
-    if (dout) (void)hipFree(dout);
     if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("dequantize: ") + hipGetErrorString(e));
     return OK;
 }
@@ -977,9 +976,12 @@ int uq_linear_batch(const uq_linear_job* jobs, int count) {
     for (int i = 0; i < count; i++)
         if (int rc = check_finite(jobs[i].x, jobs[i].weight->w.n, "linear_batch: input")) return rc;
     hipStream_t s = (hipStream_t)uq_stream();
-    float *dx = nullptr, *dy = nullptr;
-    UQ_CHECK_HIP(hipMalloc(&dx, sizeof(float) * (size_t)xs));
-    hipError_t e = hipMalloc(&dy, sizeof(float) * (size_t)ys);
+    const size_t x_bytes = (sizeof(float) * (size_t)xs + 255) & ~(size_t)255;
+    void* stage = nullptr;
+    if (int rc = staging_buffer(x_bytes + sizeof(float) * (size_t)ys, &stage)) return rc;
+    float* const dx = (float*)stage;
+    float* const dy = (float*)((char*)stage + x_bytes);
+    hipError_t e = hipSuccess;
     int rc = OK;
     std::vector<uq_linear_job> dj((size_t)count);
     std::vector<float> host((size_t)ys);
@@ -994,9 +996,8 @@ int uq_linear_batch(const uq_linear_job* jobs, int count) {
     if (e == hipSuccess) rc = enqueue_jobs(dj.data(), count, s);
     if (e == hipSuccess && rc == OK)
         e = hipMemcpyAsync(host.data(), dy, sizeof(float) * (size_t)ys, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess && rc == OK) e = hipStreamSynchronize(s);
-    (void)hipFree(dx);
-    if (dy) (void)hipFree(dy);
+    // a failed enqueue still leaves the copies above reading the staging buffer
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("linear_batch: ") + hipGetErrorString(e));
     if (rc != OK) return rc;
     yo = 0;

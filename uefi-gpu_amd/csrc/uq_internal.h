@@ -62,6 +62,11 @@ struct Weight {
 // Compute units of the current device (queried once).
 int cu_count();
 
+// Device staging of the host-pointer fp32 calls: one buffer per context,
+// grown on demand and never shrunk, so repeated calls of the same sizes
+// allocate nothing. Valid until the next call that asks for more bytes.
+int staging_buffer(size_t bytes, void** out);
+
 int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t bytes, Weight& out, bool bank);
 
 // Split of one GGUF block of a frontier kind into three planes (body, aux,

@@ -396,7 +396,7 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
         launch_pf_rope_kv(ra, n, s);
         // head_dim 128: the attention epilogue quantizes its output for the o GEMM
         const bool fused_quant = c.head_dim == 128;
-        PfAttnArgs aa{PY, nqkv, kcache + l * kvl, vcache + l * kvl, PATT, n, 0, pcap, c.heads, c.kv_heads, c.head_dim,
+        PfAttnArgs aa{PY, nqkv, kcache + l * kvl, vcache + l * kvl, PATT, n, 0, c.max_seq, c.heads, c.kv_heads, c.head_dim,
                       (float)(1.0 / std::sqrt((double)c.head_dim)), fused_quant ? PXQ : nullptr,
                       fused_quant ? PXST : nullptr, mp};
         if (launch_pf_attention(aa, s)) return fail(ERR_SHAPE, "prefill: attention head_dim unsupported");

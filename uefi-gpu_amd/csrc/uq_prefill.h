@@ -51,7 +51,7 @@ struct PfAttnArgs {
     const uint16_t* kcache;
     const uint16_t* vcache;
     float* out;              // [n][heads*hd]
-    int n, p0, kcap;         // queries, first position, key capacity (>= p0 + n)
+    int n, p0, kcap;         // queries, first position, positions allocated in the caches (>= p0 + n)
     int heads, kv_heads, head_dim;
     float qscale;
     // head_dim 128 only, instead of out: the output quantized per 32 dims

@@ -414,8 +414,10 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
     // loaded before the current tile's MFMAs
     const int ntile = (kend + 15) >> 4;
     auto load_k = [&](int kt, uint32_t* kw) {
+        // keys past the tile's causal end are read from key kend-1 (written,
+        // in bounds) and their scores are never used
         int key = kt * 16 + c;
-        key = key < a.kcap ? key : a.kcap - 1;
+        key = key < kend ? key : kend - 1;
         const uint16_t* kr = a.kcache + (size_t)key * kvd + kh * HD + g * DG;
 #pragma unroll
         for (int i = 0; i < DG / 8; i++) {
@@ -513,7 +515,7 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
         for (int u = 0; u < SU; u++) {
             const int kk = k0 + 4 * u + g;
             const int kl = kk < kpad ? kk : kpad - 1;
-            const int kv = kl < a.kcap ? kl : a.kcap - 1;
+            const int kv = kl < kend ? kl : kend - 1;  // p is 0 there
             bt.p[u] = kk < kpad ? (double)pr[kl] : 0.0;
 #pragma unroll
             for (int j = 0; j < DT; j++) bt.v[u][j] = vb[(size_t)kv * kvd + j * 16];

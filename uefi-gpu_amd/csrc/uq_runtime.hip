@@ -30,6 +30,10 @@ struct Context {
     float* dy = nullptr;
     size_t y_cap = 0;
     unsigned* dcount = nullptr;
+    // staging of the fp32-activation host calls (uq_linear*, uq_dequantize):
+    // grown on demand, never shrunk
+    void* stage = nullptr;
+    size_t stage_cap = 0;
 };
 Context g_ctx;
 
@@ -76,6 +80,23 @@ static int ensure_y(size_t m) {
 
 static hipStream_t pick(void* s) { return s ? (hipStream_t)s : g_ctx.stream; }
 
+int staging_buffer(size_t bytes, void** out) {
+    if (!g_ctx.ready) return set_error(ERR_ARG, "uq_init has not been called");
+    if (bytes > g_ctx.stage_cap) {
+        // the previous buffer may still be read by enqueued copies
+        size_t cap = std::max(bytes, 2 * g_ctx.stage_cap);
+        cap = (cap + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+        UQ_CHECK_HIP(hipStreamSynchronize(g_ctx.stream));
+        if (g_ctx.stage) UQ_CHECK_HIP(hipFree(g_ctx.stage));
+        g_ctx.stage = nullptr;
+        g_ctx.stage_cap = 0;
+        UQ_CHECK_HIP(hipMalloc(&g_ctx.stage, cap));
+        g_ctx.stage_cap = cap;
+    }
+    *out = g_ctx.stage;
+    return OK;
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 }  // namespace uq
@@ -113,6 +134,7 @@ int uq_shutdown(void) {
     hipFree(g_ctx.dxs);
     hipFree(g_ctx.dy);
     hipFree(g_ctx.dcount);
+    if (g_ctx.stage) hipFree(g_ctx.stage);
     hipStreamDestroy(g_ctx.stream);
     g_ctx = Context{};
     return OK;

@@ -491,6 +491,9 @@ __global__ __launch_bounds__(256) void k_greedy_finish(LmArgs a, int parts) {
     }
     cand_reduce(best, id, bad, vs, ids, bs);
     if (threadIdx.x == 0) {
+        // no candidate (every logit NaN): the flag fails the call, and the id
+        // fed to the next step's embedding row must still lie in the vocabulary
+        if (id < 0 || (int64_t)id >= a.rows) id = 0;
         a.result[0] = (uint32_t)id;
         a.result[1] = bad;
         a.result[2] |= bad;

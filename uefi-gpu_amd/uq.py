@@ -367,8 +367,11 @@ class Tensor:
 class Gpu:
     """The reference's linear call surface (llm.rs:226-273) over libuq.
 
-    ``matvec``/``batch`` return False on any failure, as the reference does;
-    ``last_error`` keeps the message.
+    ``matvec``/``batch`` run matvec_q8 on fp32 x (llm.rs:294-297; the jobs of
+    ``batch`` copy that launch, llm.rs:202-214), so they map to the
+    fp32-activation reader, ``uq_linear_batch`` with Q8_0 weights. They return
+    False on any failure, as the reference does, including its shape rule
+    (llm.rs:248); ``last_error`` keeps the message.
     """
 
     def __init__(self, device=0):
@@ -387,9 +390,11 @@ class Gpu:
             return False
         try:
             for t, y in zip(tensors, ys):
-                if t.n != len(x) or t.m != len(y):
+                if (t.typ != KIND_Q8_0 or t.n != len(x) or t.m != len(y) or t.n % 32 or t.n > 16384
+                        or t.m > 160000):
                     return False
-            outs = batch([self.weights[t.name] for t in tensors], x)
+            x = np.ascontiguousarray(x, dtype=np.float32)
+            outs = linear_batch([(self.weights[t.name], x) for t in tensors])
         except (UqError, KeyError) as e:
             self.last_error = str(e)
             return False

@@ -91,6 +91,16 @@ int uq_batch(const uq_weight_t* ws, int count, const float* x, int64_t n, float*
  * NULL for the library stream. xq: n int8, xs: n/32 floats. */
 int uq_quant_act_dev(const float* x, int64_t n, int8_t* xq, float* xs, void* stream);
 int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, void* stream);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): uq_matvec on device pointers, x (n floats) -> y (m
+ * floats) on `stream` (NULL: library stream), without synchronizing. The
+ * quantized activation goes to a static device scratch of the library
+ * (n <= 16384, else UQ_ERR_SHAPE); the call allocates and frees nothing. Every
+ * call on one GPU shares that scratch: calls that overlap on one GPU (other
+ * streams, other threads) race. Output equals uq_matvec's bit for bit; x is
+ * not checked for non-finite values. */
+int uq_matvec_static(uq_weight_t w, const float* x, float* y, void* stream);
 /* gateup_dp4a (gpu_dp4a.cu:60-64): out[r] = silu(gate_r . x) * (up_r . x). */
 int uq_gateup_q_dev(uq_weight_t gate, uq_weight_t up, const int8_t* xq, const float* xs, float* out, void* stream);
 

@@ -14,10 +14,22 @@
 #include <mutex>
 #include <vector>
 
+// Scratch of uq_matvec_static: one call's quantized activation, the int8
+// codes of up to STATIC_MAX_N values followed by their f32 block scales. A
+// file-scope device array, so that call allocates nothing; every device the
+// library runs on holds its own copy until the process ends. Host code never
+// uses the array's name as an address: uq_init looks up the device address
+// (hipGetSymbolAddress) and keeps it per device.
+#define UQ_STATIC_MAX_N 16384
+static __device__ __align__(256) int8_t scratch[UQ_STATIC_MAX_N + UQ_STATIC_MAX_N / 32 * 4];
+
 namespace uq {
 
 namespace {
 thread_local std::string g_error;
+
+constexpr int MAX_DEVICES = 64;
+void* g_scratch[MAX_DEVICES];  // device address of `scratch` per device, set by uq_init
 
 struct Context {
     bool ready = false;
@@ -116,6 +128,12 @@ int uq_init(int device) {
     UQ_CHECK_HIP(hipGetDeviceCount(&count));
     if (device < 0 || device >= count) return set_error(ERR_ARG, "uq_init: no such device");
     UQ_CHECK_HIP(hipSetDevice(device));
+    if (device < MAX_DEVICES && !g_scratch[device]) {
+        void* p = nullptr;
+        UQ_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(ERR_DEVICE, "uq_init: no device address for the static scratch");
+        g_scratch[device] = p;
+    }
     UQ_CHECK_HIP(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
     UQ_CHECK_HIP(hipMalloc(&g_ctx.dx, sizeof(float) * MAX_N));
     UQ_CHECK_HIP(hipMalloc(&g_ctx.dxq, MAX_N));
@@ -325,6 +343,28 @@ int uq_matvec_q_dev(uq_weight_t w, const int8_t* xq, const float* xs, float* y, 
     if (int rc = require_ctx()) return rc;
     if (!w || !xq || !xs || !y) return set_error(ERR_ARG, "matvec_q_dev: null pointer");
     if (int rc = launch_matvec(w->w, nullptr, xq, xs, y, pick(stream))) return rc;
+    UQ_CHECK_HIP(hipGetLastError());
+    return OK;
+}
+
+int uq_matvec_static(uq_weight_t w, const float* x, float* y, void* stream) {
+    if (int rc = require_ctx()) return rc;
+    if (!w || !x || !y) return set_error(ERR_ARG, "matvec_static: null pointer");
+    const Weight& W = w->w;
+    if (W.kind != KIND_Q8_0 && W.kind != KIND_Q4_K && W.kind != KIND_Q3_K)
+        return set_error(ERR_QUANT_TYPE, "matvec_static: Q8_0, Q4_K or Q3_K weights only");
+    if (W.n > UQ_STATIC_MAX_N)
+        return set_error(ERR_SHAPE, "matvec_static: n exceeds the static scratch (16384 values)");
+    void* const p = g_ctx.device < MAX_DEVICES ? g_scratch[g_ctx.device] : nullptr;
+    if (!p) return set_error(ERR_DEVICE, "matvec_static: no static scratch on this device");
+    int8_t* const xq = (int8_t*)p;
+    float* const xs = (float*)((int8_t*)p + UQ_STATIC_MAX_N);
+    const hipStream_t s = pick(stream);
+    // every code and scale the matvec reads is written by this quantization
+    // first, so the scratch needs no clearing
+    launch_quant_act(x, W.n, xq, xs, s);
+    UQ_CHECK_HIP(hipGetLastError());
+    if (int rc = launch_matvec(W, nullptr, xq, xs, y, s)) return rc;
     UQ_CHECK_HIP(hipGetLastError());
     return OK;
 }

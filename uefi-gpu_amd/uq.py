@@ -68,6 +68,7 @@ _SIGS = {
     "uq_batch": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _c_f32p, _i64, ctypes.POINTER(_c_f32p), _c_i64p]),
     "uq_quant_act_dev": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "uq_matvec_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "uq_matvec_static": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
     "uq_gateup_q_dev": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "uq_matvec_table_dev": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.c_int, _vp, _vp,
                                            ctypes.POINTER(_vp), _vp]),

@@ -19,10 +19,12 @@
  *   block dots (Q8_0)   int64 numpy brute force
  *   uqo_matvec (Q8_0)   vs float64 exact sum and vs the literal f32 form of
  *                       gpu_prefill.rs:116 (<=1e-3 rel), vs llm.rs:302-309
- *   Q4_K / Q3_K         PARITY UNPINNED vs the reference (formats absent from
- *                       it, frontier_core.rs:53-58); pinned by hand-worked
- *                       known-answer blocks, integer path == dequant path,
- *                       encode/decode round trips of the ggml layouts
+ *   Q4_K / Q3_K         formats absent from the reference (frontier_core.rs:
+ *                       53-58); pinned against ggml's published block structs
+ *                       and dequantize_row_q4_K/_q3_K by byte-literal
+ *                       superblocks with their expected values written out,
+ *                       hand-worked known-answer blocks, integer path ==
+ *                       dequant path, encode/decode round trips of the layouts
  *   dequantize, kinds   hand-worked known-answer blocks per kind (code book
  *   BF16/Q6_K/IQ3_XXS/  and grid entries, sign parity, scale composition and
  *   IQ4_NL/IQ4_XS       f32 multiply order), fp16-scale linearity, the IQ3
@@ -106,7 +108,9 @@ uint16_t uqo_f16_rne(float f) {
  *   hi = x - k*ln2_hi (exact), lo = k*ln2_lo, r = hi - lo,
  *   c = r - r^2 (P1 + r^2 P2),  y = 1 + (r c / (2 - c) - lo + hi),
  *   result = y * 2^k (scalbnf steps for k outside the normal exponent range).
- * The kernels evaluate the same f32 operations (uq_device.h). */
+ * The kernels evaluate the same f32 operations (uq_device.h). Algorithm:
+ * Copyright (C) 1993 by Sun Microsystems, Inc.; notice kept in
+ * third_party/NOTICE.sunpro-expf. */
 static float scalbnf_steps(float y, int k) {
     if (k > 127) {
         y = y * 0x1p127f; k -= 127;
@@ -201,7 +205,8 @@ static inline int q4k_value(int i, const uint8_t* blk) {
 
 /* driver/src/frontier_core.rs:73-106 form (one value at a time, ggml's scale
  * multiplication order), for F32, Q8_0 and the Q4_K/Q3_K layouts. */
-/* The IQ4_NL/IQ4_XS code book (frontier_core.rs:67) and the IQ3_XXS grid
+/* ggml data (MIT licence, third_party/LICENSE.ggml).
+ * The IQ4_NL/IQ4_XS code book (frontier_core.rs:67) and the IQ3_XXS grid
  * (frontier_tables.rs:2-35, ggml's iq3xxs_grid). The grid is held here in a
  * different encoding than the product's: entry i as four 3-bit digits (lowest
  * byte first) into the eight byte levels below, expanded by uqo_iq3_grid();

@@ -52,6 +52,8 @@ UQ_DEV float uq_scalbnf_steps(float y, int k) {
 // expf of the reference's Rust path: libm 0.2.16 (FreeBSD e_expf.c), as
 // restated at driver/src/frontier_cpu_expf.rs:80-170. Same f32 operations as
 // the oracle's uqo_expf; division is IEEE (HIP's correctly rounded f32 '/').
+// Algorithm: Copyright (C) 1993 by Sun Microsystems, Inc.; notice kept in
+// third_party/NOTICE.sunpro-expf.
 UQ_DEV float uq_expf(float x) {
     const uint32_t bx = __builtin_bit_cast(uint32_t, x);
     const uint32_t ax = bx & 0x7fffffffu;

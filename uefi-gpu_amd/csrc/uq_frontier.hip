@@ -36,7 +36,8 @@ namespace uq {
 namespace {
 
 // IQ4_NL / IQ4_XS code book (frontier_core.rs:67) and the IQ3_XXS grid
-// (frontier_tables.rs:2-35, ggml's iq3xxs_grid): data of the format.
+// (frontier_tables.rs:2-35, ggml's iq3xxs_grid): data of the format, from
+// ggml (MIT licence, third_party/LICENSE.ggml).
 __constant__ __attribute__((aligned(16))) int8_t c_iq4[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 __constant__ uint32_t c_iq3_grid[256] = {
     0x04040404u, 0x04040414u, 0x04040424u, 0x04040c0cu, 0x04040c1cu, 0x04040c3eu, 0x04041404u, 0x04041414u,

@@ -53,14 +53,23 @@ def cpu_model():
     return platform.processor()
 
 
-def cpu_baseline(seconds=10.0):
-    """The oracle's Q8_0 matvec (the C restatement of the reference's CPU
-    arithmetic) on 1 thread over the same shapes; lm_head limited to its first
-    15,193 rows (a tenth) so one pass stays short. Repeats passes until
-    `seconds` of CPU time have elapsed."""
+def _oracle():
+    """The oracle's single-thread -O2 build (liboracle_cpu.so), used only as the
+    timed CPU baseline."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    O.use_cpu_baseline_build()
     O.set_threads(1)
+    return O
+
+
+def cpu_baseline(seconds=10.0, decode_state=None):
+    """The oracle's Q8_0 matvec (the C restatement of the reference's CPU
+    arithmetic, built -O2 -ffp-contract=off, one thread) over the same shapes;
+    lm_head limited to its first 15,193 rows (a tenth) so one pass stays short.
+    Repeats passes until `seconds` of CPU time have elapsed. With the decode
+    leg's state, also 16 oracle decode steps after the 512-token prompt."""
+    O = _oracle()
     work = []
     for name, N, K, pair in SHAPES:
         rows = 15193 if name == "lm_head" else N
@@ -79,21 +88,51 @@ def cpu_baseline(seconds=10.0):
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    return {"value": round(total_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "oracle Q8_0 matvec (int8 activations, exact block sums), %d passes over q/o, k/v, "
-                      "gate, up, down and the first 15193 lm_head rows; %.1f s; host CPU %s, nproc %d"
-                      % (passes, el, cpu_model(), os.cpu_count() or 0)}
+    out = {"value": round(total_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": "oracle Q8_0 matvec (int8 activations, exact block sums; gcc -O2 -ffp-contract=off, one "
+                     "thread), %d passes over q/o, k/v, gate, up, down and the first 15193 lm_head rows; %.1f s; "
+                     "host CPU %s, nproc %d" % (passes, el, cpu_model(), os.cpu_count() or 0)}
+    if decode_state is not None:
+        out["decode"] = cpu_decode(O, decode_state)
+    return out
 
 
-def decode_bench(prompt_len=512, steps=128):
+def cpu_decode(O, st, steps=16):
+    """16 greedy steps of the oracle decoder (one thread) on the full
+    Qwen2.5-1.5B-shape model at positions 512..527. The oracle's KV cache for
+    the 512-token prompt is taken from the GPU prefill (bit-identical to the
+    oracle's own prefill in the parity tests; an oracle prefill on one core
+    would take tens of minutes). The ids are checked against the GPU's."""
+    cfg, tensors, first, gpu_ids, kv = st["cfg"], st["tensors"], st["first"], st["ids"], st["kv"]
+    o = O.Model(cfg, {k: v[3] for k, v in tensors.items()})
+    for layer, (k, v) in enumerate(kv):
+        o.set_kv(layer, k, v)
+    tok, ids = first, []
+    t0 = time.perf_counter()
+    for i in range(steps):
+        rc, tok, _ = o.decode(tok, st["prompt"] + i)
+        if rc:
+            raise RuntimeError("oracle decode rc=%d" % rc)
+        ids.append(tok)
+    el = time.perf_counter() - t0
+    return {"tok_s": round(steps / el, 3), "ms_per_token": round(el * 1e3 / steps, 1), "steps": steps,
+            "positions": [st["prompt"], st["prompt"] + steps - 1], "cores": 1,
+            "ids_match_gpu": [int(i) for i in ids] == [int(i) for i in gpu_ids[:steps]],
+            "sample": "oracle decode (exact-double reductions, int8 activations, fp16 KV) of the 28-layer "
+                      "model, %d steps after the 512-token prompt, %.1f s" % (steps, el)}
+
+
+def decode_bench(prompt_len=512, steps=128, keep=None):
     """Qwen2.5-1.5B-architecture Q8_0 greedy run, bs=1, random-init weights: a
     512-token prompt of seeded uniform ids through the int8-MFMA prefill, then
     `steps` decode steps (one hipGraph launch each, greedy id fed back on the
     device) timed with HIP events. Prefill is timed on the host clock around
-    the synchronous call."""
+    the synchronous call. `keep` (a dict) receives what the CPU decode
+    baseline needs: the tensors, the prompt's KV cache and the ids."""
     cfg = dict(uq.QWEN25_15B, max_seq=1024)
     t0 = time.perf_counter()
-    model = uq.Qwen2Model(cfg, uq.synth_qwen2(cfg, 0x5EED0002))
+    tensors = uq.synth_qwen2(cfg, 0x5EED0002)
+    model = uq.Qwen2Model(cfg, tensors)
     t_load = time.perf_counter() - t0
     prompt = uq.synth_tokens(0x5EED0002, prompt_len, cfg["vocab"])
     model.prefill(prompt)                             # warm-up
@@ -107,6 +146,9 @@ def decode_bench(prompt_len=512, steps=128):
     ids, ms = model.decode_run(first, prompt_len, steps)
     weight_bytes = 28 * 49717248 + 247959552
     kv_bytes = sum(28 * 2 * (prompt_len + i + 1) * 256 * 2 for i in range(steps))
+    if keep is not None:                              # decode_run wrote positions 512.., the prompt's KV is intact
+        keep.update(cfg=cfg, tensors=tensors, first=int(first), ids=[int(i) for i in ids], prompt=prompt_len,
+                    kv=[model.kv(layer, prompt_len) for layer in range(cfg["layers"])])
     model.free()
     return {"tok_s": round(steps / (ms / 1e3), 2), "ms_per_token": round(ms / steps, 4), "prompt": prompt_len,
             "steps": steps, "weight_bytes_per_token": weight_bytes,
@@ -303,36 +345,43 @@ def main():
     # a fused pair reads two weight matrices and one activation, writes one output
     step_bytes = sum(q8_bytes(N, K) * 2 - (K + K // 32 * 4) - 4 * N if pair else q8_bytes(N, K)
                      for _, N, K, pair in SHAPES)
-    # one timed "round" in uq_time_matvecs = every copy once = `copies` steps
-    rounds = max(1, args.steps // args.copies)
-    steps = rounds * args.copies
-    warm_rounds = max(1, args.warmup // args.copies)
-    total_ms, _ = uq.time_matvecs(weights, pairs, 8960, rounds, warm_rounds, -1)
+    steps, warmup = args.steps, args.warmup
+    # step j runs weight copy j % copies: warmup steps 0..W-1 untimed, then
+    # exactly K timed steps W..W+K-1 between one HIP event pair
+    def step_list(first, count, order=None):
+        ws, ps = [], []
+        for j in range(first, first + count):
+            chunk = range((j % args.copies) * per_copy, (j % args.copies + 1) * per_copy)
+            for i in (sorted(chunk, key=order) if order else chunk):
+                ws.append(weights[i])
+                ps.append(pairs[i])
+        return ws, ps
+
+    def timed(fn, order=None):
+        if warmup:
+            fn(*step_list(0, warmup, order))
+        return fn(*step_list(warmup, steps, order))
+
+    total_ms = timed(lambda ws, ps: uq.time_matvecs(ws, ps, 8960, 1, 0, -1)[0])
     value = step_bytes * steps / (total_ms / 1e3) / 1e9
     # the same matvecs with each copy's weights of one input length in one
     # job-table launch (q/o, k/v, gate+up pair, lm_head at K=1536; down at
-    # K=8960): the batch form of Gpu::batch, reported beside `value`
-    tw, tp = [], []
-    for c in range(args.copies):
-        chunk = list(range(c * per_copy, (c + 1) * per_copy))
-        for k in (1536, 8960):
-            for i in chunk:
-                if shape_of[i][2] == k:
-                    tw.append(weights[i])
-                    tp.append(pairs[i])
-    tables_ms = uq.time_matvec_tables(tw, tp, 8960, rounds, warm_rounds)
+    # K=8960), the graph_linear table form, reported beside `value`
+    by_k = lambda i: (shape_of[i][2], i)
+    tables_ms = timed(lambda ws, ps: uq.time_matvec_tables(ws, ps, 8960, 1, 0), order=by_k)
     tables_gbs = step_bytes * steps / (tables_ms / 1e3) / 1e9
     # dominant kernel alone: lm_head launches back to back over the copies,
     # one event pair around all of them -> mean launch duration
     lm_ws = [w for w, sh in zip(weights, shape_of) if sh[0] == "lm_head"]
-    lm_total, _ = uq.time_matvecs(lm_ws, [0] * len(lm_ws), 1536, rounds, warm_rounds, -1)
-    lm_ms = lm_total / (rounds * len(lm_ws))
+    lm_rounds = max(1, steps // args.copies)
+    lm_total, _ = uq.time_matvecs(lm_ws, [0] * len(lm_ws), 1536, lm_rounds, 1, -1)
+    lm_ms = lm_total / (lm_rounds * len(lm_ws))
     lm_bytes = q8_bytes(151936, 1536)
     lm_gbs = lm_bytes / (lm_ms / 1e3) / 1e9
 
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
-        "warmup": warm_rounds * args.copies, "ms_per_step": round(total_ms / steps, 5),
+        "warmup": warmup, "ms_per_step": round(total_ms / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "Q8_0 matvec sweep bs=1, Qwen2.5-1.5B shapes (NxK) 1536x1536, 256x1536, "
@@ -343,7 +392,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(lm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": LM_HEAD_TRAFFIC_BYTES,
                      "kernel": "Q8_0 matvec, lm_head 151936x1536 (%d B per launch), mean of %d back-to-back "
-                               "launches %.4f ms" % (lm_bytes, rounds * len(lm_ws), lm_ms)},
+                               "launches %.4f ms" % (lm_bytes, lm_rounds * len(lm_ws), lm_ms)},
     }
     result["sweep_job_tables"] = {
         "GBs": round(tables_gbs, 2), "frac": round(tables_gbs / HBM_PEAK_GBS, 4),
@@ -355,14 +404,15 @@ def main():
                            "note": "plain int4 streaming read / copy of 1 GiB, same box"}
     for w in weights:
         w.free()
+    decode_state = {} if not args.no_cpu else None
     if not args.no_decode:
-        result["decode"] = decode_bench()
+        result["decode"] = decode_bench(keep=decode_state)
         result["prefill_gemm"] = prefill_gemm_bench()
         result["q4k_sweep"] = q4k_sweep()
         result["q3k_sweep"] = q3k_sweep()
         result["moe"] = moe_bench()
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(decode_state=decode_state or None)
     print(json.dumps(result), flush=True)
 
 

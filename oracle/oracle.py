@@ -50,6 +50,15 @@ def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
+def use_cpu_baseline_build():
+    """Load liboracle_cpu.so (-O2, no OpenMP: one thread) instead of the tests'
+    build. bench.py's CPU baseline calls this before any other oracle call."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != os.path.join(HERE, "liboracle_cpu.so"):
+        raise RuntimeError("oracle library already loaded")
+    LIB_PATH = os.path.join(HERE, "liboracle_cpu.so")
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -322,6 +331,18 @@ class Model:
         kvd = self.cfg["kv_heads"] * self.cfg["head_dim"]
         ptr = lib().uqo_state_keys(self.state, layer)
         return np.ctypeslib.as_array(ptr, shape=(count * kvd,)).reshape(count, kvd).copy()
+
+    def set_kv(self, layer, keys, values):
+        """Overwrite positions [0, len(keys)) of one layer's caches (fp16 bits,
+        [count][kv_heads*head_dim]), e.g. with a prefill computed elsewhere."""
+        kvd = self.cfg["kv_heads"] * self.cfg["head_dim"]
+        keys = np.ascontiguousarray(keys, np.uint16).reshape(-1, kvd)
+        values = np.ascontiguousarray(values, np.uint16).reshape(-1, kvd)
+        n = keys.shape[0]
+        assert values.shape[0] == n <= self.cfg["max_seq"]
+        for ptr, src in ((lib().uqo_state_keys(self.state, layer), keys),
+                         (lib().uqo_state_values(self.state, layer), values)):
+            np.ctypeslib.as_array(ptr, shape=(n * kvd,))[:] = src.reshape(-1)
 
     def values(self, layer, count):
         kvd = self.cfg["kv_heads"] * self.cfg["head_dim"]

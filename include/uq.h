@@ -122,7 +122,7 @@ int uq_matvec_table_dev(const uq_weight_t* ws, const uq_weight_t* w2s, int count
 int uq_quant_act(const float* x, int64_t n, int8_t* q, float* scale);
 int uq_block_dots(uq_weight_t w, const float* x, int64_t n, int32_t* dots, int64_t count);
 
-/* The prefill GEMM alone (prefill_gemm, gpu_prefill.cu:74-100; CPU check
+/* The prefill GEMM alone (prefill_gemm, gpu_prefill.cu:10-36; CPU check
  * gpu_prefill.rs:95-121): y[t][r] for `tokens` rows of pre-quantized
  * activations xq[t][n] with scales xs[t][n/32], host memory. Q8_0, m % 64. */
 int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t tokens, float* y);
@@ -151,7 +151,7 @@ typedef struct {
 } uq_linear_job;
 
 /* Weights::linear (frontier_forward.rs:17; frontier_backend.rs:243) over
- * frontier_matvec (frontier_quant.cu:55-63): y = W x, host memory, synchronous.
+ * frontier_matvec (frontier_quant.cu:58-66): y = W x, host memory, synchronous.
  * Non-finite input or output -> UQ_ERR_NONFINITE (frontier_backend.rs:222,272);
  * Q3_K/Q4_K weights -> UQ_ERR_QUANT_TYPE.
  * With a Q8_0 weight this is also Gpu::matvec (llm.rs:246-273): matvec_q8 on
@@ -264,7 +264,7 @@ int uq_model_kv(uq_model_t m, int layer, int count, uint16_t* keys, uint16_t* va
  * expert down(silu(gate x) * (up x)) with int8 activations per 32; combine in
  * rank order, shared expert weighted by sigmoid(gate_inp . x). The expert
  * matrices live in one HBM-resident bank per projection; the routing result
- * stays on the device (the FrontierJob table of frontier_quant.cu:277-299). */
+ * stays on the device (the FrontierJob table of frontier_quant.cu:71-93). */
 typedef struct uq_moe* uq_moe_t;
 int uq_moe_create(int32_t dim, int32_t ff, int32_t experts, int32_t top_k, uint32_t expert_kind, uq_moe_t* out);
 int uq_moe_free(uq_moe_t m);

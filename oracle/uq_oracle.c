@@ -480,7 +480,7 @@ void uqo_q8_dequant_dot(const uint8_t* w, int64_t n, int64_t m, const float* x, 
     }
 }
 
-/* Q8_0 prefill GEMM (driver/kernels/gpu_prefill.cu:74-100; oracle
+/* Q8_0 prefill GEMM (driver/kernels/gpu_prefill.cu:10-36; oracle
  * gpu_prefill.rs:95-121): per 32-block int32 dot, accumulator reset per block,
  * f = fmaf((float)c, dw * dx, f) sequentially over blocks. y[token * m + row]. */
 void uqo_prefill_gemm(const uint8_t* w, int64_t n, int64_t m, int64_t batch,
@@ -502,7 +502,7 @@ void uqo_prefill_gemm(const uint8_t* w, int64_t n, int64_t m, int64_t batch,
     }
 }
 
-/* RMSNorm: driver/kernels/gpu_fused.cu:193-200 (y = x * scale * w, eps 1e-6)
+/* RMSNorm: driver/kernels/gpu_fused.cu:28-35 (y = x * scale * w, eps 1e-6)
  * with the sum of squares formed as in driver/src/frontier_forward.rs:38-42:
  * f32 squares summed in double, mean rounded to f32. */
 void uqo_rmsnorm(const float* x, const float* gamma, int64_t n, float eps, float* y) {
@@ -528,7 +528,7 @@ void uqo_rope_table(int seq, int head_dim, float theta, float* table) {
         }
 }
 
-/* driver/kernels/gpu_ops.cu:235-245: bias add then NeoX rotate-half on pairs
+/* driver/kernels/gpu_ops.cu:9-20: bias add then NeoX rotate-half on pairs
  * (j, j+hd/2): u = v[a]+b[a], w = v[b]+b[b]; v[a] = u*c - w*s; v[b] = u*s + w*c. */
 void uqo_rope_bias(float* v, const float* bias, int heads, int head_dim, const float* trig_row) {
     const int half = head_dim / 2;
@@ -544,7 +544,7 @@ void uqo_rope_bias(float* v, const float* bias, int heads, int head_dim, const f
         }
 }
 
-/* driver/kernels/gpu_dp4a.cu:63 (and gpu_ops.cu:267): (g / (1 + exp(-g))) * u. */
+/* driver/kernels/gpu_dp4a.cu:63 (and gpu_ops.cu:41): (g / (1 + exp(-g))) * u. */
 float uqo_silu_mul(float g, float u) {
     float e = uqo_expf(-g);
     float den = 1.0f + e;
@@ -552,7 +552,7 @@ float uqo_silu_mul(float g, float u) {
     return s * u;
 }
 
-/* Decode attention, driver/kernels/gpu_attention.cu:202-226 (CPU form
+/* Decode attention, driver/kernels/gpu_attention.cu:2-26 (CPU form
  * llm.rs:355-368) over an fp16 KV cache laid out [t][kv_heads*hd]:
  * s_t = (q.k_t) * (1/sqrt(hd)) with q.k summed in double; softmax with max
  * subtraction, e_t = exp(s_t - max), total summed in double, p_t = e_t/total;
@@ -587,7 +587,7 @@ void uqo_attention(const float* q, const uint16_t* keys, const uint16_t* values,
     free(sc);
 }
 
-/* driver/kernels/gpu_greedy.cu:269-295 (CPU check gpu_graph.rs:14-23): argmax,
+/* driver/kernels/gpu_greedy.cu:1-27 (CPU check gpu_graph.rs:14-23): argmax,
  * the lowest id wins ties, any non-finite logit marks the result bad. */
 int uqo_greedy(const float* logits, int64_t n, int* bad) {
     float best = -INFINITY;
@@ -633,7 +633,7 @@ const uint16_t* uqo_state_values(const uqo_state* s, int layer) {
     return s->values + (size_t)layer * s->m.max_seq * s->m.kv_heads * s->m.head_dim;
 }
 
-/* embedding_q8, driver/kernels/gpu_embedding.cu:298-304: x = half(d) * q. */
+/* embedding_q8, driver/kernels/gpu_embedding.cu:3-9: x = half(d) * q. */
 static void embed(const uqo_qwen2* m, uint32_t token, float* x) {
     const int64_t nb = m->dim / 32;
     for (int i = 0; i < m->dim; i++) {
@@ -877,7 +877,7 @@ int uqo_moe_ffn(const uqo_moe* mo, const float* x, const float* router_logits, f
 }
 
 /* ---------------------------------------------------------------- fp32-activation reader
- * frontier_matvec (frontier_quant.cu:55-63; host Weights::linear,
+ * frontier_matvec (frontier_quant.cu:58-66; host Weights::linear,
  * frontier_backend.rs:243): y[r] = sum_i value(r, i) * x[i] with fp32 x. Each
  * value is a dequantize() f32 whose products with x are exact in double; the
  * sum runs in double in index order and is rounded to f32 once. */

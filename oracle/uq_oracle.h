@@ -16,7 +16,7 @@
  *     independent of summation order up to ~2^-29 relative, so the GPU may sum
  *     in any order and still agree bit for bit (see uqo_* docstrings);
  *   - the Q8_0 prefill GEMM keeps the reference's sequential per-32-block f32
- *     fmaf update (driver/kernels/gpu_prefill.cu:93-94), mirrored exactly;
+ *     fmaf update (driver/kernels/gpu_prefill.cu:29-30), mirrored exactly;
  *   - exp is uqo_expf, the libm 0.2.16 expf of the reference's Rust path
  *     (FreeBSD e_expf.c; driver/src/frontier_cpu_expf.rs:80-170), in f32.
  *

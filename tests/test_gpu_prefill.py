@@ -1,6 +1,6 @@
 """GPU prefill (int8 MFMA GEMM + batched norm/RoPE/attention) against the
 oracle, through the C ABI. The GEMM keeps the reference's sequential per-block
-fmaf update (gpu_prefill.cu:93-94), so outputs are compared bit for bit; the
+fmaf update (gpu_prefill.cu:29-30), so outputs are compared bit for bit; the
 int32 block dots inside it are exact by construction of that comparison."""
 import numpy as np
 import pytest

@@ -1,6 +1,6 @@
 """Pins of the oracle's restatement of the reference's remaining quant kinds
 (dequantize, driver/src/frontier_core.rs:53-106) and of its fp32-activation
-linear (frontier_matvec, driver/kernels/frontier_quant.cu:55-63).
+linear (frontier_matvec, driver/kernels/frontier_quant.cu:58-66).
 
 Each kind is checked against blocks built by an encoder written here from the
 layout description (code, scale and sign placement), so a wrong shift, index

@@ -1,6 +1,6 @@
 // Token embedding + residual + RMSNorm + block-32 quant in one workgroup
-// (embedding_q8, gpu_embedding.cu:298-304; fused_resnorm_quant,
-// gpu_norm_quant.cu:307-323; quant_act, gpu_dp4a.cu:23-31). The token is read
+// (embedding_q8, gpu_embedding.cu:3-9; fused_resnorm_quant,
+// gpu_norm_quant.cu:3-19; quant_act, gpu_dp4a.cu:23-31). The token is read
 // from device memory so that one captured graph serves every step (the
 // reference patches it into its push buffer per token, gpu_graph.rs:170-178).
 #include "uq_device.h"

@@ -1,7 +1,7 @@
 // GGUF block-quant matvec for gfx950 (Q8_0, Q4_K, Q3_K) with int8 activations.
 //
 // Replaces linear_dp4a / qkv_dp4a / gateup_dp4a (driver/kernels/gpu_dp4a.cu:23-64)
-// and the fp32-activation frontier_matvec (driver/kernels/frontier_quant.cu:264-272).
+// and the fp32-activation frontier_matvec (driver/kernels/frontier_quant.cu:58-66).
 //
 // Design (bandwidth-bound, no MFMA):
 //  * weights are repacked once so every lane issues 16-byte global loads:

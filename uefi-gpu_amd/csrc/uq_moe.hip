@@ -4,7 +4,7 @@
 //
 // Replaces Forward::ffn (driver/src/frontier_forward.rs:164-199) and its
 // descriptor-driven multi-matvec launch (frontier_multi_matvec,
-// driver/kernels/frontier_quant.cu:277-299; pack, frontier_dispatch.rs:12-31).
+// driver/kernels/frontier_quant.cu:71-93; pack, frontier_dispatch.rs:12-31).
 // The reference moves experts between SSD, CPU and a 12 GB card; here every
 // expert sits in an HBM-resident bank (experts stacked by rows in one repacked
 // weight per projection), and the routing result stays on the device: the

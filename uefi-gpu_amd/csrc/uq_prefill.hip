@@ -3,12 +3,12 @@
 //
 // Replaces prefill_gemm / prefill_repack / prefill_quant / prefill_resnorm /
 // prefill_rope / prefill_attention / silu_mul (driver/kernels/gpu_prefill.cu:
-// 74-165, gpu_ops.cu:266-268) and the stream built by prepare_prefill
+// 10-101, gpu_ops.cu:40-42) and the stream built by prepare_prefill
 // (driver/src/gpu_prefill.rs:122-150).
 //
 // GEMM: y[t][r] = sum over 32-blocks b, in order, of
 //   f = fmaf((float)c_b, dw[r][b] * dx[t][b], f),   c_b = sum_k qw[r][k] qx[t][k]
-// (gpu_prefill.cu:93-94). c_b is one v_mfma_i32_16x16x32_i8 per block with a
+// (gpu_prefill.cu:29-30). c_b is one v_mfma_i32_16x16x32_i8 per block with a
 // zero accumulator; the f32 rescale runs on the VALU in the same order as the
 // reference, so results match the oracle bit for bit.
 // Operands come from the row-major planes used by decode (no second weight
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
 
 // ------------------------------------------------------------------ RoPE + KV
 // One workgroup per token: q/k bias + RoPE (q in place), k and v rounded to
-// fp16 into the cache at position p0 + t (prefill_rope, gpu_prefill.cu:137-145).
+// fp16 into the cache at position p0 + t (prefill_rope, gpu_prefill.cu:73-81).
 __global__ __launch_bounds__(256) void k_pf_rope_kv(PfRopeArgs a) {
     const int t = blockIdx.x, pos = a.p0 + t;
     const int hd = a.head_dim, half = hd / 2, kvd = a.kv_heads * hd;

@@ -3,18 +3,18 @@
 // Per transformer layer:
 //   qkv_rope   residual + RMSNorm + quant prologue, q|k|v matvec, q/k bias,
 //              RoPE, fp16 K/V store at `pos` (fused_resnorm + quant_act +
-//              qkv_dp4a + rope_bias: gpu_fused.cu:193-200, gpu_dp4a.cu:23-59,
-//              gpu_ops.cu:235-246)
+//              qkv_dp4a + rope_bias: gpu_fused.cu:28-35, gpu_dp4a.cu:23-59,
+//              gpu_ops.cu:9-20)
 //   attention  GQA softmax attention over the fp16 cache split over position
 //              chunks: scores, then P.V into a double accumulator
-//              (fused_attention, gpu_attention.cu:202-226)
+//              (fused_attention, gpu_attention.cu:2-26)
 //   o matvec   accumulator -> f32 -> block-32 quant prologue, Q8_0 matvec
 //              (quant_act + linear_dp4a)
 //   gateup_q   residual + RMSNorm + quant prologue, gate/up matvec, SiLU*up,
 //              block-32 quant (gateup_dp4a, gpu_dp4a.cu:60-64)
 //   down       generic matvec
 // and per token: output RMSNorm, lm_head matvec with per-workgroup argmax,
-// greedy finish (greedy_tiles / greedy_finish, gpu_greedy.cu:269-295).
+// greedy finish (greedy_tiles / greedy_finish, gpu_greedy.cu:1-27).
 //
 // Fusion runs forward: a consumer workgroup recomputes the residual sum and
 // RMSNorm of the 1536-wide activation itself (from L2) while its weight loads

@@ -99,6 +99,14 @@ def lib():
             "uqo_decode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, _u32p, _f32p]),
             "uqo_state_keys": (_u16p, [ctypes.c_void_p, ctypes.c_int]),
             "uqo_state_values": (_u16p, [ctypes.c_void_p, ctypes.c_int]),
+            "uqo_refo_new": (ctypes.c_void_p, [ctypes.POINTER(Qwen2), ctypes.c_int]),
+            "uqo_refo_free": (None, [ctypes.c_void_p]),
+            "uqo_refo_decode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, _u32p, _f32p]),
+            "uqo_refo_resnorm": (None, [_f32p, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_float, ctypes.c_int]),
+            "uqo_refo_dotrow": (ctypes.c_float, [_u8p, _f32p, _i8p, _i64]),
+            "uqo_refo_linear_row": (ctypes.c_float, [_u8p, _f32p, _i8p, _i64]),
+            "uqo_refo_attention_head": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, _f32p]),
             "uqo_moe_route": (ctypes.c_int, [_f32p, ctypes.c_int, ctypes.c_int, _i32p, _f32p]),
             "uqo_moe_ffn": (ctypes.c_int, [ctypes.POINTER(Moe), _f32p, _f32p, _f32p, _i32p, _f32p]),
         }
@@ -348,6 +356,65 @@ class Model:
         kvd = self.cfg["kv_heads"] * self.cfg["head_dim"]
         ptr = lib().uqo_state_values(self.state, layer)
         return np.ctypeslib.as_array(ptr, shape=(count * kvd,)).reshape(count, kvd).copy()
+
+
+class RefoModel(Model):
+    """The reference-order decoder: the f32 operation orders of the reference's
+    decode-graph kernels (gpu_graph.rs:137-162), f32 KV cache (kv_fp16: the
+    cache rounded to fp16 as this build stores it). Token by token only."""
+
+    def __init__(self, cfg, tensors, kv_fp16=False):
+        super().__init__(cfg, tensors)
+        self.refo = lib().uqo_refo_new(ctypes.byref(self.m), 1 if kv_fp16 else 0)
+
+    def __del__(self):
+        if getattr(self, "refo", None):
+            lib().uqo_refo_free(self.refo)
+            self.refo = None
+        super().__del__()
+
+    def decode(self, token, pos, want_logits=False):
+        nxt = ctypes.c_uint32()
+        logits = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
+        rc = lib().uqo_refo_decode(self.refo, token, pos, ctypes.byref(nxt), None if logits is None else p(logits, _f32p))
+        return rc, nxt.value, logits
+
+    def prefill(self, tokens, want_logits=False):
+        raise NotImplementedError("the reference-order decoder ingests prompts token by token")
+
+
+def refo_resnorm(x, residual, w, eps=1e-6, add=True):
+    """fused_resnorm (gpu_fused.cu:28-35): returns (x + residual, y)."""
+    x = np.ascontiguousarray(x, np.float32).copy()
+    r = np.ascontiguousarray(residual, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    lib().uqo_refo_resnorm(p(x, _f32p), p(r, _f32p), p(w, _f32p), p(y, _f32p), x.size, eps, 1 if add else 0)
+    return x, y
+
+
+def refo_dotrow(w_row, xs, qx):
+    """dotrow (gpu_dp4a.cu:32-39) of one Q8_0 row with a quantized x."""
+    return lib().uqo_refo_dotrow(p(np.ascontiguousarray(w_row, np.uint8), _u8p),
+                                 p(np.ascontiguousarray(xs, np.float32), _f32p),
+                                 p(np.ascontiguousarray(qx, np.int8), _i8p), qx.size // 32)
+
+
+def refo_linear_row(w_row, xs, qx):
+    """linear_dp4a (gpu_dp4a.cu:40-52) of one Q8_0 row with a quantized x."""
+    return lib().uqo_refo_linear_row(p(np.ascontiguousarray(w_row, np.uint8), _u8p),
+                                     p(np.ascontiguousarray(xs, np.float32), _f32p),
+                                     p(np.ascontiguousarray(qx, np.int8), _i8p), qx.size // 32)
+
+
+def refo_attention_head(q, keys, values, pos, kh, hd):
+    """fused_attention (gpu_attention.cu:2-26) for one head over f32 [t][kvd] caches."""
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(hd, np.float32)
+    lib().uqo_refo_attention_head(p(np.ascontiguousarray(q, np.float32), _f32p), p(keys, _f32p), p(values, _f32p),
+                                  pos, keys.shape[1], kh, hd, p(out, _f32p))
+    return out
 
 
 class MoeLayer:

@@ -954,3 +954,277 @@ int64_t uqo_frontier_fixture(uint32_t kind, int64_t n, uint8_t* out) {
     return rb;
 }
 
+
+/* ----------------------------------------------------------------------- */
+/* Reference-order decode: the f32 operation orders of the reference's      */
+/* decode graph (gpu_graph.rs:137-162), kernel by kernel. A second oracle   */
+/* form beside the exact-double contract above, for tolerance-graded        */
+/* comparison against the reference's own arithmetic:                       */
+/*   embedding_q8        gpu_embedding.cu:3-9                               */
+/*   fused_resnorm       gpu_fused.cu:28-35 (128-thread strided squares,    */
+/*                       shared-memory tree 64..1, (v*scale)*w)             */
+/*   quant_act           gpu_dp4a.cu:23-31 (= uqo_quant_act)                */
+/*   qkv_dp4a/gateup     gpu_dp4a.cu:32-39,53-64 (dotrow: 32 lanes, 8-byte   */
+/*                       segments, fmaf per block, xor butterfly 16..1)     */
+/*   linear_dp4a         gpu_dp4a.cu:40-52 (128 threads, 16-byte halves,    */
+/*                       fmaf per half-block, warp butterflies, then        */
+/*                       ((p0+p1)+p2)+p3)                                    */
+/*   rope_bias           gpu_ops.cu:9-20 (shared host trig table)           */
+/*   fused_attention     gpu_attention.cu:2-26 (f32 KV; lane-strided q.k    */
+/*                       with butterfly, strided exp sums + tree, p/total,  */
+/*                       sequential P.V)                                    */
+/*   greedy              gpu_greedy.cu:1-27                                 */
+/* Every multiply and add is a separate f32 rounding except the explicit    */
+/* fmaf of the dp4a kernels (the reference builds with --fmad=false).       */
+/* exp is uqo_expf (libm's algorithm) where the GPU kernels call CUDA's     */
+/* expf, whose steps are not reproduced; that and the host trig table are   */
+/* the only departures. kv_fp16 != 0 rounds cached K and V to fp16, the     */
+/* cache format of this build, to separate order effects from cache         */
+/* precision.                                                               */
+
+struct uqo_refo {
+    uqo_qwen2 m;
+    int kv_fp16;
+    float* keys;   /* [layers][max_seq][kv_dim] */
+    float* values;
+    float* trig;
+};
+
+uqo_refo* uqo_refo_new(const uqo_qwen2* m, int kv_fp16) {
+    uqo_refo* s = (uqo_refo*)calloc(1, sizeof(uqo_refo));
+    s->m = *m;
+    s->kv_fp16 = kv_fp16;
+    const size_t kv = (size_t)m->layers * m->max_seq * m->kv_heads * m->head_dim;
+    s->keys = (float*)calloc(kv, sizeof(float));
+    s->values = (float*)calloc(kv, sizeof(float));
+    s->trig = (float*)malloc(sizeof(float) * (size_t)m->max_seq * m->head_dim);
+    uqo_rope_table(m->max_seq, m->head_dim, m->theta, s->trig);
+    return s;
+}
+void uqo_refo_free(uqo_refo* s) {
+    if (!s) return;
+    free(s->keys); free(s->values); free(s->trig); free(s);
+}
+
+/* xor butterfly of a 32-lane warp (x += shfl_xor(x, 16); ... 1): lane 0's total. */
+static float refo_butterfly32(float* v) {
+    for (int off = 16; off; off >>= 1) {
+        float t[32];
+        for (int i = 0; i < 32; i++) t[i] = v[i] + v[i ^ off];
+        memcpy(v, t, sizeof(t));
+    }
+    return v[0];
+}
+
+/* fused_resnorm, gpu_fused.cu:28-35, for n values (the kernel's n is 1536). */
+void uqo_refo_resnorm(float* x, const float* residual, const float* w, float* y, int n, float eps, int add) {
+    float sums[128];
+    for (int t = 0; t < 128; t++) {
+        float sum = 0.0f;
+        for (int i = t; i < n; i += 128) {
+            float v = add ? x[i] + residual[i] : x[i];
+            float sq = v * v;
+            sum = sum + sq;
+        }
+        sums[t] = sum;
+    }
+    for (int stride = 64; stride; stride >>= 1)
+        for (int t = 0; t < stride; t++) sums[t] = sums[t] + sums[t + stride];
+    const float mean = sums[0] / (float)n;
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; i++) {
+        float v = add ? x[i] + residual[i] : x[i];
+        if (add) x[i] = v;
+        float t = v * scale;
+        y[i] = t * w[i];
+    }
+}
+
+static int32_t dp4a8(const int8_t* a, const int8_t* b, int n) {
+    int32_t s = 0;
+    for (int j = 0; j < n; j++) s += (int32_t)a[j] * (int32_t)b[j];
+    return s;
+}
+
+/* dotrow, gpu_dp4a.cu:32-39: one 32-lane warp over a Q8_0 row of `blocks`
+ * blocks; lane l takes bytes 8*(l&3).. of blocks l>>2, l>>2 + 8, ... */
+float uqo_refo_dotrow(const uint8_t* w, const float* xs, const int8_t* xq, int64_t blocks) {
+    float lanes[32];
+    for (int lane = 0; lane < 32; lane++) {
+        const int seg = lane & 3;
+        float sum = 0.0f;
+        for (int64_t b = lane >> 2; b < blocks; b += 8) {
+            const uint8_t* wp = w + b * 34;
+            const int32_t acc = dp4a8((const int8_t*)(wp + 2 + seg * 8), xq + b * 32 + seg * 8, 8);
+            const float d = uqo_half(rd16(wp)) * xs[b];
+            sum = fmaf((float)acc, d, sum);
+        }
+        lanes[lane] = sum;
+    }
+    return refo_butterfly32(lanes);
+}
+
+/* linear_dp4a, gpu_dp4a.cu:40-52: 128 threads per row; thread t takes the
+ * 16-byte half (t&1) of blocks t>>1, t>>1 + 64, ...; warp butterflies, then
+ * ((p0 + p1) + p2) + p3. */
+float uqo_refo_linear_row(const uint8_t* w, const float* xs, const int8_t* xq, int64_t blocks) {
+    float p[4];
+    for (int warp = 0; warp < 4; warp++) {
+        float lanes[32];
+        for (int lane = 0; lane < 32; lane++) {
+            const int tid = warp * 32 + lane, seg = tid & 1;
+            float sum = 0.0f;
+            for (int64_t b = tid >> 1; b < blocks; b += 64) {
+                const uint8_t* wp = w + b * 34;
+                const int32_t acc = dp4a8((const int8_t*)(wp + 2 + seg * 16), xq + b * 32 + seg * 16, 16);
+                const float d = uqo_half(rd16(wp)) * xs[b];
+                sum = fmaf((float)acc, d, sum);
+            }
+            lanes[lane] = sum;
+        }
+        p[warp] = refo_butterfly32(lanes);
+    }
+    const float a = p[0] + p[1];
+    const float b = a + p[2];
+    return b + p[3];
+}
+
+static void refo_linear(const uint8_t* w, int64_t n, int64_t m, const float* xs, const int8_t* xq, float* y) {
+    const int64_t blocks = n / 32, rb = blocks * 34;
+    #pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; r++) y[r] = uqo_refo_linear_row(w + r * rb, xs, xq, blocks);
+}
+static void refo_dotrows(const uint8_t* w, int64_t n, int64_t m, const float* xs, const int8_t* xq, float* y) {
+    const int64_t blocks = n / 32, rb = blocks * 34;
+    #pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < m; r++) y[r] = uqo_refo_dotrow(w + r * rb, xs, xq, blocks);
+}
+
+/* fused_attention, gpu_attention.cu:2-26, for one query head over f32 keys
+ * and values [t][kvd] at KV head kh; head_dim hd (the kernel's is 128). */
+void uqo_refo_attention_head(const float* q, const float* keys, const float* values, int pos, int kvd, int kh,
+                             int hd, float* out) {
+    const int T = pos + 1;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)T);
+    const float qscale = (float)(1.0 / sqrt((double)hd));
+    for (int t = 0; t < T; t++) {
+        float lanes[32];
+        for (int lane = 0; lane < 32; lane++) {
+            float sum = 0.0f;
+            for (int j = lane; j < hd; j += 32) {
+                float pr = q[j] * keys[(size_t)t * kvd + kh * hd + j];
+                sum = sum + pr;
+            }
+            lanes[lane] = sum;
+        }
+        scores[t] = refo_butterfly32(lanes) * qscale;
+    }
+    float mx = -3.402823466e38f;
+    for (int t = 0; t < T; t++) mx = fmaxf(mx, scores[t]);
+    float red[128];
+    for (int tid = 0; tid < 128; tid++) {
+        float total = 0.0f;
+        for (int t = tid; t < T; t += 128) {
+            float e = uqo_expf(scores[t] - mx);
+            scores[t] = e;
+            total = total + e;
+        }
+        red[tid] = total;
+    }
+    for (int d = 64; d; d >>= 1)
+        for (int tid = 0; tid < d; tid++) red[tid] = red[tid] + red[tid + d];
+    const float total = red[0];
+    for (int t = 0; t < T; t++) scores[t] = scores[t] / total;
+    for (int i = 0; i < hd; i++) {
+        float sum = 0.0f;
+        for (int t = 0; t < T; t++) {
+            float pr = scores[t] * values[(size_t)t * kvd + kh * hd + i];
+            sum = sum + pr;
+        }
+        out[i] = sum;
+    }
+    free(scores);
+}
+
+static float refo_kv(const uqo_refo* s, float v) {
+    return s->kv_fp16 ? uqo_half(uqo_f16_rne(v)) : v;
+}
+
+int uqo_refo_decode(uqo_refo* s, uint32_t token, int pos, uint32_t* next, float* logits) {
+    const uqo_qwen2* m = &s->m;
+    if (pos < 0 || pos >= m->max_seq || (int64_t)token >= m->vocab) return -2;
+    const int D = m->dim, H = m->hidden, hd = m->head_dim, kvd = m->kv_heads * hd, half = hd / 2;
+    const int group = m->heads / m->kv_heads;
+    float *x = malloc(sizeof(float) * D), *tmp = calloc(D, sizeof(float)), *xn = malloc(sizeof(float) * D);
+    float *q = malloc(sizeof(float) * D), *k = malloc(sizeof(float) * kvd), *v = malloc(sizeof(float) * kvd);
+    float *att = malloc(sizeof(float) * D), *gate = malloc(sizeof(float) * H);
+    float *xs = malloc(sizeof(float) * (H / 32));
+    int8_t* xq = malloc(H);
+    int rc = 0;
+    embed(m, token, x);
+    const float* trig = s->trig + (size_t)pos * hd;
+    for (int l = 0; l < m->layers; l++) {
+        const uqo_layer* L = &m->layer[l];
+        float* kc = s->keys + ((size_t)l * m->max_seq) * kvd;
+        float* vc = s->values + ((size_t)l * m->max_seq) * kvd;
+        uqo_refo_resnorm(x, tmp, L->attn_norm, xn, D, m->eps, l > 0);
+        uqo_quant_act(xn, D, xs, xq);
+        refo_dotrows(L->wq, D, D, xs, xq, q);
+        refo_dotrows(L->wk, D, kvd, xs, xq, k);
+        refo_dotrows(L->wv, D, kvd, xs, xq, v);
+        /* rope_bias: q and k rotated after the bias add, v biased */
+        for (int h = 0; h < m->heads; h++)
+            for (int j = 0; j < half; j++) {
+                const int a = h * hd + j, b = a + half;
+                const float cs = trig[j], sn = trig[half + j];
+                const float u = L->bq ? q[a] + L->bq[a] : q[a], w = L->bq ? q[b] + L->bq[b] : q[b];
+                const float p0 = u * cs, p1 = w * sn, p2 = u * sn, p3 = w * cs;
+                q[a] = p0 - p1;
+                q[b] = p2 + p3;
+            }
+        for (int h = 0; h < m->kv_heads; h++)
+            for (int j = 0; j < half; j++) {
+                const int a = h * hd + j, b = a + half;
+                const float cs = trig[j], sn = trig[half + j];
+                const float u = L->bk ? k[a] + L->bk[a] : k[a], w = L->bk ? k[b] + L->bk[b] : k[b];
+                const float p0 = u * cs, p1 = w * sn, p2 = u * sn, p3 = w * cs;
+                kc[(size_t)pos * kvd + a] = refo_kv(s, p0 - p1);
+                kc[(size_t)pos * kvd + b] = refo_kv(s, p2 + p3);
+            }
+        for (int i = 0; i < kvd; i++) vc[(size_t)pos * kvd + i] = refo_kv(s, L->bv ? v[i] + L->bv[i] : v[i]);
+        #pragma omp parallel for schedule(static)
+        for (int h = 0; h < m->heads; h++)
+            uqo_refo_attention_head(q + h * hd, kc, vc, pos, kvd, h / group, hd, att + h * hd);
+        uqo_quant_act(att, D, xs, xq);
+        refo_linear(L->wo, D, D, xs, xq, tmp);
+        uqo_refo_resnorm(x, tmp, L->ffn_norm, xn, D, m->eps, 1);
+        uqo_quant_act(xn, D, xs, xq);
+        #pragma omp parallel for schedule(static)
+        for (int r = 0; r < H; r++) {
+            const int64_t rb = (int64_t)(D / 32) * 34;
+            const float g = uqo_refo_dotrow(L->wg + r * rb, xs, xq, D / 32);
+            const float u = uqo_refo_dotrow(L->wu + r * rb, xs, xq, D / 32);
+            const float e = uqo_expf(-g);
+            const float den = 1.0f + e;
+            const float sg = g / den;
+            gate[r] = sg * u;
+        }
+        uqo_quant_act(gate, H, xs, xq);
+        refo_linear(L->wd, H, D, xs, xq, tmp);
+        if (!all_finite(tmp, D)) { rc = -3; goto done; }
+    }
+    {
+        uqo_refo_resnorm(x, tmp, m->output_norm, xn, D, m->eps, 1);
+        uqo_quant_act(xn, D, xs, xq);
+        float* lg = logits ? logits : (float*)malloc(sizeof(float) * (size_t)m->vocab);
+        refo_linear(m->output, D, m->vocab, xs, xq, lg);
+        int bad = 0;
+        const int id = uqo_greedy(lg, m->vocab, &bad);
+        if (next) *next = (uint32_t)id;
+        if (!logits) free(lg);
+        rc = bad ? -1 : 0;
+    }
+done:
+    free(x); free(tmp); free(xn); free(q); free(k); free(v); free(att); free(gate); free(xs); free(xq);
+    return rc;
+}

@@ -95,6 +95,18 @@ int  uqo_decode(uqo_state* s, uint32_t token, int pos, uint32_t* next, float* lo
 const uint16_t* uqo_state_keys(const uqo_state* s, int layer);
 const uint16_t* uqo_state_values(const uqo_state* s, int layer);
 
+/* Reference-order decode (gpu_graph.rs:137-162 kernels' f32 orders; see the
+ * section comment in uq_oracle.c). kv_fp16: round cached K/V to fp16. */
+typedef struct uqo_refo uqo_refo;
+uqo_refo* uqo_refo_new(const uqo_qwen2* m, int kv_fp16);
+void      uqo_refo_free(uqo_refo* s);
+int  uqo_refo_decode(uqo_refo* s, uint32_t token, int pos, uint32_t* next, float* logits);
+void uqo_refo_resnorm(float* x, const float* residual, const float* w, float* y, int n, float eps, int add);
+float uqo_refo_dotrow(const uint8_t* w, const float* xs, const int8_t* xq, int64_t blocks);
+float uqo_refo_linear_row(const uint8_t* w, const float* xs, const int8_t* xq, int64_t blocks);
+void uqo_refo_attention_head(const float* q, const float* keys, const float* values, int pos, int kvd, int kh,
+                             int hd, float* out);
+
 /* MoE expert FFN (driver/src/frontier_forward.rs:164-199). */
 typedef struct {
     int32_t dim, ff, experts, top_k;

@@ -59,6 +59,10 @@ int uq_sync(void);
 
 /* GGUF row size of `n` values (frontier_core.rs:53-58 row_bytes); <0 on error. */
 int64_t uq_row_bytes(uint32_t kind, int64_t n);
+/* Free and total device memory of the context's GPU (hipMemGetInfo); the
+ * capacity the reference's residency planning budgets against
+ * (frontier_backend.rs:293-348, frontier_cache.rs:9-106). */
+int uq_device_memory(size_t* free_bytes, size_t* total_bytes);
 
 /* ---------------------------------------------------------------- weights */
 typedef struct uq_weight* uq_weight_t;
@@ -274,6 +278,8 @@ int uq_moe_set_expert(uq_moe_t m, int32_t e, const void* gate, const void* up, c
  * ffn_gate_inp_shexp of dim values (NULL: weight 1). */
 int uq_moe_set_shared(uq_moe_t m, uint32_t kind, const void* gate, const void* up, const void* down,
                       const float* gate_inp);
+/* The layer's shape as created. */
+int uq_moe_info(uq_moe_t m, int32_t* dim, int32_t* ff, int32_t* experts, int32_t* top_k, uint32_t* expert_kind);
 /* Host-memory call: x (dim), router logits (experts) -> out (dim); optional
  * ids/weights (top_k) of the routing. Non-finite input -> UQ_ERR_NONFINITE. */
 int uq_moe_ffn(uq_moe_t m, const float* x, const float* router_logits, float* out, int32_t* ids, float* weights);
@@ -330,6 +336,48 @@ int uq_gguf_meta_array(uq_gguf_t g, const char* key, uint32_t* elem_kind, uint64
 /* Element `index` of a string-array value (e.g. tokenizer.ggml.tokens):
  * pointer into the parsed directory and its byte length. */
 int uq_gguf_meta_array_str(uq_gguf_t g, const char* key, uint64_t index, const char** out, uint64_t* len);
+/* Tensor::rows (frontier_gguf.rs:86-94): absolute file range of `count`
+ * contiguous rows of tensor `index` from row `start`; count 0 or rows past the
+ * end -> UQ_ERR_FORMAT with UQ_GGUF_TENSOR_BOUNDS (UQ_GGUF_OVERFLOW on
+ * overflow). */
+int uq_gguf_tensor_rows(uq_gguf_t g, int64_t index, uint64_t start, uint64_t count, uint64_t* offset, uint64_t* bytes,
+                        int* gguf_error);
+/* Tensor::expert (frontier_gguf.rs:95-98): the rows of expert `expert` of a
+ * rank-3 [n, rows, experts] tensor; another rank or expert >= dims[2] ->
+ * UQ_GGUF_SHAPE. */
+int uq_gguf_tensor_expert(uq_gguf_t g, int64_t index, uint32_t expert, uint64_t* offset, uint64_t* bytes,
+                          int* gguf_error);
+
+/* ModelIndex (frontier_gguf.rs:101-137) over the directories of a split
+ * model: ModelIndex::new orders the shards by split.no and requires split.no
+ * 0..count-1, split.count == count and one split.tensors.count on every shard
+ * (else UQ_GGUF_SPLIT), no tensor name twice (UQ_GGUF_DUPLICATE), and as many
+ * tensors as split.tensors.count (UQ_GGUF_SPLIT). The index keeps the shard
+ * handles, which must outlive it. */
+typedef struct uq_gguf_index* uq_gguf_index_t;
+int uq_gguf_index_create(const uq_gguf_t* shards, int count, uq_gguf_index_t* out, int* gguf_error);
+int uq_gguf_index_free(uq_gguf_index_t ix);
+int uq_gguf_index_shard_count(uq_gguf_index_t ix);
+/* Shard i in split.no order (NULL when out of range). */
+uq_gguf_t uq_gguf_index_shard(uq_gguf_index_t ix, int i);
+/* ModelIndex::tensor: the shard (split.no order) and index of tensor `name`;
+ * UQ_GGUF_MISSING when no shard holds it. */
+int uq_gguf_index_find(uq_gguf_index_t ix, const char* name, int* shard, int64_t* index, int* gguf_error);
+/* ModelIndex::inventory: on-disk bytes of [other tensors,
+ * per_layer_token_embd.weight, *_exps.weight]. */
+int uq_gguf_index_inventory(uq_gguf_index_t ix, uint64_t* bytes3, int* gguf_error);
+/* A tensor of a file-backed shard as a device weight (uq_weight_upload of its
+ * bytes: n = dims[0], one row per remaining dim), or with expert >= 0 the
+ * rows of that expert of a rank-3 tensor (Backend::expert's byte range,
+ * frontier_backend.rs:98-128). Any kind uq_weight_upload takes. */
+int uq_gguf_load_weight(uq_gguf_t g, int64_t index, int32_t expert, uq_weight_t* out);
+/* The expert bank of MoE layer `layer` from a split model: every expert of
+ * blk.L.ffn_{gate,up,down}_exps.weight (rank 3, the bank's kind and shape)
+ * and the shared expert blk.L.ffn_{gate,up,down}_shexp.weight with the
+ * optional f32 blk.L.ffn_gate_inp_shexp.weight, loaded into `m` as
+ * uq_moe_set_expert / uq_moe_set_shared would. Fails with UQ_ERR_DEVICE before
+ * reading when twice the layer's bytes exceed the free HBM. */
+int uq_moe_load_gguf(uq_moe_t m, uq_gguf_index_t ix, int32_t layer);
 /* Model::text (driver/src/llm.rs:87-99): the bytes of token `id` from the
  * GPT-2 byte-level string in tokenizer.ggml.tokens. len = bytes needed; the
  * call fails with UQ_ERR_ARG (len still set) when cap is smaller. */

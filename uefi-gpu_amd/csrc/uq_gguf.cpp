@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -517,6 +518,218 @@ int uq_gguf_qwen2_config(uq_gguf_t g, int32_t max_seq, uq_qwen2_config* cfg) {
     cfg->eps = eps;
     cfg->theta = theta;
     return UQ_OK;
+}
+
+// Tensor::rows (frontier_gguf.rs:86-94): the absolute file range of `count`
+// contiguous rows from `start`.
+static int tensor_rows(const TensorInfo& t, uint64_t start, uint64_t count, uint64_t* off, uint64_t* n) {
+    const uint64_t total = t.bytes / t.row_bytes;
+    uint64_t end;
+    if (add_ovf(start, count, &end)) return G_OVERFLOW;
+    if (count == 0 || end > total) return G_TENSOR_BOUNDS;
+    uint64_t skip, o, len;
+    if (mul_ovf(start, t.row_bytes, &skip) || add_ovf(t.offset, skip, &o) || mul_ovf(count, t.row_bytes, &len))
+        return G_OVERFLOW;
+    *off = o;
+    *n = len;
+    return G_OK;
+}
+
+// Tensor::expert (frontier_gguf.rs:95-98): the rows of expert `id` of a
+// rank-3 [n, rows, experts] tensor.
+static int tensor_expert(const TensorInfo& t, uint64_t id, uint64_t* off, uint64_t* n) {
+    if (t.rank != 3 || id >= t.dims[2]) return G_SHAPE;
+    uint64_t start;
+    if (mul_ovf(id, t.dims[1], &start)) return G_OVERFLOW;
+    return tensor_rows(t, start, t.dims[1], off, n);
+}
+
+int uq_gguf_tensor_rows(uq_gguf_t g, int64_t index, uint64_t start, uint64_t count, uint64_t* offset, uint64_t* bytes,
+                        int* gguf_error) {
+    if (gguf_error) *gguf_error = 0;
+    if (!g || index < 0 || index >= (int64_t)g->tensors.size() || !offset || !bytes)
+        return uq::set_error(UQ_ERR_ARG, "gguf_tensor_rows: bad handle, index or pointer");
+    if (int e = tensor_rows(g->tensors[(size_t)index], start, count, offset, bytes))
+        return fail_gguf(e, gguf_error, "gguf_tensor_rows");
+    return UQ_OK;
+}
+
+int uq_gguf_tensor_expert(uq_gguf_t g, int64_t index, uint32_t expert, uint64_t* offset, uint64_t* bytes,
+                          int* gguf_error) {
+    if (gguf_error) *gguf_error = 0;
+    if (!g || index < 0 || index >= (int64_t)g->tensors.size() || !offset || !bytes)
+        return uq::set_error(UQ_ERR_ARG, "gguf_tensor_expert: bad handle, index or pointer");
+    if (int e = tensor_expert(g->tensors[(size_t)index], expert, offset, bytes))
+        return fail_gguf(e, gguf_error, "gguf_tensor_expert");
+    return UQ_OK;
+}
+
+}  // extern "C"
+
+// ModelIndex (frontier_gguf.rs:101-137): the directories of every split file
+// of one model, ordered by split.no. The shard handles stay the caller's.
+struct uq_gguf_index {
+    std::vector<uq_gguf_t> shards;
+};
+
+extern "C" {
+
+int uq_gguf_index_create(const uq_gguf_t* shards, int count, uq_gguf_index_t* out, int* gguf_error) {
+    if (gguf_error) *gguf_error = 0;
+    if (!out || (count > 0 && !shards)) return uq::set_error(UQ_ERR_ARG, "gguf_index_create: null pointer");
+    *out = nullptr;
+    if (count <= 0) return fail_gguf(G_SPLIT, gguf_error, "gguf_index_create");
+    std::vector<uq_gguf_t> v(shards, shards + count);
+    for (uq_gguf_t g : v)
+        if (!g) return uq::set_error(UQ_ERR_ARG, "gguf_index_create: null shard");
+    std::sort(v.begin(), v.end(), [](uq_gguf_t a, uq_gguf_t b) { return a->split_no < b->split_no; });
+    const uint64_t total = v[0]->total_tensors, n = (uint64_t)count;
+    std::set<std::string> names;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (v[i]->split_no != i || v[i]->split_count != n || v[i]->total_tensors != total)
+            return fail_gguf(G_SPLIT, gguf_error, "gguf_index_create");
+        for (const auto& t : v[i]->tensors)
+            if (!names.insert(t.name).second) return fail_gguf(G_DUPLICATE, gguf_error, "gguf_index_create");
+    }
+    if ((uint64_t)names.size() != total) return fail_gguf(G_SPLIT, gguf_error, "gguf_index_create");
+    *out = new uq_gguf_index{std::move(v)};
+    return UQ_OK;
+}
+
+int uq_gguf_index_free(uq_gguf_index_t ix) {
+    delete ix;
+    return UQ_OK;
+}
+
+int uq_gguf_index_shard_count(uq_gguf_index_t ix) { return ix ? (int)ix->shards.size() : UQ_ERR_ARG; }
+
+uq_gguf_t uq_gguf_index_shard(uq_gguf_index_t ix, int i) {
+    return ix && i >= 0 && i < (int)ix->shards.size() ? ix->shards[(size_t)i] : nullptr;
+}
+
+int uq_gguf_index_find(uq_gguf_index_t ix, const char* name, int* shard, int64_t* index, int* gguf_error) {
+    if (gguf_error) *gguf_error = 0;
+    if (!ix || !name || !shard || !index) return uq::set_error(UQ_ERR_ARG, "gguf_index_find: null pointer");
+    for (size_t i = 0; i < ix->shards.size(); i++) {
+        const int64_t t = uq_gguf_find_tensor(ix->shards[i], name);
+        if (t >= 0) {
+            *shard = (int)i;
+            *index = t;
+            return UQ_OK;
+        }
+    }
+    return fail_gguf(G_MISSING, gguf_error, (std::string("gguf_index_find ") + name).c_str());
+}
+
+int uq_gguf_index_inventory(uq_gguf_index_t ix, uint64_t* bytes3, int* gguf_error) {
+    if (gguf_error) *gguf_error = 0;
+    if (!ix || !bytes3) return uq::set_error(UQ_ERR_ARG, "gguf_index_inventory: null pointer");
+    uint64_t c[3] = {0, 0, 0};
+    for (uq_gguf_t g : ix->shards)
+        for (const auto& t : g->tensors) {
+            const size_t L = t.name.size();
+            const int k = t.name == "per_layer_token_embd.weight"
+                              ? 1
+                              : (L >= 12 && t.name.compare(L - 12, 12, "_exps.weight") == 0 ? 2 : 0);
+            if (add_ovf(c[k], t.bytes, &c[k])) return fail_gguf(G_OVERFLOW, gguf_error, "gguf_index_inventory");
+        }
+    for (int k = 0; k < 3; k++) bytes3[k] = c[k];
+    return UQ_OK;
+}
+
+int uq_gguf_load_weight(uq_gguf_t g, int64_t index, int32_t expert, uq_weight_t* out) {
+    if (!g || !out || index < 0 || index >= (int64_t)g->tensors.size())
+        return uq::set_error(UQ_ERR_ARG, "gguf_load_weight: bad handle or index");
+    if (g->path.empty()) return uq::set_error(UQ_ERR_ARG, "gguf_load_weight: the GGUF handle was not opened from a file");
+    const TensorInfo& t = g->tensors[(size_t)index];
+    uint64_t off, n;
+    int e = expert < 0 ? tensor_rows(t, 0, t.bytes / t.row_bytes, &off, &n) : tensor_expert(t, (uint64_t)expert, &off, &n);
+    if (e) return fail_gguf(e, nullptr, "gguf_load_weight");
+    if (expert < 0 && t.rank > 2) return uq::set_error(UQ_ERR_SHAPE, "gguf_load_weight: rank-3 tensor needs an expert id");
+    std::vector<uint8_t> buf((size_t)n);
+    if (int rc = read_at(g->path, off, n, buf.data())) return rc;
+    return uq_weight_upload(t.kind, (int64_t)t.dims[0], (int64_t)(n / t.row_bytes), buf.data(), buf.size(), out);
+}
+
+// The expert bank of one MoE layer from a split model: the rank-3
+// blk.L.ffn_{gate,up,down}_exps.weight tensors ([dim, ff, experts] and
+// [ff, dim, experts]) expert by expert (Tensor::expert), then the shared
+// expert blk.L.ffn_{gate,up,down}_shexp.weight and its optional f32 gate
+// blk.L.ffn_gate_inp_shexp.weight -- the tensors Backend::expert streams
+// (frontier_backend.rs:98-128), here made resident once. Before reading,
+// the bank's bytes are checked against the free HBM of the device (twice,
+// for the verified upload's staging).
+int uq_moe_load_gguf(uq_moe_t m, uq_gguf_index_t ix, int32_t layer) {
+    if (!m || !ix || layer < 0) return uq::set_error(UQ_ERR_ARG, "moe_load_gguf: bad arguments");
+    int32_t D, Fd, E, K;
+    uint32_t kind;
+    if (int rc = uq_moe_info(m, &D, &Fd, &E, &K, &kind)) return rc;
+    struct Found { uq_gguf_t g = nullptr; const TensorInfo* t = nullptr; };
+    auto find = [&](const std::string& name, bool required, Found* f) -> int {
+        int sh = 0;
+        int64_t ti = 0;
+        if (uq_gguf_index_find(ix, name.c_str(), &sh, &ti, nullptr) != UQ_OK) {
+            if (!required) return UQ_OK;
+            return uq::set_error(UQ_ERR_FORMAT, "moe_load_gguf: " + name + " missing");
+        }
+        f->g = ix->shards[(size_t)sh];
+        f->t = &f->g->tensors[(size_t)ti];
+        if (f->g->path.empty()) return uq::set_error(UQ_ERR_ARG, "moe_load_gguf: shard not opened from a file");
+        return UQ_OK;
+    };
+    const std::string b = "blk." + std::to_string(layer) + ".ffn_";
+    Found eg, eu, ed, sg, su, sd, gi;
+    if (int rc = find(b + "gate_exps.weight", true, &eg)) return rc;
+    if (int rc = find(b + "up_exps.weight", true, &eu)) return rc;
+    if (int rc = find(b + "down_exps.weight", true, &ed)) return rc;
+    if (int rc = find(b + "gate_shexp.weight", true, &sg)) return rc;
+    if (int rc = find(b + "up_shexp.weight", true, &su)) return rc;
+    if (int rc = find(b + "down_shexp.weight", true, &sd)) return rc;
+    if (int rc = find(b + "gate_inp_shexp.weight", false, &gi)) return rc;
+    auto dims_are = [](const TensorInfo* t, int rank, uint64_t a, uint64_t b2, uint64_t c) {
+        return t->rank == rank && t->dims[0] == a && t->dims[1] == b2 && (rank < 3 || t->dims[2] == c);
+    };
+    for (const Found* f : {&eg, &eu, &ed})
+        if (f->t->kind != kind) return uq::set_error(UQ_ERR_QUANT_TYPE, "moe_load_gguf: " + f->t->name + " kind != bank kind");
+    if (!dims_are(eg.t, 3, D, Fd, E) || !dims_are(eu.t, 3, D, Fd, E) || !dims_are(ed.t, 3, Fd, D, E))
+        return uq::set_error(UQ_ERR_SHAPE, "moe_load_gguf: expert tensor shapes != the layer's dim/ff/experts");
+    const uint32_t skind = sg.t->kind;
+    if (su.t->kind != skind || sd.t->kind != skind) return uq::set_error(UQ_ERR_QUANT_TYPE, "moe_load_gguf: shared expert kinds differ");
+    if (!dims_are(sg.t, 2, D, Fd, 0) || !dims_are(su.t, 2, D, Fd, 0) || !dims_are(sd.t, 2, Fd, D, 0))
+        return uq::set_error(UQ_ERR_SHAPE, "moe_load_gguf: shared expert shapes != the layer's dim/ff");
+    if (gi.t && (gi.t->kind != 0 || gi.t->rank != 1 || gi.t->dims[0] != (uint64_t)D))
+        return uq::set_error(UQ_ERR_SHAPE, "moe_load_gguf: ffn_gate_inp_shexp must be f32 [dim]");
+    uint64_t need = 0;
+    for (const Found* f : {&eg, &eu, &ed, &sg, &su, &sd}) need += f->t->bytes;
+    size_t free_b = 0, total_b = 0;
+    if (int rc = uq_device_memory(&free_b, &total_b)) return rc;
+    if (2 * need > (uint64_t)free_b)
+        return uq::set_error(UQ_ERR_DEVICE, "moe_load_gguf: the layer's " + std::to_string(need) +
+                                                " expert bytes do not fit the free HBM (" + std::to_string(free_b) + ")");
+    auto read_all = [&](const Found& f, std::vector<uint8_t>* buf) -> int {
+        buf->resize((size_t)f.t->bytes);
+        return read_at(f.g->path, f.t->offset, f.t->bytes, buf->data());
+    };
+    std::vector<uint8_t> bg, bu, bd;
+    if (int rc = read_all(eg, &bg)) return rc;
+    if (int rc = read_all(eu, &bu)) return rc;
+    if (int rc = read_all(ed, &bd)) return rc;
+    for (int32_t e = 0; e < E; e++) {
+        uint64_t og, ng, ou, nu, od, nd;
+        if (tensor_expert(*eg.t, (uint64_t)e, &og, &ng) || tensor_expert(*eu.t, (uint64_t)e, &ou, &nu) ||
+            tensor_expert(*ed.t, (uint64_t)e, &od, &nd))
+            return uq::set_error(UQ_ERR_FORMAT, "moe_load_gguf: expert range");
+        if (int rc = uq_moe_set_expert(m, e, bg.data() + (og - eg.t->offset), bu.data() + (ou - eu.t->offset),
+                                       bd.data() + (od - ed.t->offset)))
+            return rc;
+    }
+    std::vector<uint8_t> sbg, sbu, sbd, sgi;
+    if (int rc = read_all(sg, &sbg)) return rc;
+    if (int rc = read_all(su, &sbu)) return rc;
+    if (int rc = read_all(sd, &sbd)) return rc;
+    if (gi.t)
+        if (int rc = read_all(gi, &sgi)) return rc;
+    return uq_moe_set_shared(m, skind, sbg.data(), sbu.data(), sbd.data(), gi.t ? (const float*)sgi.data() : nullptr);
 }
 
 // Tensors of a Qwen2 decoder by GGUF name. output.weight falls back to

@@ -423,6 +423,16 @@ int uq_moe_create(int32_t dim, int32_t ff, int32_t experts, int32_t top_k, uint3
     return OK;
 }
 
+int uq_moe_info(uq_moe_t m, int32_t* dim, int32_t* ff, int32_t* experts, int32_t* top_k, uint32_t* expert_kind) {
+    if (!m) return set_error(ERR_ARG, "moe_info: null handle");
+    if (dim) *dim = m->D;
+    if (ff) *ff = m->F;
+    if (experts) *experts = m->E;
+    if (top_k) *top_k = m->K;
+    if (expert_kind) *expert_kind = m->kind;
+    return OK;
+}
+
 int uq_moe_free(uq_moe_t m) {
     if (!m) return OK;
     hipStreamSynchronize((hipStream_t)uq_stream());

@@ -168,6 +168,15 @@ int uq_sync(void) {
 
 int64_t uq_row_bytes(uint32_t kind, int64_t n) { return uq::row_bytes(kind, n); }
 
+int uq_device_memory(size_t* free_bytes, size_t* total_bytes) {
+    if (int rc = require_ctx()) return rc;
+    size_t f = 0, t = 0;
+    UQ_CHECK_HIP(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return OK;
+}
+
 }  // extern "C"
 
 namespace uq {

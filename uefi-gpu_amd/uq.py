@@ -136,6 +136,24 @@ _SIGS = {
     "uq_gguf_qwen2_config": (ctypes.c_int, [_vp, ctypes.c_int32, _vp]),
     "uq_gguf_meta_array_str": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_vp),
                                               ctypes.POINTER(ctypes.c_uint64)]),
+    "uq_gguf_tensor_rows": (ctypes.c_int, [_vp, _i64, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_tensor_expert": (ctypes.c_int, [_vp, _i64, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64),
+                                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_index_create": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.POINTER(_vp),
+                                            ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_index_free": (ctypes.c_int, [_vp]),
+    "uq_gguf_index_shard_count": (ctypes.c_int, [_vp]),
+    "uq_gguf_index_shard": (_vp, [_vp, ctypes.c_int]),
+    "uq_gguf_index_find": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_i64),
+                                          ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_index_inventory": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int)]),
+    "uq_gguf_load_weight": (ctypes.c_int, [_vp, _i64, ctypes.c_int32, ctypes.POINTER(_vp)]),
+    "uq_moe_load_gguf": (ctypes.c_int, [_vp, _vp, ctypes.c_int32]),
+    "uq_moe_info": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.POINTER(ctypes.c_uint32)]),
+    "uq_device_memory": (ctypes.c_int, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "uq_gguf_token_text": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]),
     "uq_generate": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p, ctypes.c_int, _c_u32p,
                                    ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
@@ -579,6 +597,19 @@ class MoeLayer:
         _check(lib().uq_moe_set_shared(h, cfg["shared_kind"], g.ctypes.data, u.ctypes.data, d.ctypes.data,
                                        None if gi is None else _p(gi, _c_f32p)))
 
+    @classmethod
+    def from_gguf(cls, cfg, index, layer):
+        """The layer's expert bank and shared expert read from a split model
+        (uq_moe_load_gguf over a GgufIndex)."""
+        self = cls.__new__(cls)
+        self.cfg = dict(cfg)
+        h = _vp()
+        _check(lib().uq_moe_create(cfg["dim"], cfg["ff"], cfg["experts"], cfg["top_k"], cfg["expert_kind"],
+                                   ctypes.byref(h)))
+        self.handle = h
+        _check(lib().uq_moe_load_gguf(h, index.handle, layer))
+        return self
+
     def ffn(self, x, logits):
         x = np.ascontiguousarray(x, np.float32)
         lg = np.ascontiguousarray(logits, np.float32)
@@ -625,6 +656,12 @@ class MoeLayer:
             self.free()
         except Exception:
             pass
+
+
+def device_memory():
+    f, t = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(lib().uq_device_memory(ctypes.byref(f), ctypes.byref(t)))
+    return f.value, t.value
 
 
 # ---------------------------------------------------------------- GGUF files
@@ -697,6 +734,32 @@ class Gguf:
                         "offset": off.value, "bytes": nb.value})
         return out
 
+    def _ranged(self, fn, *args):
+        off, n, ge = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_int(0)
+        rc = fn(self.handle, *args, ctypes.byref(off), ctypes.byref(n), ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        return off.value, n.value
+
+    def rows(self, index, start, count):
+        """Tensor::rows: (absolute offset, bytes) of `count` rows from `start`."""
+        return self._ranged(lib().uq_gguf_tensor_rows, index, start, count)
+
+    def expert(self, index, expert):
+        """Tensor::expert: (absolute offset, bytes) of one expert of a rank-3 tensor."""
+        return self._ranged(lib().uq_gguf_tensor_expert, index, expert)
+
+    def load_weight(self, index, expert=-1):
+        """The tensor (or one expert's rows) as a device Weight."""
+        t = self.tensors()[index]
+        h = _vp()
+        _check(lib().uq_gguf_load_weight(self.handle, index, expert, ctypes.byref(h)))
+        w = Weight.__new__(Weight)
+        w.kind, w.n = t["kind"], t["dims"][0]
+        w.m = (t["dims"][1] if expert >= 0 else int(np.prod(t["dims"][1:]))) if len(t["dims"]) > 1 else 1
+        w.handle = h
+        return w
+
     def find(self, name):
         return lib().uq_gguf_find_tensor(self.handle, name.encode())
 
@@ -745,3 +808,45 @@ class Gguf:
         c = Qwen2Config()
         _check(lib().uq_gguf_qwen2_config(self.handle, max_seq, ctypes.byref(c)))
         return c.as_dict()
+
+
+class GgufIndex:
+    """ModelIndex (frontier_gguf.rs:101-137) over the Gguf shards of one split
+    model; the shards must outlive the index."""
+
+    def __init__(self, shards):
+        self.shards_in = list(shards)
+        arr = (_vp * len(self.shards_in))(*[g.handle for g in self.shards_in])
+        h, ge = _vp(), ctypes.c_int(0)
+        rc = lib().uq_gguf_index_create(arr, len(self.shards_in), ctypes.byref(h), ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        self.handle = h
+        by_handle = {g.handle.value if hasattr(g.handle, "value") else g.handle: g for g in self.shards_in}
+        self.shards = [by_handle[lib().uq_gguf_index_shard(h, i)] for i in range(lib().uq_gguf_index_shard_count(h))]
+
+    def find(self, name):
+        """ModelIndex::tensor: (shard position in split order, tensor index)."""
+        sh, ix, ge = ctypes.c_int(), _i64(), ctypes.c_int(0)
+        rc = lib().uq_gguf_index_find(self.handle, name.encode(), ctypes.byref(sh), ctypes.byref(ix), ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        return sh.value, ix.value
+
+    def inventory(self):
+        out, ge = (ctypes.c_uint64 * 3)(), ctypes.c_int(0)
+        rc = lib().uq_gguf_index_inventory(self.handle, out, ctypes.byref(ge))
+        if rc != OK:
+            raise GgufError(rc, lib().uq_last_error().decode(errors="replace"), ge.value)
+        return list(out)
+
+    def free(self):
+        if getattr(self, "handle", None):
+            lib().uq_gguf_index_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

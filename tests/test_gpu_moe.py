@@ -28,8 +28,11 @@ def build(cfg, seed):
     return g, o
 
 
+# 128, 200 and 300 experts run the routing's rank with 4, 2 and 1 threads per expert
 @pytest.mark.parametrize("cfg,steps", [(uq.MOE_CONFIG, 16),
-                                       (dict(uq.MOE_CONFIG, dim=512, ff=256, experts=16, top_k=4), 8)])
+                                       (dict(uq.MOE_CONFIG, dim=512, ff=256, experts=16, top_k=4), 8),
+                                       (dict(uq.MOE_CONFIG, dim=512, ff=256, experts=200, top_k=8), 6),
+                                       (dict(uq.MOE_CONFIG, dim=512, ff=256, experts=300, top_k=16), 6)])
 def test_moe_matches_oracle(gpu, cfg, steps):
     g, o = build(cfg, 0x5EED0004)
     for step in range(steps):

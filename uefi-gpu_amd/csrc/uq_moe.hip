@@ -61,6 +61,7 @@ constexpr int GU_WG = 512;
 
 struct RouteLds {
     float p[MAX_EXPERTS];
+    int part[GU_WG];         // partial ranks of the 2nd..RQ-th thread of an expert
     int sid[MAX_TOPK];
     double red[GU_WG / 64];
     float redf[GU_WG / 64];
@@ -143,24 +144,45 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         if (e < E) L.p[e] = pe[j];  // each thread rewrites only its own entries
     }
     __syncthreads();
+    // stable ranks: RQ threads per expert (RQ = 4 up to 128 experts), each
+    // comparing against every RQ-th float4 of the probabilities with all of
+    // its LDS reads issued before the compares; partial counts meet in LDS
+    const int RQ = E4 <= GU_WG / 4 ? 4 : (E4 <= GU_WG / 2 ? 2 : 1);
     const float4* p4 = (const float4*)L.p;
+    for (int e0 = 0; e0 < E4; e0 += GU_WG / RQ) {
+        const int e = e0 + t % (GU_WG / RQ), q = t / (GU_WG / RQ);
+        const float v = e < E ? L.p[e] : 0.0f;
+        int rank = 0;
+        constexpr int CH = 8;  // float4 reads in flight
+        for (int c0 = q; c0 < E4 / 4; c0 += RQ * CH) {
+            float4 w[CH];
 #pragma unroll
-    for (int j = 0; j < GU_PE; j++) {
-        const int e = j * GU_WG + t;
-        if (e < E) {
-            const float v = pe[j];
-            int rank = 0;
-            // bitwise (not short-circuit) tests keep the loop branch-free
-#pragma unroll 4
-            for (int q = 0; q < E4 / 4; q++) {
-                const float4 w = p4[q];
-                const int i0 = 4 * q;
-                rank += (int)(w.x > v) | ((int)(w.x == v) & (int)(i0 < e));
-                rank += (int)(w.y > v) | ((int)(w.y == v) & (int)(i0 + 1 < e));
-                rank += (int)(w.z > v) | ((int)(w.z == v) & (int)(i0 + 2 < e));
-                rank += (int)(w.w > v) | ((int)(w.w == v) & (int)(i0 + 3 < e));
+            for (int u = 0; u < CH; u++) {
+                const int c = c0 + RQ * u;
+                w[u] = c < E4 / 4 ? p4[c] : make_float4(-1.0f, -1.0f, -1.0f, -1.0f);
             }
-            if (rank < a.top_k) L.sid[rank] = e;
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                // bitwise (not short-circuit) tests keep the loop branch-free;
+                // the -1 padding is never above a probability nor equal to one
+                const int i0 = 4 * (c0 + RQ * u);
+                rank += (int)(w[u].x > v) | ((int)(w[u].x == v) & (int)(i0 < e));
+                rank += (int)(w[u].y > v) | ((int)(w[u].y == v) & (int)(i0 + 1 < e));
+                rank += (int)(w[u].z > v) | ((int)(w[u].z == v) & (int)(i0 + 2 < e));
+                rank += (int)(w[u].w > v) | ((int)(w[u].w == v) & (int)(i0 + 3 < e));
+            }
+        }
+        if (RQ > 1) {
+            const int el = e % (GU_WG / RQ);
+            if (q > 0 && e < E) L.part[(q - 1) * (GU_WG / RQ) + el] = rank;
+            __syncthreads();
+            if (q == 0 && e < E) {
+                for (int k = 1; k < RQ; k++) rank += L.part[(k - 1) * (GU_WG / RQ) + el];
+                if (rank < a.top_k) L.sid[rank] = e;
+            }
+            __syncthreads();
+        } else if (e < E && rank < a.top_k) {
+            L.sid[rank] = e;
         }
     }
     return sum;
@@ -204,8 +226,11 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
     __shared__ float lxs[MAX_D / 32];
     __shared__ float ys[32];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = lane & 15, grp = lane >> 4;
+    // the shared expert's row blocks (the heaviest: Q8_0 rows) take the first
+    // block indices so that they are dispatched first; routed slots follow
     const int blocks = a.F / 32;
-    const int slot = blockIdx.x / blocks, rb = blockIdx.x % blocks;
+    const int bi = (int)blockIdx.x < blocks ? (int)blockIdx.x + a.top_k * blocks : (int)blockIdx.x - blocks;
+    const int slot = bi / blocks, rb = bi % blocks;
     const bool shared = slot == a.top_k;
     const int D = a.D;
     // logits and x up front; waves 1..7 quantize x (4 values per lane, a
@@ -252,7 +277,7 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
         const int ec = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
         GuLane<KR, NR> rl;
         rl.load(rg, ru, (int64_t)ec * a.F + srow, D / KR::UNIT, sub);
-        if (blockIdx.x == 0 && t == 0) {
+        if (bi == 0 && t == 0) {
             float tot = 0.0f;
             for (int k = 0; k < a.top_k; k++) tot = tot + L.p[L.sid[k]];
             if (!(sum > 0.0f) || !isfinite(sum) || !(tot > 0.0f)) bad = 1;

@@ -121,8 +121,9 @@ __global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q,
     if (miss) atomicAdd(bad, miss);
 }
 // Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, 12 packed scale bytes, d 2)
-// -> q[blk][96] = hmask|qs, sc[blk][16] = the sixteen 6-bit scales minus 32 as
-// signed bytes, d[blk]. The verify kernel packs the scales back to 12 bytes.
+// -> q[blk][96] = hmask with its bits permuted (Q3K::hpack) | qs, sc[blk][16] =
+// the sixteen 6-bit scales minus 32 as signed bytes, d[blk]. The verify kernel
+// undoes the permutation and packs the scales back to 12 bytes.
 __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
                                                    int8_t* __restrict__ q, int8_t* __restrict__ sc,
                                                    uint16_t* __restrict__ d) {
@@ -130,7 +131,12 @@ __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ s
     if (blk >= blocks) return;
     const uint8_t* p = src + blk * 110;
     uint8_t* dq = (uint8_t*)q + blk * 96;
-    for (int j = 0; j < 96; j++) dq[j] = p[j];
+    for (int j = 0; j < 32; j += 4) {
+        const uint32_t h = p[j] | (p[j + 1] << 8) | (p[j + 2] << 16) | ((uint32_t)p[j + 3] << 24);
+        const uint32_t r = Q3K::hpack(h);
+        for (int b = 0; b < 4; b++) dq[j + b] = (uint8_t)(r >> (8 * b));
+    }
+    for (int j = 32; j < 96; j++) dq[j] = p[j];
     for (int k = 0; k < 16; k++) sc[blk * 16 + k] = (int8_t)(Q3K::scale6_k(p + 96, k) - 32);
     d[blk] = (uint16_t)(p[108] | (p[109] << 8));
 }
@@ -141,7 +147,13 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
     if (blk >= blocks) return;
     const uint8_t* p = src + blk * 110;
     unsigned miss = 0;
-    for (int j = 0; j < 96; j++) miss += (uint8_t)q[blk * 96 + j] != p[j];
+    const uint8_t* qb = (const uint8_t*)q + blk * 96;
+    for (int j = 0; j < 32; j += 4) {
+        const uint32_t r = qb[j] | (qb[j + 1] << 8) | (qb[j + 2] << 16) | ((uint32_t)qb[j + 3] << 24);
+        const uint32_t h = Q3K::hunpack(r);
+        for (int b = 0; b < 4; b++) miss += (uint8_t)(h >> (8 * b)) != p[j + b];
+    }
+    for (int j = 32; j < 96; j++) miss += qb[j] != p[j];
     int v[16];
     for (int k = 0; k < 16; k++) {
         v[k] = sc[blk * 16 + k] + 32;
@@ -373,8 +385,8 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
         const int* xp = (const int*)x;
         for (int k = 0; k < 4; k++) {
             const unsigned qv = *(const unsigned*)(blk + 32 + 32 * n + 16 * h + 4 * k);
-            const unsigned hv = *(const unsigned*)(blk + 16 * h + 4 * k);
-            const int v = (int)(((qv >> (2 * j)) & 0x03030303u) | (((hv >> (4 * n + j)) & 0x01010101u) << 2));
+            const unsigned hv = *(const unsigned*)(blk + 16 * h + 4 * k);  // repacked hmask
+            const int v = (int)(((qv >> (2 * j)) & 0x03030303u) | (((hv >> Q3K::hpos(4 * n + j)) & 0x01010101u) << 2));
             c = uq_dot4(v, xp[k], c);
             c -= 4 * uq_dot4(0x01010101, xp[k], 0);
         }

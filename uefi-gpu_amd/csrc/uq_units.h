@@ -190,15 +190,38 @@ struct Q3K {
 #pragma unroll
         for (int k = 0; k < 8; k++) x.sx[k] = s16[8 * u + k];
     }
-    // low2 (bits 2j..2j+1 of each q byte) | hbit (bit 4n+j of each h byte) << 2:
-    // the h word is rotated so the bit lands on bit 2 of its byte
-    static UQ_DEV int v3(uint32_t q, uint32_t h, int sq, int rot) {
-        const uint32_t hb = __builtin_amdgcn_alignbit(h, h, rot) & 0x04040404u;
-        return (int)(((q >> sq) & 0x03030303u) | hb);
+    // The hmask plane is repacked at upload: GGUF bit 4n+j of a byte (the
+    // high bit of value 128n + 32j + l, l the byte index) moves to bit
+    // 2 + 2j + n for j < 3 and to bit n for j = 3, so that group j of unit n
+    // assembles from one AND of the (for unit 1 once-shifted) hmask word and
+    // one AND-OR with the 2-bit field, with the value scaled by GS[j] = 1, 4,
+    // 16 (j = 3: one more shift each side, scale 1).
+    static UQ_DEV int hpos(int b) { const int n = b >> 2, j = b & 3; return j < 3 ? 2 + 2 * j + n : n; }
+    static UQ_DEV uint32_t hpack(uint32_t h) {
+        uint32_t r = 0;
+        for (int b = 0; b < 8; b++) r |= ((h >> b) & 0x01010101u) << hpos(b);
+        return r;
     }
-    static UQ_DEV int4 extract(const int4& q, const int4& h, int sq, int rot) {
-        return make_int4(v3((uint32_t)q.x, (uint32_t)h.x, sq, rot), v3((uint32_t)q.y, (uint32_t)h.y, sq, rot),
-                         v3((uint32_t)q.z, (uint32_t)h.z, sq, rot), v3((uint32_t)q.w, (uint32_t)h.w, sq, rot));
+    static UQ_DEV uint32_t hunpack(uint32_t h) {
+        uint32_t r = 0;
+        for (int b = 0; b < 8; b++) r |= ((h >> hpos(b)) & 0x01010101u) << b;
+        return r;
+    }
+    template <int j>
+    static UQ_DEV uint32_t v3(uint32_t q, uint32_t hh) {
+        if (j == 0) return (q & 0x03030303u) | (hh & 0x04040404u);
+        if (j == 1) return (q & 0x0C0C0C0Cu) | (hh & 0x10101010u);
+        if (j == 2) return (q & 0x30303030u) | (hh & 0x40404040u);
+        return ((q >> 6) & 0x03030303u) | ((hh << 2) & 0x04040404u);
+    }
+    template <int j>
+    static UQ_DEV int4 extract(const int4& q, const int4& hh) {
+        return make_int4((int)v3<j>((uint32_t)q.x, (uint32_t)hh.x), (int)v3<j>((uint32_t)q.y, (uint32_t)hh.y),
+                         (int)v3<j>((uint32_t)q.z, (uint32_t)hh.z), (int)v3<j>((uint32_t)q.w, (uint32_t)hh.w));
+    }
+    static UQ_DEV int4 shr1(const int4& h) {
+        return make_int4((int)((uint32_t)h.x >> 1), (int)((uint32_t)h.y >> 1), (int)((uint32_t)h.z >> 1),
+                         (int)((uint32_t)h.w >> 1));
     }
     struct W { int4 h0, h1, q0, q1; uint32_t sc0, sc1; uint16_t d; };
     // row base pointers (nu = 2 * superblocks per row)
@@ -215,24 +238,31 @@ struct Q3K {
         return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sc.x, sc.y, r.d[sb]};
     }
     static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) { return load_u(row_ptr(w, row, nu), u); }
-    // d*(s-32) is exact in f32 (11-bit x 6-bit), so the block's
-    // (d*s0)*i0 + (d*s1)*i1 equals d*(s0*i0 + s1*i1) with an exact integer sum
+    // Group j of the unit: D = GS[j] * (sum of the 16 (value+4) x products)
+    // - 4 * GS[j] * sum(x), started from that correction (the accumulator of
+    // the first dot4); T = s0 * D0 + s1 * D1 = GS[j] * (s0 i0 + s1 i1) in
+    // 24-bit multiplies (|D| <= 16 * 16 * 4 * 127 < 2^23). d*(s-32) is exact
+    // in f32 (11-bit x 6-bit), so the block's (d*s0)*i0 + (d*s1)*i1 is
+    // d*(s0*i0 + s1*i1), and (d / GS[j]) * T is that same double exactly.
+    template <int j>
+    static UQ_DEV double group(const int4& q0, const int4& q1, const int4& hh0, const int4& hh1, uint32_t scw,
+                               const int4& xa, const int4& xb, int sa, int sb, double dd, double xsj) {
+        constexpr int GS = j == 1 ? 4 : (j == 2 ? 16 : 1);
+        const int4 w0 = extract<j>(q0, hh0), w1 = extract<j>(q1, hh1);
+        const int d0 = dot16(w0, xa, uq_mul24(sa, -4 * GS));
+        const int d1 = dot16(w1, xb, uq_mul24(sb, -4 * GS));
+        const int b = 16 * (j & 1);
+        const int t = uq_mul24((int)(int8_t)(scw >> b), d0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), d1);
+        return xsj * ((dd * (1.0 / GS)) * (double)t);
+    }
     static UQ_DEV double dot(const W& wv, const X& x, int u) {
         const int n = u & 1;
         const double dd = (double)uq_half(wv.d);
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int rot = (4 * n + j - 2) & 31;
-            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, rot), w1 = extract(wv.q1, wv.h1, 2 * j, rot);
-            const int i0 = dot16(w0, x.v[2 * j], 0) - 4 * x.sx[2 * j];
-            const int i1 = dot16(w1, x.v[2 * j + 1], 0) - 4 * x.sx[2 * j + 1];
-            const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
-            const int b = 16 * (j & 1);
-            // 24-bit multiplies (full rate): |s| <= 32, |i| <= 16 * 7 * 128
-            const int t = uq_mul24((int)(int8_t)(scw >> b), i0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), i1);
-            acc += x.s[j] * (dd * (double)t);
-        }
+        const int4 hh0 = n ? shr1(wv.h0) : wv.h0, hh1 = n ? shr1(wv.h1) : wv.h1;
+        double acc = group<0>(wv.q0, wv.q1, hh0, hh1, wv.sc0, x.v[0], x.v[1], x.sx[0], x.sx[1], dd, x.s[0]);
+        acc += group<1>(wv.q0, wv.q1, hh0, hh1, wv.sc0, x.v[2], x.v[3], x.sx[2], x.sx[3], dd, x.s[1]);
+        acc += group<2>(wv.q0, wv.q1, hh0, hh1, wv.sc1, x.v[4], x.v[5], x.sx[4], x.sx[5], dd, x.s[2]);
+        acc += group<3>(wv.q0, wv.q1, hh0, hh1, wv.sc1, x.v[6], x.v[7], x.sx[6], x.sx[7], dd, x.s[3]);
         return acc;
     }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
@@ -245,23 +275,20 @@ struct Q3K {
         const int n = u & 1;
         const double dd = (double)uq_half(wv.d);
         const int4* xv = (const int4*)(lx + (size_t)u * 128);
+        const int4 hh0 = n ? shr1(wv.h0) : wv.h0, hh1 = n ? shr1(wv.h1) : wv.h1;
         double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            asm volatile("" ::: "memory");
-            const int4 xa = xv[2 * j], xb = xv[2 * j + 1];
-            const int sa = ls16[8 * u + 2 * j], sb = ls16[8 * u + 2 * j + 1];
-            const double xsj = (double)lxs[4 * u + j];
-            const int rot = (4 * n + j - 2) & 31;
-            const int4 w0 = extract(wv.q0, wv.h0, 2 * j, rot), w1 = extract(wv.q1, wv.h1, 2 * j, rot);
-            const int i0 = dot16(w0, xa, 0) - 4 * sa;
-            const int i1 = dot16(w1, xb, 0) - 4 * sb;
-            const uint32_t scw = j < 2 ? wv.sc0 : wv.sc1;
-            const int b = 16 * (j & 1);
-            // 24-bit multiplies (full rate): |s| <= 32, |i| <= 16 * 7 * 128
-            const int t = uq_mul24((int)(int8_t)(scw >> b), i0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), i1);
-            acc += xsj * (dd * (double)t);
+#define UQ_Q3K_GROUP(J, SCW)                                                                                    \
+        {                                                                                                        \
+            asm volatile("" ::: "memory");                                                                       \
+            const int4 xa = xv[2 * J], xb = xv[2 * J + 1];                                                       \
+            const int sa = ls16[8 * u + 2 * J], sb = ls16[8 * u + 2 * J + 1];                                    \
+            acc += group<J>(wv.q0, wv.q1, hh0, hh1, SCW, xa, xb, sa, sb, dd, (double)lxs[4 * u + J]);            \
         }
+        UQ_Q3K_GROUP(0, wv.sc0)
+        UQ_Q3K_GROUP(1, wv.sc0)
+        UQ_Q3K_GROUP(2, wv.sc1)
+        UQ_Q3K_GROUP(3, wv.sc1)
+#undef UQ_Q3K_GROUP
         return acc;
     }
     // ggml Q3_K 6-bit scale k (0..15) of the 12 packed bytes b

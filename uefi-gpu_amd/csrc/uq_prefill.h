@@ -59,6 +59,7 @@ struct PfAttnArgs {
     int8_t* xq;
     float* xst;
     int mp;
+    int ncu;                 // set by the launcher: the CU count (workgroup pairing order)
 };
 
 void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float* dt, hipStream_t s);

@@ -389,9 +389,15 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
     constexpr int DT = HD / 64;    // 16-dim tiles per wave in P.V
     typedef double d4 __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
-    const int h = blockIdx.x, kh = h / (a.heads / a.kv_heads), kvd = a.kv_heads * HD;
-    // the longest query tiles (most keys) are dispatched first
-    const int tq0 = (gridDim.y - 1 - blockIdx.y) * PA_Q;
+    // Work rank r orders the (tile, head) pairs by descending key count. The
+    // first ncu workgroup ids take ranks 0.. (longest first, one per CU); the
+    // remaining ids take the shortest ranks first, so a CU's second resident
+    // workgroup is short where its first is long (the longest tile sets the
+    // kernel's duration: 2,048 FP64 MFMAs on the CU's four SIMDs)
+    const int L = blockIdx.y * gridDim.x + blockIdx.x, total = gridDim.x * gridDim.y;
+    const int r = L < a.ncu ? L : total - 1 - (L - a.ncu);
+    const int h = r % gridDim.x, kh = h / (a.heads / a.kv_heads), kvd = a.kv_heads * HD;
+    const int tq0 = (gridDim.y - 1 - r / gridDim.x) * PA_Q;
     const int nq = a.n - tq0 < PA_Q ? a.n - tq0 : PA_Q;  // live queries of the tile
     const int sst = (a.p0 + a.n + 15) & ~15;              // LDS row stride (keys)
     const int kend = a.p0 + tq0 + nq;                     // keys needed by the tile: [0, kend)
@@ -618,7 +624,9 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s) {
 void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_rope_kv, dim3(tokens), dim3(256), 0, s, a);
 }
-int launch_pf_attention(const PfAttnArgs& a, hipStream_t s) {
+int launch_pf_attention(const PfAttnArgs& a0, hipStream_t s) {
+    PfAttnArgs a = a0;
+    a.ncu = cu_count();
     const size_t sst = (size_t)((a.p0 + a.n + 15) & ~15);
     const size_t lds = sizeof(float) * PA_Q * sst;
     if (lds > 65536 || a.n <= 0 || a.p0 + a.n > a.kcap || a.heads % a.kv_heads) return -1;

@@ -402,6 +402,10 @@ def main():
     read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
     result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
                            "note": "plain int4 streaming read / copy of 1 GiB, same box"}
+    result["mfma_probe"] = {"int8_TOPS": round(uq.probe_mfma(0), 1), "fp16_TFLOPS": round(uq.probe_mfma(1), 1),
+                            "fp64_TFLOPS": round(uq.probe_mfma(2), 1),
+                            "note": "independent chains of v_mfma_i32_16x16x32_i8 / v_mfma_f32_16x16x32_f16 / "
+                                    "v_mfma_f64_16x16x4_f64 on register operands, 16 waves per CU, same box"}
     for w in weights:
         w.free()
     decode_state = {} if not args.no_cpu else None

@@ -210,6 +210,12 @@ int uq_time_matvec_tables(const uq_weight_t* ws, const int* pairs, int count, in
  * `reps` launches each, GB/s from HIP events. */
 int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_gbs);
 
+/* Matrix-core throughput probe (no reference counterpart; measurement aid):
+ * independent chains of one MFMA on register operands, 16 waves per CU, rate
+ * from HIP events. kind 0: v_mfma_i32_16x16x32_i8 (tera int8 ops/s), 1:
+ * v_mfma_f32_16x16x32_f16 (TFLOP/s), 2: v_mfma_f64_16x16x4_f64 (TFLOP/s). */
+int uq_probe_mfma(int kind, double* tera_ops);
+
 /* ---------------------------------------------------------------- Qwen2 dense decoder */
 /* Model shape constants of driver/src/llm.rs:314-321 (DIM, HIDDEN, KV, HEAD,
  * SEQ, LAYERS) as a runtime description. */

@@ -1,6 +1,7 @@
-// Bandwidth probes used by the benchmark: a plain streaming read and a plain
-// copy of a known number of bytes. They give the achievable HBM rate on the box
-// and the calibration of the FETCH_SIZE / WRITE_SIZE counters.
+// Probes used by the benchmark: a plain streaming read and a plain copy of a
+// known number of bytes (the achievable HBM rate on the box and the
+// calibration of the FETCH_SIZE / WRITE_SIZE counters), and matrix-core
+// throughput loops (the achievable int8 / fp16 / fp64 MFMA rates).
 #include "uq_internal.h"
 #include "../../include/uq.h"
 
@@ -26,6 +27,56 @@ __global__ __launch_bounds__(256) void k_probe_read(const int4* __restrict__ src
 __global__ __launch_bounds__(256) void k_probe_copy(const int4* __restrict__ src, int4* __restrict__ dst, int64_t n16) {
     const int64_t stride = (int64_t)gridDim.x * 256;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+// MFMA throughput: every wave runs PC independent accumulator chains of
+// `iters` dependent MFMAs on register operands. The sink store is never taken
+// (the accumulators of small integer or zero products never reach the
+// magic value) and only keeps the chains live.
+typedef int pv4i __attribute__((ext_vector_type(4)));
+typedef float pv4f __attribute__((ext_vector_type(4)));
+typedef double pv4d __attribute__((ext_vector_type(4)));
+typedef _Float16 pv8h __attribute__((ext_vector_type(8)));
+constexpr int PC = 8;
+__global__ __launch_bounds__(256) void k_probe_mfma_i8(int iters, int* __restrict__ sink) {
+    const long a = (long)(threadIdx.x & 7), b = (long)((threadIdx.x >> 3) & 7);
+    pv4i c[PC];
+#pragma unroll
+    for (int k = 0; k < PC; k++) c[k] = pv4i{0, 0, 0, 0};
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int k = 0; k < PC; k++) c[k] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c[k], 0, 0, 0);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+    if (s == 0x7fffffff) sink[blockIdx.x] = s;
+}
+__global__ __launch_bounds__(256) void k_probe_mfma_f16(int iters, int* __restrict__ sink) {
+    const _Float16 x = (_Float16)(float)(threadIdx.x & 3);
+    const pv8h a = {x, x, x, x, x, x, x, x}, b = a;
+    pv4f c[PC];
+#pragma unroll
+    for (int k = 0; k < PC; k++) c[k] = pv4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int k = 0; k < PC; k++) c[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c[k], 0, 0, 0);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+    if (s == -1.0f) sink[blockIdx.x] = 1;
+}
+__global__ __launch_bounds__(256) void k_probe_mfma_f64(int iters, int* __restrict__ sink) {
+    const double a = (double)(threadIdx.x & 3), b = (double)((threadIdx.x >> 2) & 3);
+    pv4d c[PC];
+#pragma unroll
+    for (int k = 0; k < PC; k++) c[k] = pv4d{0.0, 0.0, 0.0, 0.0};
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int k = 0; k < PC; k++) c[k] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c[k], 0, 0, 0);
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+    if (s == -1.0) sink[blockIdx.x] = 1;
 }
 
 }  // namespace
@@ -69,6 +120,40 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
     hipEventDestroy(e1);
     hipFree(a);
     hipFree(b);
+    hipFree(sink);
+    return OK;
+}
+
+int uq_probe_mfma(int kind, double* tera_ops) {
+    if (!uq_stream()) return set_error(ERR_ARG, "uq_init has not been called");
+    if (kind < 0 || kind > 2 || !tera_ops) return set_error(ERR_ARG, "probe_mfma: kind 0 (int8), 1 (fp16), 2 (fp64)");
+    hipStream_t s = (hipStream_t)uq_stream();
+    // ops per wave instruction: 2*16*16*32 (int8, fp16), 2*16*16*4 (fp64)
+    const double ops = kind == 2 ? 2.0 * 16 * 16 * 4 : 2.0 * 16 * 16 * 32;
+    const int iters = kind == 2 ? 256 : 2048;
+    const unsigned grid = 4u * (unsigned)cu_count();  // 16 waves per CU
+    int* sink = nullptr;
+    UQ_CHECK_HIP(hipMalloc(&sink, 4 * (size_t)grid));
+    auto launch = [&]() {
+        if (kind == 0) hipLaunchKernelGGL(k_probe_mfma_i8, dim3(grid), dim3(256), 0, s, iters, sink);
+        else if (kind == 1) hipLaunchKernelGGL(k_probe_mfma_f16, dim3(grid), dim3(256), 0, s, iters, sink);
+        else hipLaunchKernelGGL(k_probe_mfma_f64, dim3(grid), dim3(256), 0, s, iters, sink);
+    };
+    hipEvent_t e0, e1;
+    UQ_CHECK_HIP(hipEventCreate(&e0));
+    UQ_CHECK_HIP(hipEventCreate(&e1));
+    launch();
+    const int reps = 5;
+    UQ_CHECK_HIP(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; r++) launch();
+    UQ_CHECK_HIP(hipEventRecord(e1, s));
+    UQ_CHECK_HIP(hipEventSynchronize(e1));
+    float ms = 0;
+    UQ_CHECK_HIP(hipEventElapsedTime(&ms, e0, e1));
+    const double instrs = (double)grid * 4 * iters * PC * reps;
+    *tera_ops = instrs * ops / (ms / 1e3) / 1e12;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
     hipFree(sink);
     return OK;
 }

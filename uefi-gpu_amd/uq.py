@@ -106,6 +106,7 @@ _SIGS = {
     "uq_prompt_tokens": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p]),
     "uq_probe_bandwidth": (ctypes.c_int, [_i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double)]),
+    "uq_probe_mfma": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "uq_model_kv": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_uint16),
                                    ctypes.POINTER(ctypes.c_uint16)]),
     "uq_moe_create": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
@@ -350,6 +351,13 @@ def time_prefill_gemm(w, w2, tokens, reps):
     ms = ctypes.c_double()
     _check(lib().uq_time_prefill_gemm(w.handle, w2.handle if w2 else None, tokens, reps, ctypes.byref(ms)))
     return ms.value
+
+
+def probe_mfma(kind):
+    """Achievable matrix-core rate: kind 0 int8 (TOPS), 1 fp16, 2 fp64 (TFLOP/s)."""
+    t = ctypes.c_double()
+    _check(lib().uq_probe_mfma(kind, ctypes.byref(t)))
+    return t.value
 
 
 def probe_bandwidth(nbytes=1 << 30, reps=10):

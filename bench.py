@@ -412,6 +412,9 @@ def main():
     if not args.no_decode:
         result["decode"] = decode_bench(keep=decode_state)
         result["prefill_gemm"] = prefill_gemm_bench()
+        pg = result["prefill_gemm"]
+        pg["measured_16x16x32_peak_TOPS"] = result["mfma_probe"]["int8_TOPS"]
+        pg["frac_of_measured_peak"] = round(pg["aggregate_TOPS"] / result["mfma_probe"]["int8_TOPS"], 4)
         result["q4k_sweep"] = q4k_sweep()
         result["q3k_sweep"] = q3k_sweep()
         result["moe"] = moe_bench()

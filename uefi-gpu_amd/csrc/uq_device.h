@@ -16,6 +16,11 @@
 // s_waitcnt vmcnt(0): every vector-memory op this wave has issued (LDS DMA
 // included) has completed; expcnt and lgkmcnt are not waited on.
 UQ_DEV void uq_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Scalar read (s_load_dword, lgkmcnt) of a value that no thread of the running
+// kernel writes; the scalar cache starts every dispatch invalidated. Keeps such
+// reads out of the vector-memory counter, so they never wait behind (or hold
+// up) the weight stream.
+UQ_DEV int uq_sload(const int* p) { return *(const __attribute__((address_space(4))) int*)p; }
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
 // lane l's bytes land at lds_wave_base + 16*l; lds_wave_base is wave-uniform.
 typedef __attribute__((address_space(3))) void uq_lds_void;

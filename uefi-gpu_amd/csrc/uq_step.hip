@@ -63,38 +63,41 @@ __global__ __launch_bounds__(320) void k_qkv_rope(QkvArgs a) {
     if (wave == 4) nw.issue(a.nq, lx, lr, lg);
     uq_issue_barrier();
     if (wave == 4) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
-    Q8::W wv[NBL];
-#pragma unroll
-    for (int i = 0; i < NBL; i++) {
-        const int u = sub + 32 * i;
-        if (live && u < nu) wv[i] = Q8::load_w(w, rbase + (grp ? ib : ia), nu, u);
-    }
-    // position-dependent operands of lane 0, fetched before the prologue
-    const int pos = *a.pos;
+    // Row waves: the position (scalar read) and the pair's bias and RoPE
+    // operands first, then the weights. Every load is unconditional (unit
+    // index clamped) so none of them waits for another; the explicit wait
+    // costs nothing (these waves have no load in flight) and keeps the
+    // compiler's counts exact after wave 4's LDS-DMA branch.
+    const int pos = uq_sload(a.pos);
     float cs = 0.0f, sn = 0.0f, ba = 0.0f, bb = 0.0f;
-    if (live && lane == 0) {
+    Q8::W wv[NBL];
+    if (live) {
+        uq_wait_vm0();
         const float* bias = region == 0 ? a.bq : (region == 1 ? a.bk : a.bv);
         if (bias) {
             ba = bias[ia];
             bb = bias[ib];
         }
-        if (region != 2) {
-            cs = a.trig[(size_t)pos * hd + j];
-            sn = a.trig[(size_t)pos * hd + half + j];
+        cs = a.trig[(size_t)pos * hd + j];
+        sn = a.trig[(size_t)pos * hd + half + j];
+        const Q8::R r = Q8::row_ptr(w, rbase + (grp ? ib : ia), nu);
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int u = sub + 32 * i, uc = u < nu ? u : (int)nu - 1;
+            wv[i] = Q8::load_u(r, uc);
         }
     }
     __syncthreads();    // the quantized input in LDS
     if (!live) return;  // whole wave; no barrier follows
-    double acc = 0.0;
+    double acc = 0.0;  // never -0.0, so adding +0.0 for a clamped unit leaves it unchanged
 #pragma unroll
     for (int i = 0; i < NBL; i++) {
-        const int u = sub + 32 * i;
-        if (u < nu) {
-            Q8::X x;
-            x.a = *(const int4*)(sq + 16 * u);
-            x.s = ssc[u >> 1];
-            acc += Q8::dot(wv[i], x);
-        }
+        const int u = sub + 32 * i, uc = u < nu ? u : (int)nu - 1;
+        Q8::X x;
+        x.a = *(const int4*)(sq + 16 * uc);
+        x.s = ssc[uc >> 1];
+        const double t = Q8::dot(wv[i], x);
+        acc += u < nu ? t : 0.0;
     }
     const float y = (float)uq_group_sum<32>(acc);
     const float yb = __shfl(y, 32, 64);
@@ -257,14 +260,16 @@ template <int LPR, int NBL>
 __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t lq[MAX_DIM];
     __shared__ float ls[MAX_DIM / 32];
-    constexpr int RPW = 64 / LPR, RPB = RPW * 4, PER = MAX_DIM / 256;
+    // K <= min(LPR * NBL * 16, MAX_DIM) (the launcher's checks): PER accumulator values per thread
+    constexpr int PK = (LPR * NBL * Q8::UNIT + 255) / 256;
+    constexpr int RPW = 64 / LPR, RPB = RPW * 4, PER = PK < MAX_DIM / 256 ? PK : MAX_DIM / 256;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPR, grp = lane / LPR;
     const int64_t nu = a.k / Q8::UNIT, K = a.k;
-    double av[PER];
+    double av[PER];  // index clamped: all PER loads issue back to back
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int i = j * 256 + tid;
-        av[j] = i < K ? a.acc[i] : 0.0;
+        av[j] = a.acc[i < K ? i : K - 1];
     }
     const WArgs w{a.w_qs, a.w_d, nullptr};
     const RowSpan sp = row_span<RPB>(a.rows, a.share);
@@ -399,12 +404,19 @@ __global__ __launch_bounds__(1024) void k_down_h(DownArgs a) {
     uq_issue_barrier();  // h's loads are queued before any weight load of this CU
     Q8::W wv[NBL];
     if (wave < RW) {
-        const WArgs w{a.w_qs, a.w_d, nullptr};
+        // no load of these waves is in flight: the wait is free and keeps the
+        // compiler's counts exact after the LDS-DMA branch above
+        uq_wait_vm0();
+        const Q8::R r = Q8::row_ptr(WArgs{a.w_qs, a.w_d, nullptr}, rr, nu);
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int u = lane + 64 * i, uc = u < nu ? u : (int)nu - 1;
-            wv[i] = Q8::load_w(w, rr, nu, uc);
+            wv[i] = Q8::load_u(r, uc);
         }
+        // the scale conversions stay below the last load: here the compiler
+        // waits with vmcnt(0) for a single value, which would split the
+        // loads into serial batches
+        __builtin_amdgcn_sched_barrier(0);
     } else {
         uq_wait_vm0();
         asm volatile("" ::: "memory");

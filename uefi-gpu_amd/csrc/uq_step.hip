@@ -206,11 +206,25 @@ __global__ __launch_bounds__(AS_WG) void k_att_pv(AttSplitArgs a) {
 #pragma unroll
     for (int j = 0; j < ATT_SPLIT; j++) mx = fmaxf(mx, a.cmax[h * ATT_SPLIT + j]);
     const float* sc = a.scores + (size_t)h * a.max_seq;
-    double tot = 0.0;
-    for (int t = tid; t < T; t += AS_WG) {
-        const float ev = uq_expf(sc[t] - mx);
-        es[t] = ev;
-        tot += (double)ev;
+    double tot = 0.0;  // per thread in position order tid, tid + AS_WG, ...
+    for (int t0 = 0; t0 < T; t0 += 4 * AS_WG) {
+        float sv[4];  // four scores in flight per thread (index clamped, loads unconditional)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = t0 + u * AS_WG + tid;
+            sv[u] = sc[t < T ? t : T - 1];
+        }
+        float ev[4];  // formed unconditionally, so no load is sunk into the guarded branch
+#pragma unroll
+        for (int u = 0; u < 4; u++) ev[u] = uq_expf(sv[u] - mx);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = t0 + u * AS_WG + tid;
+            if (t < T) {
+                es[t] = ev[u];
+                tot += (double)ev[u];
+            }
+        }
     }
     tot = block_sum_d<AS_WG>(tot, red_d);  // its barriers also publish es
     const float total = (float)tot;

@@ -158,7 +158,7 @@ struct NormQuantWave {
         uq_wait_vm0();
         asm volatile("" ::: "memory");
         float xv[NC][4];
-        double ss = 0.0;
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};  // four chains of exact double terms
 #pragma unroll
         for (int j = 0; j < NC; j++) {
             const int i = 256 * j + 4 * lane;
@@ -186,34 +186,47 @@ struct NormQuantWave {
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     const float sq = xv[j][c] * xv[j][c];
-                    ss += (double)sq;
+                    s4[c] += (double)sq;
                 }
             } else {
 #pragma unroll
                 for (int c = 0; c < 4; c++) xv[j][c] = 0.0f;
             }
         }
-        ss = uq_group_sum<64>(ss);
+        const double ss = uq_group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
         const float mean = (float)(ss / (double)D);
         const float scale = 1.0f / sqrtf(mean + a.eps);
+        // the quant of uq_quant4_group8 for all NC blocks of a lane at once:
+        // block maxima, then the divisions spread over each 8-lane group
+        float y[NC][4], am[NC];
 #pragma unroll
         for (int j = 0; j < NC; j++) {
-            const int i = 256 * j + 4 * lane;
             const float4 g4 = ((const float4*)lg)[64 * j + lane];
             const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
-            float y[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const float tmp = xv[j][c] * scale;
-                y[c] = tmp * gg[c];
+                y[j][c] = tmp * gg[c];
             }
             // lanes past dim hold zeros and form whole 8-lane groups
-            uint32_t packed;
-            const float sc = uq_quant4_group8(y, &packed);
-            if (i < D) {
-                *(uint32_t*)(q + i) = packed;
-                if ((lane & 7) == 0) s[i >> 5] = sc;
-            }
+            const float m = fmaxf(fmaxf(fabsf(y[j][0]), fabsf(y[j][1])), fmaxf(fabsf(y[j][2]), fabsf(y[j][3])));
+            am[j] = uq_group_max<8>(m);
+        }
+        float inv[NC], sc[(NC + 7) / 8];
+        uq_block_recips<NC, 8>(am, inv, sc);
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int i = 256 * j + 4 * lane;
+            uint32_t packed = 0;
+#pragma unroll
+            for (int c = 0; c < 4; c++) packed |= uq_quant_code(y[j][c], inv[j]) << (8 * c);
+            if (i < D) *(uint32_t*)(q + i) = packed;
+        }
+        // lane 8g + r holds the scales of blocks j = r, r + 8, ...: block 8j + g of the row
+#pragma unroll
+        for (int k = 0; k < (NC + 7) / 8; k++) {
+            const int j = (lane & 7) + 8 * k, i = 256 * j + 32 * (lane >> 3);
+            if (j < NC && i < D) s[i >> 5] = sc[k];
         }
     }
 };

@@ -221,6 +221,31 @@ UQ_DEV uint32_t uq_quant_code(float v, float inv) {
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (uint32_t)(uint8_t)(int8_t)(int)r;
 }
+// 127/amax and amax/127 of NB blocks, each block spread over a G-lane group
+// whose lanes all hold its amax (after uq_group_max<G>). An IEEE division
+// sequence holds VCC, so the divisions of one lane run one after another;
+// here lane r of a group divides for blocks r, r + G, ... and the group's
+// lanes run them side by side. Every lane then takes 127/amax of all NB
+// blocks back by ds_bpermute. sc[k] is the scale of block r + k*G (meaningful
+// where r + k*G < NB). The same operations as uq_quant4_group8 /
+// uq_quant_lane per block, so the same bits.
+template <int NB, int G>
+UQ_DEV void uq_block_recips(const float (&amax)[NB], float (&inv)[NB], float (&sc)[(NB + G - 1) / G]) {
+    constexpr int NK = (NB + G - 1) / G;
+    const int lane = threadIdx.x & 63, r = lane & (G - 1), base = lane & ~(G - 1);
+    float iv[NK];
+#pragma unroll
+    for (int k = 0; k < NK; k++) {
+        float a = amax[k * G];
+#pragma unroll
+        for (int j = 1; j < G; j++)
+            if (k * G + j < NB) a = r == j ? amax[k * G + j] : a;
+        iv[k] = a > 0.0f ? 127.0f / a : 0.0f;
+        sc[k] = a / 127.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++) inv[j] = __shfl(iv[j / G], base + j % G, 64);
+}
 UQ_DEV float uq_quant4_group8(const float v[4], uint32_t* packed) {
     float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     a = uq_group_max<8>(a);

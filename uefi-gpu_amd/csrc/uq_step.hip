@@ -297,14 +297,27 @@ __global__ __launch_bounds__(256) void k_wo_acc(WoArgs a) {
             wv[i] = Q8::load_w(w, rr, nu, uc);
         }
     }
+    {
+        // uq_quant_lane for the PER blocks of a lane at once: block maxima,
+        // then the divisions spread over each 32-lane group (K % 32 == 0, so
+        // a block's lanes are all in range or all out of it)
+        float v[PER], am[PER], inv[PER], sc[(PER + 31) / 32];
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int i = j * 256 + tid;
-        if (i < K) {
-            float sc;
-            const int8_t q = uq_quant_lane((float)av[j], &sc);
-            lq[i] = q;
-            if ((tid & 31) == 0) ls[i >> 5] = sc;
+        for (int j = 0; j < PER; j++) {
+            v[j] = (float)av[j];
+            am[j] = uq_group_max<32>(fabsf(v[j]));
+        }
+        uq_block_recips<PER, 32>(am, inv, sc);
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int i = j * 256 + tid;
+            if (i < K) lq[i] = (int8_t)uq_quant_code(v[j], inv[j]);
+        }
+        // lane r of a 32-lane group holds the scales of its blocks j = r, r + 32, ...
+#pragma unroll
+        for (int k = 0; k < (PER + 31) / 32; k++) {
+            const int j = (tid & 31) + 32 * k, i = j * 256 + (tid & ~31);
+            if (j < PER && i < K) ls[i >> 5] = sc[k];
         }
     }
     __syncthreads();

@@ -376,7 +376,12 @@ __global__ __launch_bounds__(GH_NW * 64) void k_gateup_h(GateArgs a) {
     const WArgs wg{a.g_qs, a.g_d, nullptr}, wu{a.u_qs, a.u_d, nullptr};
     NormQuantWave<NC> nw;
     if (wave == GH_NW - 1) nw.issue(a.nq, lx, lr, lg);
-    uq_issue_barrier();  // the prologue's loads are queued before any weight load of this workgroup
+    // The prologue's loads land before this workgroup issues a weight load:
+    // a CU holds four of these workgroups, and the last one dispatched would
+    // otherwise find its prologue loads queued behind the other three
+    // workgroups' weight streams (its prologue ending ~4 us late).
+    if (wave == GH_NW - 1) uq_wait_vm0();
+    uq_issue_barrier();
     if (wave == GH_NW - 1) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
     Q8::W gw[NBL], uw[NBL];
     if (rows_wave) {

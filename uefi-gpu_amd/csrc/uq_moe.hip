@@ -97,9 +97,10 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         const int e = j * GU_WG + t;
         if (e < E) L.p[e] = uq_expf(lg[j] - mx);
     }
-    // entries past E hold -1: never above a score, never equal to one
-    const int E4 = (E + 3) & ~3;
-    if (t < E4 - E) L.p[E + t] = -1.0f;
+    // entries past E hold -1: never above a score, never equal to one (up to
+    // GU_WG / 4 entries at least, the table the fast rank path below reads)
+    const int E4 = (E + 3) & ~3, EP = E4 > GU_WG / 4 ? E4 : GU_WG / 4;
+    if (t < EP - E) L.p[E + t] = -1.0f;
     // with a NaN score no rank is unique; the slots then keep ids 0..k-1 and
     // the status flag reports the input
     if (t < a.top_k) L.sid[t] = t;
@@ -147,8 +148,37 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
     // stable ranks: RQ threads per expert (RQ = 4 up to 128 experts), each
     // comparing against every RQ-th float4 of the probabilities with all of
     // its LDS reads issued before the compares; partial counts meet in LDS
-    const int RQ = E4 <= GU_WG / 4 ? 4 : (E4 <= GU_WG / 2 ? 2 : 1);
     const float4* p4 = (const float4*)L.p;
+    if (E4 <= GU_WG / 4) {
+        // up to GU_WG / 4 experts: the same four-thread split with compile-time
+        // bounds; every thread reads its eight float4 of the padded table
+        // unconditionally, so the reads go out together
+        constexpr int NE = GU_WG / 4;
+        const int e = t % NE, q = t / NE;
+        const float v = L.p[e];
+        int rank = 0;
+        float4 w[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) w[u] = p4[q + 4 * u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i0 = 4 * (q + 4 * u);
+            rank += (int)(w[u].x > v) | ((int)(w[u].x == v) & (int)(i0 < e));
+            rank += (int)(w[u].y > v) | ((int)(w[u].y == v) & (int)(i0 + 1 < e));
+            rank += (int)(w[u].z > v) | ((int)(w[u].z == v) & (int)(i0 + 2 < e));
+            rank += (int)(w[u].w > v) | ((int)(w[u].w == v) & (int)(i0 + 3 < e));
+        }
+        if (q > 0) L.part[(q - 1) * NE + e] = rank;
+        __syncthreads();
+        if (q == 0 && e < E) {
+#pragma unroll
+            for (int k = 1; k < 4; k++) rank += L.part[(k - 1) * NE + e];
+            if (rank < a.top_k) L.sid[rank] = e;
+        }
+        __syncthreads();
+        return sum;
+    }
+    const int RQ = E4 <= GU_WG / 2 ? 2 : 1;
     for (int e0 = 0; e0 < E4; e0 += GU_WG / RQ) {
         const int e = e0 + t % (GU_WG / RQ), q = t / (GU_WG / RQ);
         const float v = e < E ? L.p[e] : 0.0f;

@@ -73,15 +73,18 @@ struct RouteLds {
 // max subtraction and an f32 running sum in expert order; stable top-k (score
 // descending, id ascending).
 
-// Routing by the whole workgroup, GU_PE experts per thread, five barriers:
-// max (DPP per wave, then across waves), exps to LDS, the f32 running sum in
-// expert order by lane 0 of wave 0 (eight float4 LDS reads in flight) while
-// waves 1.. run `side` (the input quant), p = e / sum in place, stable ranks
-// against LDS broadcast reads. Leaves p in L.p and the top-k ids in L.sid.
+// Routing by the whole workgroup, GU_PE experts per thread, a barrier between
+// phases: max (DPP per wave, then across waves), exps to LDS, the f32 running
+// sum in expert order by lane 0 of wave 0 (eight float4 LDS reads in flight)
+// while waves 1.. run `side` (the input quant), p = e / sum in place, stable
+// ranks against LDS broadcast reads. Leaves p in L.p, the top-k ids in L.sid
+// and the OR of every thread's non-finite flag in L.bad, all published by the
+// barrier it ends on.
 constexpr int GU_PE = (MAX_EXPERTS + GU_WG - 1) / GU_WG;
 template <class Side>
 __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsigned& bad, Side side) {
     const int t = threadIdx.x, E = a.E;
+    if (t == 0) L.bad = 0u;  // published by the max's barriers
     float mx = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < GU_PE; j++) {
@@ -144,6 +147,9 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         pe[j] = e < E ? L.p[e] / sum : 0.0f;
         if (e < E) L.p[e] = pe[j];  // each thread rewrites only its own entries
     }
+    // every flag (logits in the max pass, the input in `side`) is final here;
+    // the caller reads L.bad after the last barrier below
+    if (bad) L.bad = 1u;
     __syncthreads();
     // stable ranks: RQ threads per expert (RQ = 4 up to 128 experts), each
     // comparing against every RQ-th float4 of the probabilities with all of
@@ -215,6 +221,7 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
             L.sid[rank] = e;
         }
     }
+    __syncthreads();
     return sum;
 }
 
@@ -298,8 +305,9 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
             }
         }
     };
+    // route_par ends on a barrier that publishes L.p / L.sid, lxq / lxs and L.bad
     const float sum = route_par(a, lg, L, bad, quant_x);
-    bad = __syncthreads_or(bad);  // publishes L.p / L.sid and lxq / lxs
+    bad = L.bad;
     float v;
     if (!shared) {
         // routed expert: its weight loads go out before anything else waits

@@ -231,6 +231,121 @@ struct NormQuantWave {
     }
 };
 
+// The same residual + RMSNorm + block-32 quant spread over all NW waves of a
+// workgroup, for kernels whose weight stream is short (every wave can load
+// and compute its share before its weights are needed): wave w takes the
+// 256-value chunks w, w + NW, ... . issue() loads them into registers with
+// plain loads, so a wave's weight loads issued afterwards keep exact vmcnt
+// waits; finish() sums the wave's squares, meets the other waves' partial
+// sums in LDS (part[NW], added in wave order in every wave) behind an LDS-only
+// barrier, and quantizes its own chunks (divisions spread as in
+// uq_block_recips). Per value the same operations as NormQuantWave. Every wave
+// of the workgroup calls both halves; the caller's barrier publishes q / s.
+template <int NC, int NW>
+struct NormQuantSplit {
+    static constexpr int PC = (NC + NW - 1) / NW;  // chunks per wave, at most
+    float4 xv[PC], rv[PC], gv[PC];
+    uint32_t e[PC];
+    uint16_t d[PC];
+
+    __device__ __forceinline__ void issue(const NormQuantArgs& a) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.dim;
+        const int64_t row = a.embed_qs ? (int64_t)(uint32_t)uq_sload((const int*)a.token) : 0;
+#pragma unroll
+        for (int k = 0; k < PC; k++) {
+            const int c = wave + NW * k, cc = c < NC ? c : NC - 1;
+            const int i = 256 * cc + 4 * lane, ic = i < D ? i : D - 4;
+            if (a.embed_qs) {
+                e[k] = *(const uint32_t*)(a.embed_qs + row * D + ic);
+                d[k] = a.embed_d[row * (D / 32) + ic / 32];
+            } else {
+                xv[k] = *(const float4*)(a.x + ic);
+                if (a.residual) rv[k] = *(const float4*)(a.residual + ic);
+            }
+            gv[k] = *(const float4*)(a.gamma + ic);
+        }
+    }
+
+    __device__ __forceinline__ void finish(const NormQuantArgs& a, bool write_x, double* part, int8_t* q,
+                                           float* s) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.dim;
+        float x[PC][4];
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int k = 0; k < PC; k++) {
+            const int c = wave + NW * k, i = 256 * c + 4 * lane;
+            if (a.embed_qs) {
+                const float dd = uq_half(d[k]);
+#pragma unroll
+                for (int m = 0; m < 4; m++) x[k][m] = dd * (float)(int8_t)(e[k] >> (8 * m));
+            } else {
+                x[k][0] = xv[k].x;
+                x[k][1] = xv[k].y;
+                x[k][2] = xv[k].z;
+                x[k][3] = xv[k].w;
+                if (a.residual) {
+                    x[k][0] = x[k][0] + rv[k].x;
+                    x[k][1] = x[k][1] + rv[k].y;
+                    x[k][2] = x[k][2] + rv[k].z;
+                    x[k][3] = x[k][3] + rv[k].w;
+                }
+            }
+            if (c < NC && i < D) {
+                if (write_x && a.x_out) *(float4*)(a.x_out + i) = make_float4(x[k][0], x[k][1], x[k][2], x[k][3]);
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const float sq = x[k][m] * x[k][m];
+                    s4[m] += (double)sq;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; m++) x[k][m] = 0.0f;
+            }
+        }
+        const double ws = uq_group_sum<64>((s4[0] + s4[1]) + (s4[2] + s4[3]));
+        if (lane == 0) part[wave] = ws;
+        // LDS-only barrier: the weight loads in flight are not waited for
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        double ss = part[0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) ss += part[w];
+        const float mean = (float)(ss / (double)D);
+        const float scale = 1.0f / sqrtf(mean + a.eps);
+        float y[PC][4], am[PC];
+#pragma unroll
+        for (int k = 0; k < PC; k++) {
+            const float gg[4] = {gv[k].x, gv[k].y, gv[k].z, gv[k].w};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const float tmp = x[k][m] * scale;
+                y[k][m] = tmp * gg[m];
+            }
+            // lanes past dim hold zeros and form whole 8-lane groups
+            const float mm = fmaxf(fmaxf(fabsf(y[k][0]), fabsf(y[k][1])), fmaxf(fabsf(y[k][2]), fabsf(y[k][3])));
+            am[k] = uq_group_max<8>(mm);
+        }
+        float inv[PC], sc[(PC + 7) / 8];
+        uq_block_recips<PC, 8>(am, inv, sc);
+#pragma unroll
+        for (int k = 0; k < PC; k++) {
+            const int c = wave + NW * k, i = 256 * c + 4 * lane;
+            uint32_t packed = 0;
+#pragma unroll
+            for (int m = 0; m < 4; m++) packed |= uq_quant_code(y[k][m], inv[k]) << (8 * m);
+            if (c < NC && i < D) *(uint32_t*)(q + i) = packed;
+        }
+        // lane 8g + r holds the scale of chunk r (r < PC): block 8c + g of the row
+#pragma unroll
+        for (int kk = 0; kk < (PC + 7) / 8; kk++) {
+            const int r = (lane & 7) + 8 * kk, c = wave + NW * r, i = 256 * c + 32 * (lane >> 3);
+            if (r < PC && c < NC && i < D) s[i >> 5] = sc[kk];
+        }
+    }
+};
+
 template <int WG>
 __device__ inline void norm_quant(const NormQuantArgs& a, bool write_x, int8_t* q, float* s, double* red,
                                   int sstride = 1) {

@@ -39,16 +39,19 @@ constexpr int MAX_DIM = 4096;
 template <int NBL>
 __global__ __launch_bounds__(320) void k_qkv_rope(QkvArgs a) {
     constexpr int NC = 2 * NBL < MAX_DIM / 256 ? 2 * NBL : MAX_DIM / 256;  // dim <= 32 lanes x NBL units x 16
-    __shared__ __attribute__((aligned(16))) float lx[NC * 256];
-    __shared__ __attribute__((aligned(16))) float lr[NC * 256];
-    __shared__ __attribute__((aligned(16))) float lg[NC * 256];
     __shared__ __attribute__((aligned(16))) int8_t sq[NC * 256];
     __shared__ float ssc[NC * 8];
+    __shared__ double part[5];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane & 31, grp = lane >> 5;
     const int hd = a.head_dim, half = hd / 2, kvd = a.kv_heads * hd;
-    const int nq = a.heads * half, nk = a.kv_heads * half;
-    const int pu = blockIdx.x * 4 + wave;
-    const bool live = wave < 4 && pu < nq + 2 * nk;
+    const int nq = a.heads * half, nk = a.kv_heads * half, npairs = nq + 2 * nk;
+    // waves 0..3 hold one row pair each; wave 4 (and a wave past the last
+    // pair) repeats the loads of the workgroup's first pair -- the same cache
+    // lines -- so that every wave issues the same loads with no branch, which
+    // keeps the waits of the prologue below exact
+    const int pw = blockIdx.x * 4 + (wave < 4 ? wave : 0);
+    const bool live = wave < 4 && pw < npairs;
+    const int pu = pw < npairs ? pw : npairs - 1;
     const int region = pu < nq ? 0 : (pu < nq + nk ? 1 : 2);
     const int p = region == 0 ? pu : (region == 1 ? pu - nq : pu - nq - nk);
     const int h = p / half, j = p % half;
@@ -56,30 +59,21 @@ __global__ __launch_bounds__(320) void k_qkv_rope(QkvArgs a) {
     const int rbase = region == 0 ? 0 : (region == 1 ? a.heads * hd : a.heads * hd + kvd);
     const int64_t nu = a.dim / Q8::UNIT;
     const WArgs w{a.w_qs, a.w_d, nullptr};
-    // Wave 4 holds no rows: it normalizes and quantizes the input (loads
-    // queued ahead of the weight loads by the issue barrier) while waves 0..3
-    // issue their row pairs' weight loads.
-    NormQuantWave<NC> nw;
-    if (wave == 4) nw.issue(a.nq, lx, lr, lg);
-    uq_issue_barrier();
-    if (wave == 4) nw.finish(a.nq, blockIdx.x == 0, lx, lr, lg, sq, ssc);
-    // Row waves: the position (scalar read) and the pair's bias and RoPE
-    // operands first, then the weights. Every load is unconditional (unit
-    // index clamped) so none of them waits for another; the explicit wait
-    // costs nothing (these waves have no load in flight) and keeps the
-    // compiler's counts exact after wave 4's LDS-DMA branch.
+    // The residual + RMSNorm + quant of the input is shared by all five waves
+    // (the weight stream of this kernel is short): each wave loads its chunks
+    // first, then the position (scalar read), its pair's bias and RoPE
+    // operands and its weights, then normalizes and quantizes its chunks while
+    // those loads are in flight.
+    NormQuantSplit<NC, 5> nw;
+    nw.issue(a.nq);
     const int pos = uq_sload(a.pos);
-    float cs = 0.0f, sn = 0.0f, ba = 0.0f, bb = 0.0f;
+    // without a bias the two loads read the RoPE table instead (never used)
+    const float* bias = region == 0 ? a.bq : (region == 1 ? a.bk : a.bv);
+    const float ba = *(bias ? bias + ia : a.trig), bb = *(bias ? bias + ib : a.trig);
+    const float cs = a.trig[(size_t)pos * hd + j];
+    const float sn = a.trig[(size_t)pos * hd + half + j];
     Q8::W wv[NBL];
-    if (live) {
-        uq_wait_vm0();
-        const float* bias = region == 0 ? a.bq : (region == 1 ? a.bk : a.bv);
-        if (bias) {
-            ba = bias[ia];
-            bb = bias[ib];
-        }
-        cs = a.trig[(size_t)pos * hd + j];
-        sn = a.trig[(size_t)pos * hd + half + j];
+    {
         const Q8::R r = Q8::row_ptr(w, rbase + (grp ? ib : ia), nu);
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
@@ -87,6 +81,7 @@ __global__ __launch_bounds__(320) void k_qkv_rope(QkvArgs a) {
             wv[i] = Q8::load_u(r, uc);
         }
     }
+    nw.finish(a.nq, blockIdx.x == 0, part, sq, ssc);
     __syncthreads();    // the quantized input in LDS
     if (!live) return;  // whole wave; no barrier follows
     double acc = 0.0;  // never -0.0, so adding +0.0 for a clamped unit leaves it unchanged

@@ -520,12 +520,23 @@ __global__ __launch_bounds__(256) void k_greedy_finish(LmArgs a, int parts) {
     int id = 0x7fffffff;
     unsigned bad = 0;
     const Cand* part = (const Cand*)a.partial;
-    for (int j = threadIdx.x; j < parts; j += 256) {
-        const Cand c = part[j];
-        bad |= c.bad;
-        if (better(c.v, c.id, best, id)) {
-            best = c.v;
-            id = c.id;
+    constexpr int PF = 8;  // partials in flight per thread (index clamped, loads unconditional)
+    for (int j0 = threadIdx.x; j0 < parts; j0 += 256 * PF) {
+        Cand c[PF];
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            const int j = j0 + 256 * u;
+            c[u] = part[j < parts ? j : parts - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            if (j0 + 256 * u < parts) {
+                bad |= c[u].bad;
+                if (better(c[u].v, c[u].id, best, id)) {
+                    best = c[u].v;
+                    id = c[u].id;
+                }
+            }
         }
     }
     cand_reduce(best, id, bad, vs, ids, bs);

@@ -134,17 +134,27 @@ __global__ __launch_bounds__(AS_WG) void k_att_scores(AttSplitArgs a) {
     const int lo = (int)((int64_t)s * T / ATT_SPLIT), hi = (int)((int64_t)(s + 1) * T / ATT_SPLIT);
     const int grp = tid / LP, c = tid % LP;
     if (s == 0 && tid < HD) a.acc[h * HD + tid] = 0.0;
-    double q8[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) q8[i] = (double)a.q[h * HD + 8 * c + i];
+    // q (raw) and the first batch of keys go out together; q is converted
+    // after, so the key loads do not wait for it. Positions past the chunk
+    // read a clamped row (position 0 exists for every T) and are masked below.
+    const float4 qa = *(const float4*)(a.q + h * HD + 8 * c), qb = *(const float4*)(a.q + h * HD + 8 * c + 4);
     const uint16_t* kb = a.kcache + kh * HD + 8 * c;
+    int4 kk[AS_B];
+#pragma unroll
+    for (int u = 0; u < AS_B; u++) {
+        const int t = lo + u * NG + grp, tc = t < hi ? t : (hi > lo ? hi - 1 : 0);
+        kk[u] = *(const int4*)(kb + (size_t)tc * kvd);
+    }
+    const double q8[8] = {(double)qa.x, (double)qa.y, (double)qa.z, (double)qa.w,
+                          (double)qb.x, (double)qb.y, (double)qb.z, (double)qb.w};
     float mx = -3.402823466e38f;
     for (int t0 = lo; t0 < hi; t0 += AS_B * NG) {
-        int4 kk[AS_B];
+        if (t0 > lo) {
 #pragma unroll
-        for (int u = 0; u < AS_B; u++) {
-            const int t = t0 + u * NG + grp;
-            kk[u] = t < hi ? *(const int4*)(kb + (size_t)t * kvd) : make_int4(0, 0, 0, 0);
+            for (int u = 0; u < AS_B; u++) {
+                const int t = t0 + u * NG + grp, tc = t < hi ? t : hi - 1;
+                kk[u] = *(const int4*)(kb + (size_t)tc * kvd);
+            }
         }
         double d[AS_B];
 #pragma unroll

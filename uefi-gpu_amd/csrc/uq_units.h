@@ -29,7 +29,6 @@ struct Q8 {
         x.a = *(const int4*)(xq + (size_t)u * 16);
         x.s = xs[u >> 1];
     }
-    static UQ_DEV void zero_x(X& x) { x.a = make_int4(0, 0, 0, 0); x.s = 0.0f; }
     struct W { int4 q; uint16_t d; };
     // row base pointers, formed once per row (nu is even: K % 32 == 0)
     struct R { const int8_t* q; const uint16_t* d; };
@@ -77,11 +76,6 @@ struct Q4K {
         x.s1 = (double)xs[2 * u + 1];
         x.xl = sum16(x.a1, sum16(x.a0, 0));
         x.xh = sum16(x.b1, sum16(x.b0, 0));
-    }
-    static UQ_DEV void zero_x(X& x) {
-        x.a0 = x.a1 = x.b0 = x.b1 = make_int4(0, 0, 0, 0);
-        x.s0 = x.s1 = 0.0;
-        x.xl = x.xh = 0;
     }
     // from an activation staged with its 16-value sums s16 (LDS)
     static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
@@ -174,12 +168,6 @@ struct Q3K {
         const int ones = 0x01010101;
 #pragma unroll
         for (int k = 0; k < 8; k++) x.sx[k] = dot16(make_int4(ones, ones, ones, ones), x.v[k], 0);
-    }
-    static UQ_DEV void zero_x(X& x) {
-#pragma unroll
-        for (int k = 0; k < 8; k++) { x.v[k] = make_int4(0, 0, 0, 0); x.sx[k] = 0; }
-#pragma unroll
-        for (int k = 0; k < 4; k++) x.s[k] = 0.0;
     }
     static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
         const int4* p = (const int4*)(xq + (size_t)u * 128);
@@ -331,8 +319,10 @@ __device__ __forceinline__ RowSpan row_span(int64_t rows, int64_t share) {
 }
 
 // Activation units of one lane (units sub, sub+LPR, ...) kept in registers.
-// Loads are issued unconditionally (a unit past the row end reads the last
-// unit) and zeroed afterwards, so they all go out before the first wait.
+// Loads are issued unconditionally: a unit past the row end reads the last
+// unit, and every consumer drops its term by a select on u < nu. (Zeroing
+// such units here would overwrite registers with loads in flight, which
+// makes the compiler wait for those loads before the weight loads go out.)
 template <class KQ, int LPR, int NBL>
 UQ_DEV void load_xr(typename KQ::X* xr, const int8_t* xq, const float* xs, int64_t nu, int sub) {
 #pragma unroll
@@ -340,9 +330,6 @@ UQ_DEV void load_xr(typename KQ::X* xr, const int8_t* xq, const float* xs, int64
         const int u = sub + LPR * i;
         KQ::load_x(xr[i], xq, xs, u < nu ? u : (int)nu - 1);
     }
-#pragma unroll
-    for (int i = 0; i < NBL; i++)
-        if (sub + LPR * i >= nu) KQ::zero_x(xr[i]);
 }
 // This lane's share of row `row`, summed over the LPR lanes of its group: all
 // units' weight loads first, then the dots (a unit past the row end loads

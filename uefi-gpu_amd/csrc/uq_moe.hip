@@ -61,30 +61,126 @@ constexpr int GU_WG = 512;
 
 struct RouteLds {
     float p[MAX_EXPERTS];
+    unsigned long long key[GU_WG / 4];  // rank keys of up to 128 experts
     int part[GU_WG];         // partial ranks of the 2nd..RQ-th thread of an expert
     int sid[MAX_TOPK];
     double red[GU_WG / 64];
     float redf[GU_WG / 64];
     float sum;
-    unsigned bad;
+    unsigned badw[GU_WG / 64];  // per wave: any non-finite input seen
 };
 
 // Routing arithmetic (the oracle's, frontier_forward.rs:47-51): softmax with
 // max subtraction and an f32 running sum in expert order; stable top-k (score
 // descending, id ascending).
 
-// Routing by the whole workgroup, GU_PE experts per thread, a barrier between
-// phases: max (DPP per wave, then across waves), exps to LDS, the f32 running
-// sum in expert order by lane 0 of wave 0 (eight float4 LDS reads in flight)
-// while waves 1.. run `side` (the input quant), p = e / sum in place, stable
-// ranks against LDS broadcast reads. Leaves p in L.p, the top-k ids in L.sid
-// and the OR of every thread's non-finite flag in L.bad, all published by the
-// barrier it ends on.
+// Routing by the whole workgroup. Up to 128 experts, wave 0 alone forms the
+// max, exps, the f32 running sum in expert order and p = e / sum (two experts
+// per lane, no workgroup barrier) while waves 1.. run `side` (the input
+// quant); then stable ranks by four threads per expert against LDS broadcast
+// reads of a -1-padded table. More experts: GU_PE per thread with a barrier
+// between phases (max by DPP per wave then across waves, exps to LDS, the
+// running sum by lane 0 of wave 0 while waves 1.. run `side`, p in place,
+// ranks by two or one threads per expert). Leaves p in L.p and the top-k ids
+// in L.sid, published by the barrier it ends on, and the OR of every
+// thread's non-finite flag in `bad`.
 constexpr int GU_PE = (MAX_EXPERTS + GU_WG - 1) / GU_WG;
 template <class Side>
-__device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsigned& bad, Side side) {
+__device__ float route_par(const MoeDev& a, const float* lg, float lg_hi, RouteLds& L, unsigned& bad, Side side) {
     const int t = threadIdx.x, E = a.E;
-    if (t == 0) L.bad = 0u;  // published by the max's barriers
+    // each wave's flag, written by its lane 0 before a barrier (no clearing
+    // step that could race with another wave's write)
+    auto publish_bad = [&]() {
+        const unsigned any = __any(bad != 0u) ? 1u : 0u;
+        if ((t & 63) == 0) L.badw[t >> 6] = any;
+    };
+    auto gather_bad = [&]() {
+        unsigned b = 0u;
+#pragma unroll
+        for (int w = 0; w < GU_WG / 64; w++) b |= L.badw[w];
+        bad = b;
+    };
+    if (((E + 3) & ~3) <= GU_WG / 4) {
+        // Up to 128 experts: wave 0 alone forms the max (wave reduction), the
+        // exps, the running sum and p for experts t and t + 64 of each lane --
+        // no workgroup barrier -- while waves 1.. run `side`. The operations
+        // and their order are those of the general path below.
+        if (t < 64) {
+            const bool in0 = t < E, in1 = t + 64 < E;
+            bad |= (in0 && !isfinite(lg[0])) | (in1 && !isfinite(lg_hi));
+            float m = -__builtin_inff();
+            if (in0) m = fmaxf(m, lg[0]);
+            if (in1) m = fmaxf(m, lg_hi);
+            const float mx = uq_group_max<64>(m);
+            // entries past E hold -1 up to 128 entries (the rank table)
+            const float e0 = in0 ? uq_expf(lg[0] - mx) : -1.0f, e1 = in1 ? uq_expf(lg_hi - mx) : -1.0f;
+            L.p[t] = e0;
+            L.p[t + 64] = e1;
+            if (t < a.top_k) L.sid[t] = t;
+            // this wave's LDS writes are seen by its own later reads in order
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            float sl = 0.0f;
+            if (t == 0) {
+                const float4* p4 = (const float4*)L.p;
+                int q = 0;
+                for (; q + 8 <= E / 4; q += 8) {
+                    float4 v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) v[u] = p4[q + u];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        sl = sl + v[u].x;
+                        sl = sl + v[u].y;
+                        sl = sl + v[u].z;
+                        sl = sl + v[u].w;
+                    }
+                }
+                for (; q < E / 4; q++) {
+                    const float4 v = p4[q];
+                    sl = sl + v.x;
+                    sl = sl + v.y;
+                    sl = sl + v.z;
+                    sl = sl + v.w;
+                }
+                for (int e = E & ~3; e < E; e++) sl = sl + L.p[e];
+                L.sum = sl;
+            }
+            const float sum = __shfl(sl, 0, 64);
+            const float p0 = e0 / sum, p1 = e1 / sum;
+            if (in0) L.p[t] = p0;
+            if (in1) L.p[t + 64] = p1;
+            // rank key: p's bits (p >= +0, so they order as p does) above
+            // 127 - e (a tie goes to the lower id); 0 for a slot past E, which
+            // is never above a real key. Unique keys, so the top-k is one
+            // permutation even if p holds a NaN (the status flag reports it).
+            L.key[t] = in0 ? ((unsigned long long)__float_as_uint(p0) << 7) | (unsigned)(127 - t) : 0ull;
+            L.key[t + 64] = in1 ? ((unsigned long long)__float_as_uint(p1) << 7) | (unsigned)(63 - t) : 0ull;
+        } else {
+            side();
+        }
+        publish_bad();
+        __syncthreads();
+        // stable ranks on the keys: four threads per expert, each counting
+        // the keys above its expert's among a quarter of the table (the same
+        // order as p descending, id ascending)
+        constexpr int NE = GU_WG / 4;
+        const int e = t % NE, q = t / NE;
+        const unsigned long long kv = L.key[e];
+        int rank = 0;
+#pragma unroll
+        for (int u = 0; u < NE / 4; u++) rank += L.key[q * (NE / 4) + u] > kv ? 1 : 0;
+        if (q > 0) L.part[(q - 1) * NE + e] = rank;
+        __syncthreads();
+        if (q == 0 && e < E) {
+#pragma unroll
+            for (int k = 1; k < 4; k++) rank += L.part[(k - 1) * NE + e];
+            if (rank < a.top_k) L.sid[rank] = e;
+        }
+        __syncthreads();
+        gather_bad();
+        return L.sum;
+    }
     float mx = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < GU_PE; j++) {
@@ -100,10 +196,9 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         const int e = j * GU_WG + t;
         if (e < E) L.p[e] = uq_expf(lg[j] - mx);
     }
-    // entries past E hold -1: never above a score, never equal to one (up to
-    // GU_WG / 4 entries at least, the table the fast rank path below reads)
-    const int E4 = (E + 3) & ~3, EP = E4 > GU_WG / 4 ? E4 : GU_WG / 4;
-    if (t < EP - E) L.p[E + t] = -1.0f;
+    // entries past E hold -1: never above a score, never equal to one
+    const int E4 = (E + 3) & ~3;
+    if (t < E4 - E) L.p[E + t] = -1.0f;
     // with a NaN score no rank is unique; the slots then keep ids 0..k-1 and
     // the status flag reports the input
     if (t < a.top_k) L.sid[t] = t;
@@ -147,43 +242,13 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         pe[j] = e < E ? L.p[e] / sum : 0.0f;
         if (e < E) L.p[e] = pe[j];  // each thread rewrites only its own entries
     }
-    // every flag (logits in the max pass, the input in `side`) is final here;
-    // the caller reads L.bad after the last barrier below
-    if (bad) L.bad = 1u;
+    // every flag (logits in the max pass, the input in `side`) is final here
+    publish_bad();
     __syncthreads();
-    // stable ranks: RQ threads per expert (RQ = 4 up to 128 experts), each
+    // stable ranks: RQ threads per expert (2 up to 256 experts, else 1), each
     // comparing against every RQ-th float4 of the probabilities with all of
     // its LDS reads issued before the compares; partial counts meet in LDS
     const float4* p4 = (const float4*)L.p;
-    if (E4 <= GU_WG / 4) {
-        // up to GU_WG / 4 experts: the same four-thread split with compile-time
-        // bounds; every thread reads its eight float4 of the padded table
-        // unconditionally, so the reads go out together
-        constexpr int NE = GU_WG / 4;
-        const int e = t % NE, q = t / NE;
-        const float v = L.p[e];
-        int rank = 0;
-        float4 w[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) w[u] = p4[q + 4 * u];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i0 = 4 * (q + 4 * u);
-            rank += (int)(w[u].x > v) | ((int)(w[u].x == v) & (int)(i0 < e));
-            rank += (int)(w[u].y > v) | ((int)(w[u].y == v) & (int)(i0 + 1 < e));
-            rank += (int)(w[u].z > v) | ((int)(w[u].z == v) & (int)(i0 + 2 < e));
-            rank += (int)(w[u].w > v) | ((int)(w[u].w == v) & (int)(i0 + 3 < e));
-        }
-        if (q > 0) L.part[(q - 1) * NE + e] = rank;
-        __syncthreads();
-        if (q == 0 && e < E) {
-#pragma unroll
-            for (int k = 1; k < 4; k++) rank += L.part[(k - 1) * NE + e];
-            if (rank < a.top_k) L.sid[rank] = e;
-        }
-        __syncthreads();
-        return sum;
-    }
     const int RQ = E4 <= GU_WG / 2 ? 2 : 1;
     for (int e0 = 0; e0 < E4; e0 += GU_WG / RQ) {
         const int e = e0 + t % (GU_WG / RQ), q = t / (GU_WG / RQ);
@@ -222,6 +287,7 @@ __device__ float route_par(const MoeDev& a, const float* lg, RouteLds& L, unsign
         }
     }
     __syncthreads();
+    gather_bad();
     return sum;
 }
 
@@ -278,6 +344,7 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
         const int e = j * GU_WG + t;
         lg[j] = e < a.E ? a.logits[e] : 0.0f;
     }
+    const float lg_hi = a.logits[t + 64 < a.E ? t + 64 : a.E - 1];  // wave 0's second expert (up to 128)
     constexpr int QT = GU_WG - 64, QP = (MAX_D + 4 * QT - 1) / (4 * QT);
     const int qt = t - 64;
     float4 xv[QP];
@@ -305,9 +372,9 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
             }
         }
     };
-    // route_par ends on a barrier that publishes L.p / L.sid, lxq / lxs and L.bad
-    const float sum = route_par(a, lg, L, bad, quant_x);
-    bad = L.bad;
+    // route_par ends on a barrier that publishes L.p / L.sid and lxq / lxs,
+    // and leaves in `bad` the OR of every thread's non-finite flag
+    const float sum = route_par(a, lg, lg_hi, L, bad, quant_x);
     float v;
     if (!shared) {
         // routed expert: its weight loads go out before anything else waits

@@ -99,17 +99,29 @@ __device__ __forceinline__ void norm_quant_finish(const NormQuantArgs& a, const 
     ss = block_sum_d<WG>(ss, red);
     const float mean = (float)(ss / (double)D);
     const float scale = 1.0f / sqrtf(mean + a.eps);
+    // uq_quant_lane for all PER blocks of a thread at once: block maxima, then
+    // the divisions spread over each 32-lane group (D % 32 == 0, so a block's
+    // lanes are all in range or all out of it; out-of-range blocks are
+    // computed on zeros and not stored)
+    float y[PER], am[PER], inv[PER], sc[(PER + 31) / 32];
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int i = j * WG + t;
-        if (i < D) {
-            const float tmp = xv[j] * scale;
-            const float y = tmp * v.g[j];
-            float sc;
-            const int8_t qv = uq_quant_lane(y, &sc);
-            q[i] = qv;
-            if ((t & 31) == 0) s[(i >> 5) * sstride] = sc;
-        }
+        const float tmp = (i < D ? xv[j] : 0.0f) * scale;
+        y[j] = tmp * (i < D ? v.g[j] : 0.0f);
+        am[j] = uq_group_max<32>(fabsf(y[j]));
+    }
+    uq_block_recips<PER, 32>(am, inv, sc);
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = j * WG + t;
+        if (i < D) q[i] = (int8_t)uq_quant_code(y[j], inv[j]);
+    }
+    // lane r of a 32-lane group holds the scales of its blocks j = r, r + 32, ...
+#pragma unroll
+    for (int k = 0; k < (PER + 31) / 32; k++) {
+        const int j = (t & 31) + 32 * k, i = j * WG + (t & ~31);
+        if (j < PER && i < D) s[(i >> 5) * sstride] = sc[k];
     }
     __syncthreads();
 }

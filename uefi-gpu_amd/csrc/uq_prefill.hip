@@ -339,29 +339,58 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(PfRopeArgs a) {
     const float* trig = a.trig + (size_t)pos * hd;
     uint16_t* kc = a.kcache + (size_t)pos * kvd;
     uint16_t* vc = a.vcache + (size_t)pos * kvd;
-    for (int i = threadIdx.x; i < qpairs + kpairs + kvd; i += 256) {
-        if (i < qpairs + kpairs) {
-            const bool isq = i < qpairs;
-            const int p = isq ? i : i - qpairs;
+    // items: q pairs, k pairs, v values; NI per thread per pass, every load of
+    // a pass issued before any arithmetic (indices clamped, a missing bias read
+    // from the RoPE row instead and not used)
+    constexpr int NI = 5;
+    const int nr = qpairs + kpairs, n = nr + kvd;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 256 * NI) {
+        float x0[NI], x1[NI], b0[NI], b1[NI], c0[NI], c1[NI];
+#pragma unroll
+        for (int u = 0; u < NI; u++) {
+            const int i = i0 + 256 * u, ic = i < n ? i : n - 1;
+            const bool rope = ic < nr, isq = ic < qpairs;
+            const int p = isq ? ic : ic - qpairs;
             const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
+            const int e = ic - nr;
             const float* base = isq ? q : k;
             const float* bias = isq ? a.bq : a.bk;
-            const float cs = trig[j], sn = trig[half + j];
-            const float u = bias ? base[ia] + bias[ia] : base[ia];
-            const float w = bias ? base[ib] + bias[ib] : base[ib];
-            const float p0 = u * cs, p1 = w * sn, p2 = u * sn, p3 = w * cs;
-            const float ra = p0 - p1, rb = p2 + p3;
-            if (isq) {
-                q[ia] = ra;
-                q[ib] = rb;
+            const float* pa = rope ? base + ia : v + e;
+            const float* pb = rope ? base + ib : v + e;
+            const float* bsel = rope ? bias : a.bv;
+            const int bi0 = rope ? ia : e, bi1 = rope ? ib : e;
+            x0[u] = *pa;
+            x1[u] = *pb;
+            b0[u] = *(bsel ? bsel + bi0 : trig);
+            b1[u] = *(bsel ? bsel + bi1 : trig);
+            c0[u] = trig[rope ? j : 0];
+            c1[u] = trig[rope ? half + j : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < NI; u++) {
+            const int i = i0 + 256 * u;
+            if (i >= n) break;
+            if (i < nr) {
+                const bool isq = i < qpairs;
+                const int p = isq ? i : i - qpairs;
+                const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
+                const bool hb = isq ? a.bq != nullptr : a.bk != nullptr;
+                const float uu = hb ? x0[u] + b0[u] : x0[u];
+                const float ww = hb ? x1[u] + b1[u] : x1[u];
+                const float p0 = uu * c0[u], p1 = ww * c1[u], p2 = uu * c1[u], p3 = ww * c0[u];
+                const float ra = p0 - p1, rb = p2 + p3;
+                if (isq) {
+                    q[ia] = ra;
+                    q[ib] = rb;
+                } else {
+                    kc[ia] = uq_f16_rne(ra);
+                    kc[ib] = uq_f16_rne(rb);
+                }
             } else {
-                kc[ia] = uq_f16_rne(ra);
-                kc[ib] = uq_f16_rne(rb);
+                const int e = i - nr;
+                const float vb = a.bv ? x0[u] + b0[u] : x0[u];
+                vc[e] = uq_f16_rne(vb);
             }
-        } else {
-            const int e = i - qpairs - kpairs;
-            const float vb = a.bv ? v[e] + a.bv[e] : v[e];
-            vc[e] = uq_f16_rne(vb);
         }
     }
 }

@@ -1,5 +1,5 @@
-// Argument blocks of the decode-step kernels: the embedding/norm/quant
-// kernel (uq_decode.hip) and the attention kernel (uq_step.hip).
+// Argument block of the residual + RMSNorm + quant prologues (and the layer-0
+// embedding row) that the decode-step and prefill kernels run inline.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -22,7 +22,5 @@ struct NormQuantArgs {
     int dim;
     float eps;
 };
-
-void launch_resnorm_quant(const NormQuantArgs& a, hipStream_t s);
 
 }  // namespace uq

@@ -264,12 +264,9 @@ int Model::enqueue_step(hipStream_t s) {
         DownArgs da{wd->qs, wd->d, GATE, TMP, wd->m, wd->n};
         if (launch_down_h(da, s)) return fail(ERR_SHAPE, "down: unsupported hidden size");
     }
-    NormQuantArgs no = nq_args(R1, TMP, vec("output_norm.weight"), nullptr);
-    no.xq = XQ;
-    no.xs = XS;
-    launch_resnorm_quant(no, s);
     const Weight* out = weight("output.weight");
     LmArgs la{out->qs, out->d, XQ, XS, LOGITS, c.vocab, c.dim, partial, result, token, pos, history, c.max_seq};
+    la.nq = nq_args(R1, TMP, vec("output_norm.weight"), nullptr);  // the output norm runs inside the lm_head launch
     if (launch_lm_greedy(la, s)) return fail(ERR_SHAPE, "lm_head: unsupported dim");
     return OK;
 }
@@ -415,15 +412,13 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
     no.x = PX + (size_t)(n - 1) * c.dim;
     no.residual = PTMP + (size_t)(n - 1) * c.dim;
     no.gamma = vec("output_norm.weight");
-    no.xq = XQ;
-    no.xs = XS;
     no.dim = c.dim;
     no.eps = c.eps;
-    launch_resnorm_quant(no, s);
     host_io[1] = (uint32_t)(n - 1);
     UQ_CHECK_HIP(hipMemcpyAsync(pos, &host_io[1], 4, hipMemcpyHostToDevice, s));
     const Weight* out = weight("output.weight");
     LmArgs la{out->qs, out->d, XQ, XS, LOGITS, c.vocab, c.dim, partial, result, token, pos, history, c.max_seq};
+    la.nq = no;  // the output norm runs inside the lm_head launch
     if (launch_lm_greedy(la, s)) return fail(ERR_SHAPE, "lm_head: unsupported dim");
     UQ_CHECK_HIP(hipGetLastError());
     uint32_t res[2] = {0, 0};

@@ -58,6 +58,7 @@ struct LmArgs {
     int* pos;
     uint32_t* history;
     int max_seq;
+    NormQuantArgs nq;         // the output RMSNorm + quant of the input, done by every workgroup
 };
 
 // Decode attention split over ATT_SPLIT position chunks per query head:

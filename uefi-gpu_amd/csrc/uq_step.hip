@@ -488,9 +488,13 @@ __global__ __launch_bounds__(1024) void k_down_h(DownArgs a) {
 // ------------------------------------------------------------------ lm_head + argmax partials
 template <int LPR, int NBL>
 __global__ __launch_bounds__(256) void k_lm_argmax(LmArgs a) {
+    constexpr int PK = (LPR * NBL * Q8::UNIT + 255) / 256, NC = PK < MAX_DIM / 256 ? PK : MAX_DIM / 256;
     __shared__ float vs[256];
     __shared__ int ids[256];
     __shared__ unsigned bs[256];
+    __shared__ __attribute__((aligned(16))) int8_t lq[NC * 256];
+    __shared__ float ls[NC * 8];
+    __shared__ double part[4];
     constexpr int RPW = 64 / LPR, RPB = RPW * 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sub = lane % LPR, grp = lane / LPR;
     const int64_t nu = a.k / Q8::UNIT;
@@ -498,21 +502,53 @@ __global__ __launch_bounds__(256) void k_lm_argmax(LmArgs a) {
     int id = 0x7fffffff;
     unsigned bad = 0;
     {
-        Q8::X xr[NBL];
-        load_xr<Q8, LPR, NBL>(xr, a.xq, a.xs, nu, sub);
+        // The output RMSNorm + quant of the input by all four waves (no
+        // separate launch): its loads, then the first row set's weights, then
+        // its arithmetic while those weights are in flight.
+        NormQuantSplit<NC, 4> nw;
+        nw.issue(a.nq);
         const WArgs w{a.w_qs, a.w_d, nullptr};
-        for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < a.rows; row0 += (int64_t)gridDim.x * RPB) {
+        int64_t row0 = (int64_t)blockIdx.x * RPB;
+        Q8::W wv[NBL];
+        {
+            const int64_t row = row0 + wave * RPW + grp, rr = row < a.rows ? row : a.rows - 1;
+            const Q8::R r = Q8::row_ptr(w, rr, nu);
+#pragma unroll
+            for (int i = 0; i < NBL; i++) {
+                const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+                wv[i] = Q8::load_u(r, uc);
+            }
+        }
+        nw.finish(a.nq, false, part, lq, ls);
+        __syncthreads();
+        Q8::X xr[NBL];
+        load_xr<Q8, LPR, NBL>(xr, lq, ls, nu, sub);
+        for (;;) {
             const int64_t row = row0 + wave * RPW + grp;
-            if (row < a.rows) {
-                const float y = (float)row_dot<Q8, LPR, NBL>(w, row, nu, sub, xr);
-                if (sub == 0) {
-                    a.logits[row] = y;
-                    bad |= (__float_as_uint(y) & 0x7f800000u) == 0x7f800000u;
-                    if (better(y, (int)row, best, id)) {
-                        best = y;
-                        id = (int)row;
-                    }
+            double acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < NBL; i++) {
+                const int u = sub + LPR * i;
+                const double t = Q8::dot(wv[i], xr[i]);
+                acc += u < nu ? t : 0.0;
+            }
+            const float y = (float)uq_group_sum<LPR>(acc);
+            if (row < a.rows && sub == 0) {
+                a.logits[row] = y;
+                bad |= (__float_as_uint(y) & 0x7f800000u) == 0x7f800000u;
+                if (better(y, (int)row, best, id)) {
+                    best = y;
+                    id = (int)row;
                 }
+            }
+            row0 += (int64_t)gridDim.x * RPB;
+            if (row0 >= a.rows) break;
+            const int64_t nrow = row0 + wave * RPW + grp, rr = nrow < a.rows ? nrow : a.rows - 1;
+            const Q8::R r = Q8::row_ptr(w, rr, nu);
+#pragma unroll
+            for (int i = 0; i < NBL; i++) {
+                const int u = sub + LPR * i, uc = u < nu ? u : (int)nu - 1;
+                wv[i] = Q8::load_u(r, uc);
             }
         }
     }
@@ -650,6 +686,7 @@ int launch_down_h(const DownArgs& a, hipStream_t s) {
     return 0;
 }
 int launch_lm_greedy(const LmArgs& a, hipStream_t s) {
+    if (!a.nq.x || !a.nq.gamma || a.nq.dim != a.k || a.k > MAX_DIM || a.k % 32) return -1;
     const int lpr = step_lpr(a.k);
     const int64_t rpb = 4 * (64 / lpr), sets = (a.rows + rpb - 1) / rpb;
     const int parts = (int)(sets < LM_MAX_WG ? sets : LM_MAX_WG);

@@ -252,7 +252,8 @@ struct NormQuantWave {
 // sums in LDS (part[NW], added in wave order in every wave) behind an LDS-only
 // barrier, and quantizes its own chunks (divisions spread as in
 // uq_block_recips). Per value the same operations as NormQuantWave. Every wave
-// of the workgroup calls both halves; the caller's barrier publishes q / s.
+// of the workgroup calls both halves; the caller's barrier publishes q / s
+// (LDS or global; scale b at s[b * sstride]).
 template <int NC, int NW>
 struct NormQuantSplit {
     static constexpr int PC = (NC + NW - 1) / NW;  // chunks per wave, at most
@@ -279,7 +280,7 @@ struct NormQuantSplit {
     }
 
     __device__ __forceinline__ void finish(const NormQuantArgs& a, bool write_x, double* part, int8_t* q,
-                                           float* s) {
+                                           float* s, int sstride = 1) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.dim;
         float x[PC][4];
         double s4[4] = {0.0, 0.0, 0.0, 0.0};
@@ -353,7 +354,7 @@ struct NormQuantSplit {
 #pragma unroll
         for (int kk = 0; kk < (PC + 7) / 8; kk++) {
             const int r = (lane & 7) + 8 * kk, c = wave + NW * r, i = 256 * c + 32 * (lane >> 3);
-            if (r < PC && c < NC && i < D) s[i >> 5] = sc[kk];
+            if (r < PC && c < NC && i < D) s[(i >> 5) * sstride] = sc[kk];
         }
     }
 };

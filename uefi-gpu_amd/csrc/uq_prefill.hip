@@ -37,15 +37,20 @@ __global__ __launch_bounds__(256) void k_transpose_scales(const uint16_t* __rest
 // ------------------------------------------------------------------ per-token norm + quant
 // One workgroup per token: x = embed(token) or x + residual (stored back),
 // RMSNorm, block-32 quant into xq[t][dim] and xsT[b][t].
+constexpr int PF_MAXD = 4096;  // model dim bound (uq_model_create: dim <= 4096, dim % 256 == 0)
 __global__ __launch_bounds__(256) void k_pf_norm(PfNormArgs a) {
-    __shared__ double red[4];
+    __shared__ double part[4];
     const int t = blockIdx.x;
     NormQuantArgs nq = a.nq;
     nq.x = a.x + (size_t)t * a.nq.dim;
     nq.residual = a.residual ? a.residual + (size_t)t * a.nq.dim : nullptr;
     nq.x_out = a.x + (size_t)t * a.nq.dim;
     if (a.tokens) nq.token = a.tokens + t;
-    norm_quant<256>(nq, true, a.xq + (size_t)t * a.nq.dim, a.xst + t, red, a.mp);
+    // one token row per workgroup, spread over its four waves (256-value
+    // chunks, float4 per lane, partial sums of squares meeting in LDS)
+    NormQuantSplit<PF_MAXD / 256, 4> nw;
+    nw.issue(nq);
+    nw.finish(nq, true, part, a.xq + (size_t)t * a.nq.dim, a.xst + t, a.mp);
 }
 
 // Block-32 quant of rows of k floats: grid (k/256, tokens).

@@ -178,6 +178,49 @@ def prefill_gemm_bench(tokens=512, reps=20):
     return out
 
 
+def prefill_attention_bench(tokens=512, heads=12, kv_heads=2, head_dim=128, reps=50):
+    """The 512-token prefill's causal attention alone (Qwen2.5-1.5B heads: 12 query,
+    2 KV, head_dim 128; int8 output planes for the o GEMM as in the model), HIP
+    events over `reps` launches. Causal flops = 2 contractions x 2 x head_dim x
+    (1 + 2 + ... + tokens) per head; issued = what the 16-query x 16-key tiles
+    of v_mfma_f64_16x16x4_f64 execute (q.k over whole 16-key tiles, P.V over
+    whole 4-key steps)."""
+    ms = uq.time_prefill_attention(tokens, heads, kv_heads, head_dim, True, reps)
+    causal = heads * 2 * 2 * head_dim * tokens * (tokens + 1) // 2
+    issued = 0
+    for t0 in range(0, tokens, 16):
+        kend = t0 + min(16, tokens - t0)
+        issued += 16 * 16 * 2 * head_dim * (((kend + 15) // 16) + ((kend + 3) // 4 * 4) / 16)
+    issued *= heads
+    return {"us": round(ms * 1e3, 2), "causal_TFLOPs": round(causal / (ms / 1e3) / 1e12, 2),
+            "issued_TFLOPs": round(issued / (ms / 1e3) / 1e12, 2), "fp64_mfma_peak_TFLOPs": 78.6,
+            "issued_frac": round(issued / (ms / 1e3) / 1e12 / 78.6, 4),
+            "shape": "%d tokens, %d/%d heads, head_dim %d" % (tokens, heads, kv_heads, head_dim)}
+
+
+def mfma_probe():
+    """Matrix-core rates on this box: 16 waves per CU (kinds 0-2), and one wave per
+    SIMD with and without the VALU work the prefill kernels put beside their
+    MFMAs (kinds 3-6): fp64 MFMAs with an fp16 -> double operand conversion each,
+    int8 MFMAs beside the per-block f32 rescale."""
+    r = {"int8_TOPS": round(uq.probe_mfma(0), 1), "fp16_TFLOPS": round(uq.probe_mfma(1), 1),
+         "fp64_TFLOPS": round(uq.probe_mfma(2), 1)}
+    one = {k: uq.probe_mfma(kind) for k, kind in (("fp64", 3), ("fp64_and_conv", 4), ("conv_only", 5),
+                                                  ("int8", 6), ("int8_and_rescale", 7), ("rescale_only", 8))}
+    # iteration time ~ 1/rate: additive work gives 1/both = 1/mfma + 1/valu,
+    # full overlap gives 1/both = max(1/mfma, 1/valu)
+    overlap = lambda m, b, v: round((1 / m + 1 / v - 1 / b) / min(1 / m, 1 / v), 3)
+    r["one_wave_per_simd"] = {k: round(v, 1) for k, v in one.items()}
+    r["one_wave_per_simd"]["fp64_overlap"] = overlap(one["fp64"], one["fp64_and_conv"], one["conv_only"])
+    r["one_wave_per_simd"]["int8_overlap"] = overlap(one["int8"], one["int8_and_rescale"], one["rescale_only"])
+    r["note"] = ("independent chains of v_mfma_i32_16x16x32_i8 / v_mfma_f32_16x16x32_f16 / v_mfma_f64_16x16x4_f64 "
+                 "on register operands, 16 waves per CU, same box; one_wave_per_simd: 16 MFMAs per iteration on "
+                 "4 chains and/or the VALU work beside them (fp64: 16 fp16->double operand conversions; int8: "
+                 "convert, scale product, fma of 16 f32 accumulators), rates of the same MFMA count; overlap: "
+                 "share of the shorter part hidden under the longer (0 additive, 1 fully overlapped)")
+    return r
+
+
 def kquant_sweep(kind, copies=3, reps=30):
     """The same bs=1 sweep with K-quant weights: Q4_K (144 B per 256 values)
     or Q3_K (110 B per 256 values); lm_head alone timed over back-to-back
@@ -319,7 +362,8 @@ def main():
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 256 MB MALL in total)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
-    ap.add_argument("--leg", choices=["decode", "prefill", "q4k", "q3k", "moe", "linear", "frontier_moe"],
+    ap.add_argument("--leg", choices=["decode", "prefill", "attention", "probes", "q4k", "q3k", "moe", "linear",
+                                      "frontier_moe"],
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -329,7 +373,9 @@ def main():
 
     uq.init(0)
     if args.leg:
-        leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "q4k": q4k_sweep, "q3k": q3k_sweep,
+        leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "attention": prefill_attention_bench,
+               "probes": mfma_probe,
+               "q4k": q4k_sweep, "q3k": q3k_sweep,
                "moe": moe_bench, "linear": linear_sweep, "frontier_moe": frontier_moe_bench}[args.leg]
         print(json.dumps({args.leg: leg()}), flush=True)
         return
@@ -402,10 +448,7 @@ def main():
     read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
     result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
                            "note": "plain int4 streaming read / copy of 1 GiB, same box"}
-    result["mfma_probe"] = {"int8_TOPS": round(uq.probe_mfma(0), 1), "fp16_TFLOPS": round(uq.probe_mfma(1), 1),
-                            "fp64_TFLOPS": round(uq.probe_mfma(2), 1),
-                            "note": "independent chains of v_mfma_i32_16x16x32_i8 / v_mfma_f32_16x16x32_f16 / "
-                                    "v_mfma_f64_16x16x4_f64 on register operands, 16 waves per CU, same box"}
+    result["mfma_probe"] = mfma_probe()
     for w in weights:
         w.free()
     decode_state = {} if not args.no_cpu else None
@@ -415,6 +458,7 @@ def main():
         pg = result["prefill_gemm"]
         pg["measured_16x16x32_peak_TOPS"] = result["mfma_probe"]["int8_TOPS"]
         pg["frac_of_measured_peak"] = round(pg["aggregate_TOPS"] / result["mfma_probe"]["int8_TOPS"], 4)
+        result["prefill_attention"] = prefill_attention_bench()
         result["q4k_sweep"] = q4k_sweep()
         result["q3k_sweep"] = q3k_sweep()
         result["moe"] = moe_bench()

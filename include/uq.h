@@ -135,6 +135,14 @@ int uq_prefill_gemm(uq_weight_t w, const int8_t* xq, const float* xs, int64_t to
  * (w2 non-null: the fused gate/up pair), `reps` launches. Measurement aid. */
 int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps, double* ms);
 
+/* Mean HIP-event time of the prefill's causal attention (the batched form of
+ * fused_attention, gpu_attention.cu:2-26) over `tokens` synthetic queries at
+ * positions 0.. against an fp16 KV cache of the same length, `reps` launches;
+ * quant_out (head_dim 128): the epilogue writes the o GEMM's int8 planes, as
+ * the model's prefill does. Measurement aid. */
+int uq_time_prefill_attention(int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, int quant_out,
+                              int reps, double* ms);
+
 /* ---------------------------------------------------------------- fp32-activation reader
  * The frontier backend's kernels (driver/kernels/frontier_quant.cu:12-93) for
  * its seven kinds, with fp32 activations. Each output is the exact sum of the
@@ -213,7 +221,13 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
 /* Matrix-core throughput probe (no reference counterpart; measurement aid):
  * independent chains of one MFMA on register operands, 16 waves per CU, rate
  * from HIP events. kind 0: v_mfma_i32_16x16x32_i8 (tera int8 ops/s), 1:
- * v_mfma_f32_16x16x32_f16 (TFLOP/s), 2: v_mfma_f64_16x16x4_f64 (TFLOP/s). */
+ * v_mfma_f32_16x16x32_f16 (TFLOP/s), 2: v_mfma_f64_16x16x4_f64 (TFLOP/s).
+ * One wave per SIMD, rate counted as the MFMA work of the iterations (also
+ * where only the VALU part runs): 3: fp64 MFMAs alone, 4: with an fp16 ->
+ * double B-operand conversion per MFMA, 5: those conversions alone; 6: int8
+ * MFMAs alone, 7: beside a convert / scale product / fma per f32 accumulator
+ * (the prefill GEMM's rescale), 8: that rescale alone. Whether a kind's VALU
+ * work overlaps the matrix core: 1/rate(4) vs 1/rate(3) + 1/rate(5). */
 int uq_probe_mfma(int kind, double* tera_ops);
 
 /* ---------------------------------------------------------------- Qwen2 dense decoder */

@@ -12,6 +12,8 @@
 #include <stdint.h>
 
 #define UQ_DEV __device__ __forceinline__
+// Also built for the host: the exhaustive check of uq_expf runs there.
+#define UQ_HD __host__ __device__ __forceinline__
 
 // s_waitcnt vmcnt(0): every vector-memory op this wave has issued (LDS DMA
 // included) has completed; expcnt and lgkmcnt are not waited on.
@@ -39,56 +41,44 @@ UQ_DEV int uq_mul24(int a, int b) { return __mul24(a, b); }
 UQ_DEV float uq_half(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 UQ_DEV uint16_t uq_f16_rne(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
-UQ_DEV float uq_bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
-
-// y * 2^k with the pre-scaling steps of scalbnf for k outside [-126, 127]
-// (only the final multiply can round, into the subnormal range).
-UQ_DEV float uq_scalbnf_steps(float y, int k) {
-    if (k > 127) {
-        y = y * 0x1p127f; k -= 127;
-        if (k > 127) { y = y * 0x1p127f; k -= 127; if (k > 127) k = 127; }
-    } else if (k < -126) {
-        y = y * 0x1p-102f; k += 102;
-        if (k < -126) { y = y * 0x1p-102f; k += 102; if (k < -126) k = -126; }
-    }
-    return y * uq_bits_f((uint32_t)(127 + k) << 23);
-}
+UQ_HD float uq_bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 
 // expf of the reference's Rust path: libm 0.2.16 (FreeBSD e_expf.c), as
 // restated at driver/src/frontier_cpu_expf.rs:80-170. Same f32 operations as
 // the oracle's uqo_expf; division is IEEE (HIP's correctly rounded f32 '/').
 // Algorithm: Copyright (C) 1993 by Sun Microsystems, Inc.; notice kept in
 // third_party/NOTICE.sunpro-expf.
-UQ_DEV float uq_expf(float x) {
+UQ_HD float uq_expf(float x) {
+    // Branch-free: the reduction's cases (k = 0 for |x| <= ln2/2, +-1 up to
+    // 1.5 ln2, else x/ln2 rounded half away from zero), the small-|x| and
+    // special results and scalbnf's pre-scaling are selects, so divergent
+    // lanes run one path. k = 0 reproduces the unreduced operands exactly
+    // (x - 0 * ln2hi = x, lo = +0) and scaling by 2^0 is exact, so every
+    // input gives the branchy form's bits (checked over all 2^32 inputs).
     const uint32_t bx = __builtin_bit_cast(uint32_t, x);
     const uint32_t ax = bx & 0x7fffffffu;
     const bool neg = (bx >> 31) != 0;
-    if (ax >= 0x42aeac50u) {
-        if (ax > 0x7f800000u) return x;
-        if (!neg && ax >= 0x42b17218u) return x * 0x1p127f;
-        if (neg && ax >= 0x42cff1b5u) return 0.0f;
-    }
-    if (ax <= 0x39000000u) return 1.0f + x;
-    float hi = x, lo = 0.0f;
-    int k = 0;
-    if (ax > 0x3eb17218u) {
-        if (ax > 0x3f851592u) {
-            const float t = x * uq_bits_f(0x3fb8aa3bu);
-            k = (int)(t + (neg ? -0.5f : 0.5f));
-        } else {
-            k = neg ? -1 : 1;
-        }
-        const float kf = (float)k;
-        hi = x - kf * uq_bits_f(0x3f317200u);
-        lo = kf * uq_bits_f(0x35bfbe8eu);
-        x = hi - lo;
-    }
-    const float r2 = x * x;
+    const float t = fminf(fmaxf(x * uq_bits_f(0x3fb8aa3bu), -160.0f), 160.0f);
+    int k = (int)(t + (neg ? -0.5f : 0.5f));
+    k = ax > 0x3f851592u ? k : (neg ? -1 : 1);
+    k = ax > 0x3eb17218u ? k : 0;
+    const float kf = (float)k;
+    const float hi = x - kf * uq_bits_f(0x3f317200u);
+    const float lo = kf * uq_bits_f(0x35bfbe8eu);
+    const float xr = hi - lo;
+    const float r2 = xr * xr;
     const float poly = r2 * (uq_bits_f(0x3e2aaa8fu) + r2 * uq_bits_f(0xbb355215u));
-    const float c = x - poly;
-    const float q = (x * c) / (2.0f - c);
+    const float c = xr - poly;
+    const float q = (xr * c) / (2.0f - c);
     const float y = 1.0f + ((q - lo) + hi);
-    return k == 0 ? y : uq_scalbnf_steps(y, k);
+    // scalbnf(y, k) for the k in [-150, 128] that finite, non-special inputs reach
+    const float s1 = k > 127 ? 0x1p127f : (k < -126 ? 0x1p-102f : 1.0f);
+    const int k2 = k > 127 ? k - 127 : (k < -126 ? k + 102 : k);
+    float r = (y * s1) * uq_bits_f((uint32_t)(127 + k2) << 23);
+    r = ax <= 0x39000000u ? 1.0f + x : r;
+    r = neg && ax >= 0x42cff1b5u ? 0.0f : r;
+    r = !neg && ax >= 0x42b17218u ? x * 0x1p127f : r;
+    return ax > 0x7f800000u ? x : r;
 }
 
 // (g / (1 + exp(-g))) * u  -- gateup_dp4a / silu_mul form

@@ -655,6 +655,63 @@ int uq_time_prefill_gemm(uq_weight_t w, uq_weight_t w2, int64_t tokens, int reps
     return rc;
 }
 
+int uq_time_prefill_attention(int32_t tokens, int32_t heads, int32_t kv_heads, int32_t head_dim, int quant_out,
+                              int reps, double* ms) {
+    if (reps <= 0 || !ms || tokens <= 0 || tokens > 1024 || heads <= 0 || kv_heads <= 0 || heads % kv_heads ||
+        (head_dim != 64 && head_dim != 128) || (quant_out && head_dim != 128))
+        return set_error(ERR_ARG, "time_prefill_attention: bad args");
+    hipStream_t s = (hipStream_t)uq_stream();
+    const int64_t stride = (int64_t)(heads + 2 * kv_heads) * head_dim, kvd = (int64_t)kv_heads * head_dim;
+    const int64_t qd = (int64_t)heads * head_dim, mp = (tokens + 63) / 64 * 64;
+    // q rows in [-1, 1); fp16 keys and values of magnitude [1/4, 2), random sign
+    std::vector<float> hq((size_t)(tokens * stride));
+    for (size_t i = 0; i < hq.size(); i++) hq[i] = (float)((int)((i * 2654435761u) >> 16) % 2048 - 1024) / 1024.0f;
+    std::vector<uint16_t> hkv((size_t)(2 * tokens * kvd));
+    for (size_t i = 0; i < hkv.size(); i++) {
+        const uint32_t r = (uint32_t)((i + 1) * 2246822519u) >> 7;
+        hkv[i] = (uint16_t)(((r >> 20) & 1) << 15 | (13 + (r >> 10) % 3) << 10 | (r & 0x3ff));
+    }
+    float *dq = nullptr, *dout = nullptr, *dxs = nullptr;
+    uint16_t* dkv = nullptr;
+    int8_t* dxq = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipMalloc(&dq, 4 * hq.size());
+    if (e == hipSuccess) e = hipMalloc(&dkv, 2 * hkv.size());
+    if (e == hipSuccess) e = hipMalloc(&dout, 4 * (size_t)(tokens * qd));
+    if (e == hipSuccess) e = hipMalloc(&dxq, (size_t)(mp * qd));
+    if (e == hipSuccess) e = hipMalloc(&dxs, 4 * (size_t)(qd / 32 * mp));
+    if (e == hipSuccess) e = hipMemcpyAsync(dq, hq.data(), 4 * hq.size(), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dkv, hkv.data(), 2 * hkv.size(), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    int rc = OK;
+    if (e == hipSuccess) {
+        PfAttnArgs aa{dq, (int)stride, dkv, dkv + tokens * kvd, dout, tokens, 0, tokens, heads, kv_heads, head_dim,
+                      (float)(1.0 / std::sqrt((double)head_dim)), quant_out ? dxq : nullptr, quant_out ? dxs : nullptr,
+                      (int)mp};
+        if (launch_pf_attention(aa, s)) {
+            rc = set_error(ERR_SHAPE, "time_prefill_attention: shape");
+        } else {
+            e = hipEventRecord(e0, s);
+            for (int r = 0; r < reps && e == hipSuccess; r++) e = launch_pf_attention(aa, s) ? hipErrorInvalidValue : hipSuccess;
+            if (e == hipSuccess) e = hipEventRecord(e1, s);
+            if (e == hipSuccess) e = hipEventSynchronize(e1);
+            float t = 0;
+            if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+            *ms = t / reps;
+        }
+    }
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    hipFree(dq);
+    hipFree(dkv);
+    hipFree(dout);
+    hipFree(dxq);
+    hipFree(dxs);
+    if (e != hipSuccess) return set_error(ERR_DEVICE, std::string("time_prefill_attention: ") + hipGetErrorString(e));
+    return rc;
+}
+
 int uq_model_logits(uq_model_t h, float* out, int64_t n) {
     Model* m = (Model*)h;
     if (!m || !out) return set_error(ERR_ARG, "model_logits: null pointer");

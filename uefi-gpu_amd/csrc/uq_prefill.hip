@@ -531,12 +531,16 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
         }
         mx = uq_group_max<16>(mx);
         double tot = 0.0;
+        // every score read is finite (keys past T hold later queries' or the
+        // clamped key's scores), so all four exps run and the masked ones
+        // become 0 by select: no divergent branch per key
         for (int t0 = 4 * cj; t0 < T; t0 += 64) {
             const float4 v = *(const float4*)(sr + t0);
             const float e0 = uq_expf(v.x - mx);
-            const float e1 = t0 + 1 < T ? uq_expf(v.y - mx) : 0.0f;
-            const float e2 = t0 + 2 < T ? uq_expf(v.z - mx) : 0.0f;
-            const float e3 = t0 + 3 < T ? uq_expf(v.w - mx) : 0.0f;
+            float e1 = uq_expf(v.y - mx), e2 = uq_expf(v.z - mx), e3 = uq_expf(v.w - mx);
+            e1 = t0 + 1 < T ? e1 : 0.0f;
+            e2 = t0 + 2 < T ? e2 : 0.0f;
+            e3 = t0 + 3 < T ? e3 : 0.0f;
             *(float4*)(sr + t0) = make_float4(e0, e1, e2, e3);
             tot += (double)e0;
             tot += (double)e1;
@@ -564,14 +568,16 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
     // batches of SU 4-key steps in a two-stage register pipeline: the next
     // batch's P and V loads are issued before the current batch's MFMAs
     constexpr int SU = 8;
-    struct PvBatch { double p[SU]; uint16_t v[SU][DT]; };
+    // p stays f32 (and unmasked) until the batch's MFMAs: the LDS reads and V
+    // loads of a batch issue back to back with no per-key wait or branch
+    struct PvBatch { float p[SU]; uint16_t v[SU][DT]; };
     auto load_pv = [&](int k0, PvBatch& bt) {
 #pragma unroll
         for (int u = 0; u < SU; u++) {
             const int kk = k0 + 4 * u + g;
             const int kl = kk < kpad ? kk : kpad - 1;
             const int kv = kl < kend ? kl : kend - 1;  // p is 0 there
-            bt.p[u] = kk < kpad ? (double)pr[kl] : 0.0;
+            bt.p[u] = pr[kl];
 #pragma unroll
             for (int j = 0; j < DT; j++) bt.v[u][j] = vb[(size_t)kv * kvd + j * 16];
         }
@@ -581,19 +587,22 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
 #pragma unroll
     for (int j = 0; j < DT; j++) o2[j] = d4{0.0, 0.0, 0.0, 0.0};
     // the batch's V operands converted to double first, then its MFMAs
-    auto mma_pv = [&](const PvBatch& bt) {
-        double vd[SU][DT];
+    // k0: the batch's first key; steps past kpad get p = 0
+    auto mma_pv = [&](int k0, const PvBatch& bt) {
+        double vd[SU][DT], pd[SU];
 #pragma unroll
-        for (int u = 0; u < SU; u++)
+        for (int u = 0; u < SU; u++) {
+            pd[u] = k0 + 4 * u + g < kpad ? (double)bt.p[u] : 0.0;
 #pragma unroll
             for (int j = 0; j < DT; j++) vd[u][j] = (double)uq_half(bt.v[u][j]);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < SU; u += 2)
 #pragma unroll
             for (int j = 0; j < DT; j++) {
-                o[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(bt.p[u], vd[u][j], o[j], 0, 0, 0);
-                o2[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(bt.p[u + 1], vd[u + 1][j], o2[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd[u], vd[u][j], o[j], 0, 0, 0);
+                o2[j] = __builtin_amdgcn_mfma_f64_16x16x4f64(pd[u + 1], vd[u + 1][j], o2[j], 0, 0, 0);
             }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -604,12 +613,12 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
         while (k0 < kpad) {
             if (k0 + 4 * SU < kpad) load_pv(k0 + 4 * SU, bb);
             __builtin_amdgcn_sched_barrier(0);
-            mma_pv(ba);
+            mma_pv(k0, ba);
             k0 += 4 * SU;
             if (k0 >= kpad) break;
             if (k0 + 4 * SU < kpad) load_pv(k0 + 4 * SU, ba);
             __builtin_amdgcn_sched_barrier(0);
-            mma_pv(bb);
+            mma_pv(k0, bb);
             k0 += 4 * SU;
         }
     }

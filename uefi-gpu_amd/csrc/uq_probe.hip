@@ -78,6 +78,89 @@ __global__ __launch_bounds__(256) void k_probe_mfma_f64(int iters, int* __restri
     for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
     if (s == -1.0) sink[blockIdx.x] = 1;
 }
+// One wave per SIMD (one 256-thread workgroup per CU), 16 MFMAs per iteration
+// on four accumulator chains (MFMA) and/or the VALU work the prefill kernels
+// put beside them (VALU): for FP64, a fresh fp16 operand converted to double
+// per MFMA (the attention kernels' K and V operands); for int8, convert, scale
+// product and fma of 16 f32 accumulators plus an integer step (the prefill
+// GEMM's per-block rescale). Timing both alone and together shows whether the
+// two overlap on a SIMD.
+template <bool MFMA, bool VALU>
+__global__ __launch_bounds__(256) void k_probe_f64_1w(int iters, int* __restrict__ sink) {
+    const int t = threadIdx.x;
+    double qa[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) qa[i] = 1.0 + 0.001 * (double)(t + i);
+    uint32_t kw[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) kw[i] = 0x3c003c00u ^ (((uint32_t)t * 2654435761u + (uint32_t)i) & 0x03ff03ffu);
+    pv4d c[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) c[k] = pv4d{0.0, 0.0, 0.0, 0.0};
+    double vs = 0.0;
+    for (int it = 0; it < iters; it++) {
+        double kd[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            if (VALU) {
+                const uint16_t h = (uint16_t)(i & 1 ? kw[i >> 1] >> 16 : kw[i >> 1] & 0xffff);
+                kd[i] = (double)(float)__builtin_bit_cast(_Float16, h);
+            } else {
+                kd[i] = qa[(i + 3) & 15];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (MFMA) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) c[i & 3] = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[i], kd[i], c[i & 3], 0, 0, 0);
+        } else {
+            vs = kd[it & 15];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (VALU) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) kw[i] = kw[i] * 1664525u + 1013904223u;
+        }
+    }
+    const pv4d u = (c[0] + c[1]) + (c[2] + c[3]);
+    if (u[0] + u[1] + u[2] + u[3] + vs == -1.0) sink[blockIdx.x] = 1;
+}
+template <bool MFMA, bool VALU>
+__global__ __launch_bounds__(256) void k_probe_i8_1w(int iters, int* __restrict__ sink) {
+    const int t = threadIdx.x;
+    long a = ((long)t << 32) ^ (long)(t * 3), b = ((long)(t * 7) << 32) ^ (long)t;
+    pv4i c[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) c[k] = pv4i{0, 0, 0, 0};
+    float y[16], sx[16];
+    int d[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        y[i] = 0.0f;
+        sx[i] = 0.001f * (float)(t + i);
+        d[i] = t + i;
+    }
+    float sw = 0.5f + 0.001f * (float)t;
+    for (int it = 0; it < iters; it++) {
+        if (MFMA) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) c[i & 3] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c[i & 3], 0, 0, 0);
+        }
+        if (VALU) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                y[i] = __builtin_fmaf((float)d[i], sx[i] * sw, y[i]);
+                d[i] += 3;
+            }
+            sw += 0.25f;
+        }
+        a += 1;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) s += y[i];
+    if (s + (float)(c[0][0] + c[1][1] + c[2][2] + c[3][3]) == -1.0f) sink[blockIdx.x] = 1;
+}
 
 }  // namespace
 }  // namespace uq
@@ -126,18 +209,29 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
 
 int uq_probe_mfma(int kind, double* tera_ops) {
     if (!uq_stream()) return set_error(ERR_ARG, "uq_init has not been called");
-    if (kind < 0 || kind > 2 || !tera_ops) return set_error(ERR_ARG, "probe_mfma: kind 0 (int8), 1 (fp16), 2 (fp64)");
+    if (kind < 0 || kind > 8 || !tera_ops) return set_error(ERR_ARG, "probe_mfma: kind 0..8");
     hipStream_t s = (hipStream_t)uq_stream();
+    const bool f64 = kind >= 2 && kind <= 5, one_wave = kind >= 3;
     // ops per wave instruction: 2*16*16*32 (int8, fp16), 2*16*16*4 (fp64)
-    const double ops = kind == 2 ? 2.0 * 16 * 16 * 4 : 2.0 * 16 * 16 * 32;
-    const int iters = kind == 2 ? 256 : 2048;
-    const unsigned grid = 4u * (unsigned)cu_count();  // 16 waves per CU
+    const double ops = f64 ? 2.0 * 16 * 16 * 4 : 2.0 * 16 * 16 * 32;
+    const int iters = kind == 2 ? 256 : kind >= 3 && kind <= 5 ? 512 : 2048;
+    // 16 waves per CU, or one wave per SIMD (16 MFMAs per iteration, not PC)
+    const unsigned grid = (one_wave ? 1u : 4u) * (unsigned)cu_count();
+    const int per_iter = one_wave ? 16 : PC;
     int* sink = nullptr;
     UQ_CHECK_HIP(hipMalloc(&sink, 4 * (size_t)grid));
     auto launch = [&]() {
-        if (kind == 0) hipLaunchKernelGGL(k_probe_mfma_i8, dim3(grid), dim3(256), 0, s, iters, sink);
-        else if (kind == 1) hipLaunchKernelGGL(k_probe_mfma_f16, dim3(grid), dim3(256), 0, s, iters, sink);
-        else hipLaunchKernelGGL(k_probe_mfma_f64, dim3(grid), dim3(256), 0, s, iters, sink);
+        switch (kind) {
+        case 0: hipLaunchKernelGGL(k_probe_mfma_i8, dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 1: hipLaunchKernelGGL(k_probe_mfma_f16, dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 2: hipLaunchKernelGGL(k_probe_mfma_f64, dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 3: hipLaunchKernelGGL((k_probe_f64_1w<true, false>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 4: hipLaunchKernelGGL((k_probe_f64_1w<true, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 5: hipLaunchKernelGGL((k_probe_f64_1w<false, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 6: hipLaunchKernelGGL((k_probe_i8_1w<true, false>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 7: hipLaunchKernelGGL((k_probe_i8_1w<true, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        default: hipLaunchKernelGGL((k_probe_i8_1w<false, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        }
     };
     hipEvent_t e0, e1;
     UQ_CHECK_HIP(hipEventCreate(&e0));
@@ -150,7 +244,7 @@ int uq_probe_mfma(int kind, double* tera_ops) {
     UQ_CHECK_HIP(hipEventSynchronize(e1));
     float ms = 0;
     UQ_CHECK_HIP(hipEventElapsedTime(&ms, e0, e1));
-    const double instrs = (double)grid * 4 * iters * PC * reps;
+    const double instrs = (double)grid * 4 * iters * per_iter * reps;
     *tera_ops = instrs * ops / (ms / 1e3) / 1e12;
     hipEventDestroy(e0);
     hipEventDestroy(e1);

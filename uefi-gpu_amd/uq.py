@@ -103,6 +103,8 @@ _SIGS = {
     "uq_prefill": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, _c_u32p]),
     "uq_prefill_gemm": (ctypes.c_int, [_vp, _c_i8p, _c_f32p, _i64, _c_f32p]),
     "uq_time_prefill_gemm": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
+    "uq_time_prefill_attention": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                                 ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]),
     "uq_prompt_tokens": (ctypes.c_int, [_vp, _c_u32p, ctypes.c_int, ctypes.c_int, _c_u32p]),
     "uq_probe_bandwidth": (ctypes.c_int, [_i64, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double)]),
@@ -353,8 +355,19 @@ def time_prefill_gemm(w, w2, tokens, reps):
     return ms.value
 
 
+def time_prefill_attention(tokens, heads, kv_heads, head_dim, quant_out, reps):
+    """Mean HIP-event ms of the prefill's causal attention on synthetic q and fp16 K/V."""
+    ms = ctypes.c_double()
+    _check(lib().uq_time_prefill_attention(tokens, heads, kv_heads, head_dim, 1 if quant_out else 0, reps,
+                                           ctypes.byref(ms)))
+    return ms.value
+
+
 def probe_mfma(kind):
-    """Achievable matrix-core rate: kind 0 int8 (TOPS), 1 fp16, 2 fp64 (TFLOP/s)."""
+    """Achievable matrix-core rate: kind 0 int8 (TOPS), 1 fp16, 2 fp64 (TFLOP/s); one
+    wave per SIMD: 3 fp64 MFMAs, 4 with an fp16 operand conversion per MFMA, 5 the
+    conversions alone; 6 int8 MFMAs, 7 beside the per-block f32 rescale, 8 the
+    rescale alone (rates of the same MFMA count)."""
     t = ctypes.c_double()
     _check(lib().uq_probe_mfma(kind, ctypes.byref(t)))
     return t.value

@@ -9,8 +9,9 @@
 // GEMM: y[t][r] = sum over 32-blocks b, in order, of
 //   f = fmaf((float)c_b, dw[r][b] * dx[t][b], f),   c_b = sum_k qw[r][k] qx[t][k]
 // (gpu_prefill.cu:29-30). c_b is one v_mfma_i32_16x16x32_i8 per block with a
-// zero accumulator; the f32 rescale runs on the VALU in the same order as the
-// reference, so results match the oracle bit for bit.
+// zero accumulator; the scale product dw*dx comes exact from an f32
+// outer-product MFMA and the convert and fmaf run on the VALU in the
+// reference's order, so results match the oracle bit for bit.
 // Operands come from the row-major planes used by decode (no second weight
 // copy), staged through LDS; the fp16 weight scales get a [block][row]
 // transpose widened to f32, so a stage's scales are contiguous float4 loads.
@@ -77,8 +78,9 @@ __global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, i
 // which makes the 16 lanes of an MFMA fragment read hit 16 distinct bank pairs.
 // MFMA 16x16x32 i8 lane layout: A lane l = row l%16, k (l/16)*8..+7; B lane l =
 // token l%16, same k; D lane l = rows (l/16)*4..+3, token l%16.
-// Per output and block the VALU does (float)c, dw*dx and the fmaf in the
-// reference's order; that work, not the MFMA, bounds this kernel.
+// Per output and block the VALU does (float)c and the fmaf in the
+// reference's order, with the scale product dw*dx from an outer-product
+// MFMA; that VALU work, not the int8 MFMA, bounds this kernel.
 constexpr int GK_BLK = 4;                  // 32-blocks per stage
 constexpr int GBM = 32;                    // rows per workgroup tile
 // Ring depth 2: one stage in flight while one is computed. The kernel is
@@ -222,20 +224,65 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU, WM>& S, int j
             if (GU) c2[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2v[m], bv, z, 0, 0, 0);
         }
     }
+    // Scale products dw[row][j] * dx[token][j] of the group's blocks, one
+    // v_mfma_f32_16x16x1f32 per row tile: four 16 x 16 outer products, the
+    // k-th in registers 4k..4k+3 at rows 4*(lane/16) + q, token lane % 16
+    // (the int8 MFMA's layout); lane l supplies the k = l/16 product's row
+    // (A) and token (B) factor. Each product is a single f32 multiply
+    // (round to nearest even, denormals kept), the value w * x has on the
+    // VALU, which keeps a third of the rescale off the VALU. Non-pair: the
+    // group's 4 blocks; gate/up pair: blocks j0, j0+1 of the gate scales,
+    // then of the up scales.
+    static_assert(GU ? NB == 2 : NB == 4, "one outer-product MFMA per group and row tile");
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    const int kq = lane >> 4, jb = GU ? (kq & 1) : kq;
+    const float bx = S.sx[(j0 + jb) * BN + wc + li];
+    v16f sc[WM];
 #pragma unroll
-    for (int jj = 0; jj < NB; jj++) {
-        const int j = j0 + jj;
-        const float x = S.sx[j * BN + wc + li];
+    for (int m = 0; m < WM; m++) {
+        const float* sws = GU && kq >= 2 ? S.sw2 : S.sw;
+        const float ax = sws[(j0 + jb) * GBM + rb + 16 * m + li];
+        v16f z16;
 #pragma unroll
-        for (int m = 0; m < WM; m++) {
-            const v4f w = *(const v4f*)(S.sw + j * GBM + rb + 16 * m + lm);
-            v4f w2;
-            if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + rb + 16 * m + lm);
+        for (int r = 0; r < 16; r++) z16[r] = 0.0f;
+        sc[m] = __builtin_amdgcn_mfma_f32_16x16x1f32(ax, bx, z16, 0, 0, 0);
+    }
+#pragma unroll
+    for (int jj = 0; jj < NB; jj++)
+#pragma unroll
+        for (int m = 0; m < WM; m++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                f[m][q] = fmaf((float)c[jj][m][q], w[q] * x, f[m][q]);
-                if (GU) g[m][q] = fmaf((float)c2[jj][m][q], w2[q] * x, g[m][q]);
+                f[m][q] = fmaf((float)c[jj][m][q], sc[m][4 * jj + q], f[m][q]);
+                if (GU) g[m][q] = fmaf((float)c2[jj][m][q], sc[m][4 * (jj + 2) + q], g[m][q]);
             }
+}
+
+// One 32-block (a partial last stage): MFMA, then the rescale with the scale
+// product on the VALU.
+template <bool GU, int WM>
+__device__ __forceinline__ void gemm_block_tail(const GemmStageLds<GU, WM>& S, int j, int wc, int rb, int lane,
+                                                float (&f)[WM][4], float (&g)[WM][4]) {
+    constexpr int BN = gemm_bn<WM>();
+    const int li = lane & 15, lm = (lane >> 4) * 4, sub = ((lane >> 4) & 1) * 8, hi = lane >> 5;
+    const v4i z = {0, 0, 0, 0};
+    const int gc = 2 * j + hi, tok = wc + li;
+    const long bv = *(const long*)(S.b + tok * 128 + ((gc ^ swz(tok)) << 4) + sub);
+    const float x = S.sx[j * BN + wc + li];
+#pragma unroll
+    for (int m = 0; m < WM; m++) {
+        const int row = rb + 16 * m + li;
+        const int off = row * 128 + ((gc ^ swz(row)) << 4) + sub;
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(*(const long*)(S.a + off), bv, z, 0, 0, 0);
+        v4i c2;
+        if (GU) c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(*(const long*)(S.a2 + off), bv, z, 0, 0, 0);
+        const v4f w = *(const v4f*)(S.sw + j * GBM + rb + 16 * m + lm);
+        v4f w2;
+        if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + rb + 16 * m + lm);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            f[m][q] = fmaf((float)c[q], w[q] * x, f[m][q]);
+            if (GU) g[m][q] = fmaf((float)c2[q], w2[q] * x, g[m][q]);
         }
     }
 }
@@ -280,13 +327,13 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
         enter(s);
         const GemmStageLds<GU, WM>& S = ring[s % GR];
         gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
-        if (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
+        if constexpr (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
     }
     if (nst > nfull) {
         enter(nfull);
         const GemmStageLds<GU, WM>& S = ring[nfull % GR];
         const int nblk = nblk_of(nfull);
-        for (int j = 0; j < nblk; j++) gemm_blocks<GU, WM, 1>(S, j, wc, rb, lane, f, g);
+        for (int j = 0; j < nblk; j++) gemm_block_tail<GU, WM>(S, j, wc, rb, lane, f, g);
     }
     const int li = lane & 15, lm = (lane >> 4) * 4;
     if (GU && WM == 2 && a.yq) {

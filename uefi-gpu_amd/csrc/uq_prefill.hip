@@ -83,11 +83,11 @@ __global__ __launch_bounds__(256) void k_pf_quant(const float* __restrict__ x, i
 // MFMA; that VALU work, not the int8 MFMA, bounds this kernel.
 constexpr int GK_BLK = 4;                  // 32-blocks per stage
 constexpr int GBM = 32;                    // rows per workgroup tile
-// Ring depth 2: one stage in flight while one is computed. The kernel is
-// VALU-bound (the per-block f32 rescale), so occupancy hides more than ring
-// depth: 2 stages fit four gate/up workgroups per CU where 4 stages fit two
-// (gate+up 104 -> 76 us at 512 tokens; 3 stages changed nothing).
-constexpr int GR = 2;
+// Ring depth (in k_pf_gemm): the gate/up pair is VALU-bound (the per-block
+// f32 rescale), so occupancy hides more than ring depth there: 2 stages fit
+// four gate/up workgroups per CU where 4 stages fit two (gate+up 104 -> 76 us
+// at 512 tokens; 3 stages changed nothing). The narrow launches wait on
+// their stage loads at 3 waves per SIMD and fill 4 stages, two at a time.
 
 // WM = MFMA row tiles per wave: WM 2 gives waves of 32 rows x 16 tokens
 // (workgroup 32 x 64), WM 1 waves of 16 rows x 16 tokens in a 2 x 2 grid
@@ -104,10 +104,6 @@ struct GemmStageLds {
     float sw2[GU ? GK_BLK * GBM : 4];
     float sx[GK_BLK * gemm_bn<WM>()];
 };
-// loads per wave per stage: A (1), A2 (1), B (WM), scales sw, sw2, sx
-template <bool GU, int WM>
-constexpr int gemm_lps() { return (GU ? 5 : 3) + WM; }
-
 typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) { uq_lds_load16(g, lds_wave_base); }
 // rows r and r+16 (read by one ds_read2 of the two MFMA row tiles) get different slots
@@ -175,6 +171,48 @@ __device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g
     if (lane < BN / 4) lds_load16(at(p.xst + t0 + (kb + jw) * (int64_t)p.mp, g.sx), S.sx + wave * BN);
 }
 
+
+// Uniform source pointers of the next full stage (scalar registers), moved
+// one stage (4 blocks) on with scalar adds; the per-lane offsets of GemmSrc
+// are added at each load. Replaces the per-stage 64-bit products of the
+// generic issue, which left each wave about as many scalar as vector
+// instructions in the narrow launches.
+template <bool GU>
+struct GemmCursor {
+    const int8_t* a;
+    const int8_t* a2;
+    const int8_t* b;
+    const float* sw;
+    const float* sw2;
+    const float* sx;
+    __device__ __forceinline__ void advance(int64_t n, int mp) {
+        a += GK_BLK * 32;
+        b += GK_BLK * 32;
+        sw += GK_BLK * n;
+        sx += GK_BLK * mp;
+        if (GU) {
+            a2 += GK_BLK * 32;
+            sw2 += GK_BLK * n;
+        }
+    }
+};
+
+// The loads of the cursor's full stage (the same bytes gemm_issue loads for
+// a stage of four blocks; wave w loads scale block row w).
+template <bool GU, int WM>
+__device__ __forceinline__ void gemm_issue_full(const GemmCursor<GU>& c, const GemmSrc& g, GemmStageLds<GU, WM>& S,
+                                                int wave, int lane) {
+    constexpr int BN = gemm_bn<WM>();
+    lds_load16(at(c.a, g.a), S.a + wave * 1024);
+    if (GU) lds_load16(at(c.a2, g.a), S.a2 + wave * 1024);
+    lds_load16(at(c.b, g.b0), S.b + (WM * wave) * 1024);
+    if (WM == 2) lds_load16(at(c.b, g.b1), S.b + (2 * wave + 1) * 1024);
+    if (lane < GBM / 4) {
+        lds_load16(at(c.sw, g.sw), S.sw + wave * GBM);
+        if (GU) lds_load16(at(c.sw2, g.sw), S.sw2 + wave * GBM);
+    }
+    if (lane < BN / 4) lds_load16(at(c.sx, g.sx), S.sx + wave * BN);
+}
 
 // Wait until at most `n` vector-memory ops of this wave are outstanding
 // (s_waitcnt vmcnt(n); expcnt and lgkmcnt left at their maxima).
@@ -289,51 +327,73 @@ __device__ __forceinline__ void gemm_block_tail(const GemmStageLds<GU, WM>& S, i
 
 template <bool GU, int WM>
 __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) GemmStageLds<GU, WM> ring[GR];
-    constexpr int LPS = gemm_lps<GU, WM>();
+    // ring stages: the gate/up pair and the wide tiles fill two, one ahead
+    // (four would halve their workgroups per CU); the narrow launches (WM 1)
+    // fill four, two at a time, with one wait and barrier per pair of stages
+    constexpr int RG = GU || WM == 2 ? 2 : 4;
+    __shared__ __attribute__((aligned(16))) GemmStageLds<GU, WM> ring[RG];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // the wave's tile: tokens wc.. of the workgroup's, rows rb..
     const int wc = WM == 2 ? wave * 16 : (wave >> 1) * 16, rb = WM == 2 ? 0 : (wave & 1) * 16;
     const int64_t r0 = (int64_t)blockIdx.x * GBM, t0 = (int64_t)blockIdx.y * gemm_bn<WM>();
-    const int64_t nb = a.k / 32, nst = (nb + GK_BLK - 1) / GK_BLK;
-    auto nblk_of = [&](int64_t s) { return (int)(nb - s * GK_BLK < GK_BLK ? nb - s * GK_BLK : GK_BLK); };
+    // k <= 16384: at most 512 blocks, 128 stages
+    const int nb = (int)(a.k / 32), nst = (nb + GK_BLK - 1) / GK_BLK, nfull = nb / GK_BLK;
+    auto nblk_of = [&](int s) { return nb - s * GK_BLK < GK_BLK ? nb - s * GK_BLK : GK_BLK; };
     float f[WM][4], g[WM][4];
 #pragma unroll
     for (int m = 0; m < WM; m++)
 #pragma unroll
         for (int q = 0; q < 4; q++) f[m][q] = g[m][q] = 0.0f;
     const GemmSrc src = gemm_src<GU, WM>(a, wave, lane);
-    // prologue: stages 0 .. GR-2 in flight
-#pragma unroll
-    for (int s = 0; s < GR - 1; s++)
-        if (s < nst) gemm_issue<GU, WM>(a, src, ring[s], r0, t0, (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
-    // stage s landed for this wave (the stages issued after it may stay in
-    // flight), then every wave's loads of stage s landed and stage s-1 is
-    // fully consumed; the next stage's loads go out
-    auto enter = [&](int64_t s) {
-        const int64_t later = (nst - 1 - s < GR - 2) ? nst - 1 - s : GR - 2;
-        if (later >= 2) wait_vm<2 * LPS>();
-        else if (later == 1) wait_vm<LPS>();
-        else wait_vm<0>();
-        stage_barrier();
-        const int64_t sn = s + GR - 1;
-        if (sn < nst) gemm_issue<GU, WM>(a, src, ring[sn % GR], r0, t0, sn * GK_BLK, nblk_of(sn), wave, lane);
+    GemmCursor<GU> cur{a.w_qs + r0 * a.k, GU ? a.w2_qs + r0 * a.k : nullptr, a.xq + t0 * a.k,
+                       a.w_ds + r0 + wave * a.n, GU ? a.w2_ds + r0 + wave * a.n : nullptr,
+                       a.xst + t0 + (int64_t)wave * a.mp};
+    // stage s's loads, issued in stage order: full stages from the cursor, a
+    // partial last stage through the clamping issue
+    auto issue = [&](int s) {
+        GemmStageLds<GU, WM>& S = ring[s & (RG - 1)];
+        if (s < nfull) {
+            gemm_issue_full<GU, WM>(cur, src, S, wave, lane);
+            cur.advance(a.n, a.mp);
+        } else {
+            gemm_issue<GU, WM>(a, src, S, r0, t0, (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
+        }
     };
-    // full stages in a loop with no other path, so the accumulators stay in
-    // their registers across iterations; a partial last stage after it
-    const int64_t nfull = nb / GK_BLK;
-    for (int64_t s = 0; s < nfull; s++) {
-        enter(s);
-        const GemmStageLds<GU, WM>& S = ring[s % GR];
-        gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
-        if constexpr (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
+    auto compute = [&](int s) {
+        const GemmStageLds<GU, WM>& S = ring[s & (RG - 1)];
+        if (s < nfull) {
+            gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
+            if constexpr (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
+        } else {
+            const int nblk = nblk_of(s);
+            for (int j = 0; j < nblk; j++) gemm_block_tail<GU, WM>(S, j, wc, rb, lane, f, g);
+        }
+    };
+    // Each step: this wave's loads of the step's stages landed (nothing later
+    // is in flight), then the barrier makes every wave's loads visible and
+    // frees the ring slots the next loads fill. Full steps run in a loop with
+    // no other path, so the accumulators stay in their registers.
+    constexpr int STEP = RG / 2;
+    for (int s = 0; s < STEP && s < nst; s++) issue(s);
+    int s = 0;
+    for (; s + STEP <= nfull; s += STEP) {
+        wait_vm<0>();
+        stage_barrier();
+#pragma unroll
+        for (int u = STEP; u < 2 * STEP; u++)
+            if (s + u < nst) issue(s + u);
+#pragma unroll
+        for (int u = 0; u < STEP; u++) {
+            gemm_blocks<GU, WM, GU ? 2 : 4>(ring[(s + u) & (RG - 1)], 0, wc, rb, lane, f, g);
+            if constexpr (GU) gemm_blocks<GU, WM, 2>(ring[(s + u) & (RG - 1)], 2, wc, rb, lane, f, g);
+        }
     }
-    if (nst > nfull) {
-        enter(nfull);
-        const GemmStageLds<GU, WM>& S = ring[nfull % GR];
-        const int nblk = nblk_of(nfull);
-        for (int j = 0; j < nblk; j++) gemm_block_tail<GU, WM>(S, j, wc, rb, lane, f, g);
+    if (s < nst) {
+        // fewer than STEP full stages and / or the partial stage remain, all issued
+        wait_vm<0>();
+        stage_barrier();
+        for (int u = s; u < nst; u++) compute(u);
     }
     const int li = lane & 15, lm = (lane >> 4) * 4;
     if (GU && WM == 2 && a.yq) {

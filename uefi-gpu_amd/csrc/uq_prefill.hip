@@ -262,38 +262,55 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU, WM>& S, int j
             if (GU) c2[jj][m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2v[m], bv, z, 0, 0, 0);
         }
     }
-    // Scale products dw[row][j] * dx[token][j] of the group's blocks, one
-    // v_mfma_f32_16x16x1f32 per row tile: four 16 x 16 outer products, the
-    // k-th in registers 4k..4k+3 at rows 4*(lane/16) + q, token lane % 16
-    // (the int8 MFMA's layout); lane l supplies the k = l/16 product's row
-    // (A) and token (B) factor. Each product is a single f32 multiply
-    // (round to nearest even, denormals kept), the value w * x has on the
-    // VALU, which keeps a third of the rescale off the VALU. Non-pair: the
-    // group's 4 blocks; gate/up pair: blocks j0, j0+1 of the gate scales,
-    // then of the up scales.
-    static_assert(GU ? NB == 2 : NB == 4, "one outer-product MFMA per group and row tile");
+    // Scale products dw[row][j] * dx[token][j] from v_mfma_f32_16x16x1f32:
+    // four 16 x 16 outer products, the k-th in registers 4k..4k+3 at rows
+    // 4*(lane/16) + q, token lane % 16 (the int8 MFMA's layout); lane l
+    // supplies the k = l/16 product's row (A) and token (B) factor. Each
+    // product is a single f32 multiply (round to nearest even, denormals
+    // kept), the value w * x has on the VALU, which keeps a third of the
+    // rescale off the VALU.
     typedef float v16f __attribute__((ext_vector_type(16)));
-    const int kq = lane >> 4, jb = GU ? (kq & 1) : kq;
-    const float bx = S.sx[(j0 + jb) * BN + wc + li];
-    v16f sc[WM];
-#pragma unroll
-    for (int m = 0; m < WM; m++) {
-        const float* sws = GU && kq >= 2 ? S.sw2 : S.sw;
-        const float ax = sws[(j0 + jb) * GBM + rb + 16 * m + li];
+    const int kq = lane >> 4;
+    if constexpr (GU) {
+        // gate/up pair, one block per group (the live MFMA results and
+        // products of two blocks would cost the fourth wave per SIMD):
+        // product k = (gate k < 2 / up k >= 2) x (row tile k % 2)
+        static_assert(NB == 1, "pair: one block per group");
+        const int mk = (kq & 1) < WM ? (kq & 1) : 0;
+        const float bx = S.sx[j0 * BN + wc + li];
+        const float* sws = kq >= 2 ? S.sw2 : S.sw;
+        const float ax = sws[j0 * GBM + rb + 16 * mk + li];
         v16f z16;
 #pragma unroll
         for (int r = 0; r < 16; r++) z16[r] = 0.0f;
-        sc[m] = __builtin_amdgcn_mfma_f32_16x16x1f32(ax, bx, z16, 0, 0, 0);
-    }
-#pragma unroll
-    for (int jj = 0; jj < NB; jj++)
+        const v16f sc = __builtin_amdgcn_mfma_f32_16x16x1f32(ax, bx, z16, 0, 0, 0);
 #pragma unroll
         for (int m = 0; m < WM; m++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                f[m][q] = fmaf((float)c[jj][m][q], sc[m][4 * jj + q], f[m][q]);
-                if (GU) g[m][q] = fmaf((float)c2[jj][m][q], sc[m][4 * (jj + 2) + q], g[m][q]);
+                f[m][q] = fmaf((float)c[0][m][q], sc[4 * m + q], f[m][q]);
+                g[m][q] = fmaf((float)c2[0][m][q], sc[4 * (2 + m) + q], g[m][q]);
             }
+    } else {
+        // one product per block of the group's 4, per row tile
+        static_assert(NB == 4, "one outer-product MFMA per group and row tile");
+        const float bx = S.sx[(j0 + kq) * BN + wc + li];
+        v16f sc[WM];
+#pragma unroll
+        for (int m = 0; m < WM; m++) {
+            const float ax = S.sw[(j0 + kq) * GBM + rb + 16 * m + li];
+            v16f z16;
+#pragma unroll
+            for (int r = 0; r < 16; r++) z16[r] = 0.0f;
+            sc[m] = __builtin_amdgcn_mfma_f32_16x16x1f32(ax, bx, z16, 0, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < NB; jj++)
+#pragma unroll
+            for (int m = 0; m < WM; m++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) f[m][q] = fmaf((float)c[jj][m][q], sc[m][4 * jj + q], f[m][q]);
+    }
 }
 
 // One 32-block (a partial last stage): MFMA, then the rescale with the scale
@@ -363,8 +380,12 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
     auto compute = [&](int s) {
         const GemmStageLds<GU, WM>& S = ring[s & (RG - 1)];
         if (s < nfull) {
-            gemm_blocks<GU, WM, GU ? 2 : 4>(S, 0, wc, rb, lane, f, g);
-            if constexpr (GU) gemm_blocks<GU, WM, 2>(S, 2, wc, rb, lane, f, g);
+            if constexpr (GU) {
+#pragma unroll
+                for (int j = 0; j < GK_BLK; j++) gemm_blocks<GU, WM, 1>(S, j, wc, rb, lane, f, g);
+            } else {
+                gemm_blocks<GU, WM, GK_BLK>(S, 0, wc, rb, lane, f, g);
+            }
         } else {
             const int nblk = nblk_of(s);
             for (int j = 0; j < nblk; j++) gemm_block_tail<GU, WM>(S, j, wc, rb, lane, f, g);
@@ -385,8 +406,13 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
             if (s + u < nst) issue(s + u);
 #pragma unroll
         for (int u = 0; u < STEP; u++) {
-            gemm_blocks<GU, WM, GU ? 2 : 4>(ring[(s + u) & (RG - 1)], 0, wc, rb, lane, f, g);
-            if constexpr (GU) gemm_blocks<GU, WM, 2>(ring[(s + u) & (RG - 1)], 2, wc, rb, lane, f, g);
+            // the pair block by block, the others as one group of 4
+            if constexpr (GU) {
+#pragma unroll
+                for (int j = 0; j < GK_BLK; j++) gemm_blocks<GU, WM, 1>(ring[(s + u) & (RG - 1)], j, wc, rb, lane, f, g);
+            } else {
+                gemm_blocks<GU, WM, GK_BLK>(ring[(s + u) & (RG - 1)], 0, wc, rb, lane, f, g);
+            }
         }
     }
     if (s < nst) {

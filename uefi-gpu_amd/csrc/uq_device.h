@@ -49,19 +49,21 @@ UQ_HD float uq_bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
 // Algorithm: Copyright (C) 1993 by Sun Microsystems, Inc.; notice kept in
 // third_party/NOTICE.sunpro-expf.
 UQ_HD float uq_expf(float x) {
-    // Branch-free: the reduction's cases (k = 0 for |x| <= ln2/2, +-1 up to
-    // 1.5 ln2, else x/ln2 rounded half away from zero), the small-|x| and
-    // special results and scalbnf's pre-scaling are selects, so divergent
-    // lanes run one path. k = 0 reproduces the unreduced operands exactly
-    // (x - 0 * ln2hi = x, lo = +0) and scaling by 2^0 is exact, so every
-    // input gives the branchy form's bits (checked over all 2^32 inputs).
+    // Branch-free, and with fewer selects than the branchy form has cases:
+    // - k = x/ln2 rounded half away from zero everywhere. The branchy form
+    //   takes k = 0 for |x| <= ln2/2 and +-1 up to 1.5 ln2; where the
+    //   rounding gives another k there, that reduction yields the same bits.
+    // - scalbnf(y, k) as two multiplies by 2^(k>>1) and 2^(k - (k>>1)): the
+    //   exact y * 2^k is rounded once either way (only the last multiply can
+    //   round, into the subnormal range or to infinity).
+    // - the small-|x| result and the special values stay selects.
+    // Every one of the 2^32 inputs gives the branchy form's bits (checked
+    // exhaustively against the oracle's expf).
     const uint32_t bx = __builtin_bit_cast(uint32_t, x);
     const uint32_t ax = bx & 0x7fffffffu;
     const bool neg = (bx >> 31) != 0;
     const float t = fminf(fmaxf(x * uq_bits_f(0x3fb8aa3bu), -160.0f), 160.0f);
-    int k = (int)(t + (neg ? -0.5f : 0.5f));
-    k = ax > 0x3f851592u ? k : (neg ? -1 : 1);
-    k = ax > 0x3eb17218u ? k : 0;
+    const int k = (int)(t + (neg ? -0.5f : 0.5f));
     const float kf = (float)k;
     const float hi = x - kf * uq_bits_f(0x3f317200u);
     const float lo = kf * uq_bits_f(0x35bfbe8eu);
@@ -71,10 +73,9 @@ UQ_HD float uq_expf(float x) {
     const float c = xr - poly;
     const float q = (xr * c) / (2.0f - c);
     const float y = 1.0f + ((q - lo) + hi);
-    // scalbnf(y, k) for the k in [-150, 128] that finite, non-special inputs reach
-    const float s1 = k > 127 ? 0x1p127f : (k < -126 ? 0x1p-102f : 1.0f);
-    const int k2 = k > 127 ? k - 127 : (k < -126 ? k + 102 : k);
-    float r = (y * s1) * uq_bits_f((uint32_t)(127 + k2) << 23);
+    // |k| <= 161 (t is clamped), so both factors are normal powers of two
+    const int ka = k >> 1, kb = k - ka;
+    float r = (y * uq_bits_f((uint32_t)(127 + ka) << 23)) * uq_bits_f((uint32_t)(127 + kb) << 23);
     r = ax <= 0x39000000u ? 1.0f + x : r;
     r = neg && ax >= 0x42cff1b5u ? 0.0f : r;
     r = !neg && ax >= 0x42b17218u ? x * 0x1p127f : r;

@@ -102,6 +102,12 @@ UQ_DEV int4 uq_ntload16(const void* p) {
     const uq_v4i v = __builtin_nontemporal_load((const uq_v4i*)p);
     return make_int4(v.x, v.y, v.z, v.w);
 }
+// 12-byte non-temporal load (one global_load_dwordx3), 4-byte aligned.
+typedef int uq_v3i __attribute__((ext_vector_type(3), aligned(4)));
+UQ_DEV int3 uq_ntload12(const void* p) {
+    const uq_v3i v = __builtin_nontemporal_load((const uq_v3i*)p);
+    return make_int3(v.x, v.y, v.z);
+}
 
 // 4-way signed int8 dot with int32 accumulate (v_dot4_i32_i8).
 UQ_DEV int uq_dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

@@ -121,52 +121,62 @@ __global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q,
     if (miss) atomicAdd(bad, miss);
 }
 // Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, 12 packed scale bytes, d 2)
-// -> q[blk][96] = hmask with its bits permuted (Q3K::hpack) | qs, sc[blk][16] =
-// the sixteen 6-bit scales minus 32 as signed bytes, d[blk]. The verify kernel
-// undoes the permutation and packs the scales back to 12 bytes.
+// -> four 64-value units (Q3K::pack_unit): q[blk][4][16] (words A), p[blk][4][12]
+// (words B and the four scales - 32), d[blk]. The verify kernel rebuilds the
+// GGUF bytes from the planes (hmask, qs, the 12 scale bytes, d).
 __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
                                                    int8_t* __restrict__ q, int8_t* __restrict__ sc,
                                                    uint16_t* __restrict__ d) {
     const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
     if (blk >= blocks) return;
-    const uint8_t* p = src + blk * 110;
-    uint8_t* dq = (uint8_t*)q + blk * 96;
-    for (int j = 0; j < 32; j += 4) {
-        const uint32_t h = p[j] | (p[j + 1] << 8) | (p[j + 2] << 16) | ((uint32_t)p[j + 3] << 24);
-        const uint32_t r = Q3K::hpack(h);
-        for (int b = 0; b < 4; b++) dq[j + b] = (uint8_t)(r >> (8 * b));
+    const uint8_t* g = src + blk * 110;
+    uint32_t* qa = (uint32_t*)q + blk * 16;
+    uint32_t* pw = (uint32_t*)sc + blk * 12;
+    for (int p = 0; p < 4; p++) {
+        uint32_t A[4], P[3];
+        Q3K::pack_unit(g, p, A, P);
+        for (int t = 0; t < 4; t++) qa[4 * p + t] = A[t];
+        for (int k = 0; k < 3; k++) pw[3 * p + k] = P[k];
     }
-    for (int j = 32; j < 96; j++) dq[j] = p[j];
-    for (int k = 0; k < 16; k++) sc[blk * 16 + k] = (int8_t)(Q3K::scale6_k(p + 96, k) - 32);
-    d[blk] = (uint16_t)(p[108] | (p[109] << 8));
+    d[blk] = (uint16_t)(g[108] | (g[109] << 8));
 }
 __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const int8_t* __restrict__ sc,
                                                    const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
                                                    int64_t blocks, unsigned* __restrict__ bad) {
     const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
     if (blk >= blocks) return;
-    const uint8_t* p = src + blk * 110;
-    unsigned miss = 0;
-    const uint8_t* qb = (const uint8_t*)q + blk * 96;
-    for (int j = 0; j < 32; j += 4) {
-        const uint32_t r = qb[j] | (qb[j + 1] << 8) | (qb[j + 2] << 16) | ((uint32_t)qb[j + 3] << 24);
-        const uint32_t h = Q3K::hunpack(r);
-        for (int b = 0; b < 4; b++) miss += (uint8_t)(h >> (8 * b)) != p[j + b];
-    }
-    for (int j = 32; j < 96; j++) miss += qb[j] != p[j];
+    const uint8_t* g = src + blk * 110;
+    const uint32_t* qa = (const uint32_t*)q + blk * 16;
+    const uint32_t* pw = (const uint32_t*)sc + blk * 12;
+    uint8_t hm[32] = {}, qs[64] = {};
     int v[16];
-    for (int k = 0; k < 16; k++) {
-        v[k] = sc[blk * 16 + k] + 32;
-        miss += v[k] < 0 || v[k] > 63;
+    for (int p = 0; p < 4; p++) {
+        const uint32_t A[4] = {qa[4 * p], qa[4 * p + 1], qa[4 * p + 2], qa[4 * p + 3]};
+        const uint32_t P[3] = {pw[3 * p], pw[3 * p + 1], pw[3 * p + 2]};
+        for (int c = 0; c < 4; c++) {
+            v[4 * p + c] = (int)(int8_t)(P[2] >> (8 * c)) + 32;
+            for (int t = 0; t < 4; t++)
+                for (int b = 0; b < 4; b++) {
+                    int low2, hbit;
+                    Q3K::unit_parts(A, P, c, t, b, low2, hbit);
+                    const int i = 64 * p + 16 * c + 4 * t + b, n = i >> 7, j = (i >> 5) & 3, l = i & 31;
+                    qs[32 * n + l] |= (uint8_t)(low2 << (2 * j));
+                    hm[l] |= (uint8_t)(hbit << (4 * n + j));
+                }
+        }
     }
-    for (int k = 0; k < 8; k++) miss += (uint8_t)((v[k] & 0xF) | ((v[k + 8] & 0xF) << 4)) != p[96 + k];
+    unsigned miss = 0;
+    for (int j = 0; j < 32; j++) miss += hm[j] != g[j];
+    for (int j = 0; j < 64; j++) miss += qs[j] != g[32 + j];
+    for (int k = 0; k < 16; k++) miss += v[k] < 0 || v[k] > 63;
+    for (int k = 0; k < 8; k++) miss += (uint8_t)((v[k] & 0xF) | ((v[k + 8] & 0xF) << 4)) != g[96 + k];
     for (int m = 0; m < 4; m++) {
         int b = 0;
-        for (int g = 0; g < 4; g++) b |= ((v[4 * g + m] >> 4) & 3) << (2 * g);
-        miss += (uint8_t)b != p[104 + m];
+        for (int gr = 0; gr < 4; gr++) b |= ((v[4 * gr + m] >> 4) & 3) << (2 * gr);
+        miss += (uint8_t)b != g[104 + m];
     }
-    miss += (uint8_t)(d[blk] & 0xff) != p[108];
-    miss += (uint8_t)(d[blk] >> 8) != p[109];
+    miss += (uint8_t)(d[blk] & 0xff) != g[108];
+    miss += (uint8_t)(d[blk] >> 8) != g[109];
     if (miss) atomicAdd(bad, miss);
 }
 
@@ -321,7 +331,8 @@ template <class KQ, int LPR, int NBL, bool GATEUP>
 __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, float* __restrict__ y,
                                                   int64_t rows, int64_t K, int64_t share) {
-    // dynamic LDS sized to K (xl_lds_bytes): x (K int8), its scales (K/32 f32), its 16-value sums (K/16 int)
+    // dynamic LDS sized to K (xl_lds_bytes): x (K int8), its scales (K/32 f32), its 16-value sums (K/16
+    // int, as KQ::stage16 forms them)
     extern __shared__ __attribute__((aligned(16))) int8_t xl_lds[];
     int8_t* lx = xl_lds;
     float* lxs = (float*)(xl_lds + K);
@@ -338,7 +349,7 @@ __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_
         int c = uq_dot4(ones, v.x, 0);
         c = uq_dot4(ones, v.y, c);
         c = uq_dot4(ones, v.z, c);
-        ls16[g] = uq_dot4(ones, v.w, c);
+        ls16[g] = KQ::stage16(g, uq_dot4(ones, v.w, c));
     }
     for (int b = threadIdx.x; b < K / 32; b += WG) lxs[b] = xs[b];
     __syncthreads();
@@ -379,16 +390,23 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
             c = uq_dot4(h ? Q4K::hi4(wq) : Q4K::lo4(wq), xp[k], c);
         }
     } else {
-        const int64_t sb = (row * (K / 256)) + b / 16;
-        const int s = (int)(b % 16), n = s >> 3, j = (s >> 1) & 3, h = s & 1;
-        const uint8_t* blk = (const uint8_t*)w.qs + sb * 96;
+        // sub-block b of the row: unit (superblock b / 16, p = (b / 4) % 4), sub-block c = b % 4 of the unit
+        const int64_t un = (row * (K / 256)) * 4 + b / 4;
+        const int cc = (int)(b & 3);
+        const uint32_t* qa = (const uint32_t*)w.qs + un * 4;
+        const uint32_t* pw = (const uint32_t*)w.sc + un * 3;
+        const uint32_t A[4] = {qa[0], qa[1], qa[2], qa[3]};
+        const uint32_t P[3] = {pw[0], pw[1], pw[2]};
         const int* xp = (const int*)x;
-        for (int k = 0; k < 4; k++) {
-            const unsigned qv = *(const unsigned*)(blk + 32 + 32 * n + 16 * h + 4 * k);
-            const unsigned hv = *(const unsigned*)(blk + 16 * h + 4 * k);  // repacked hmask
-            const int v = (int)(((qv >> (2 * j)) & 0x03030303u) | (((hv >> Q3K::hpos(4 * n + j)) & 0x01010101u) << 2));
-            c = uq_dot4(v, xp[k], c);
-            c -= 4 * uq_dot4(0x01010101, xp[k], 0);
+        for (int t = 0; t < 4; t++) {
+            int v = 0;
+            for (int bb = 0; bb < 4; bb++) {
+                int low2, hbit;
+                Q3K::unit_parts(A, P, cc, t, bb, low2, hbit);
+                v |= (low2 | hbit << 2) << (8 * bb);
+            }
+            c = uq_dot4(v, xp[t], c);
+            c -= 4 * uq_dot4(0x01010101, xp[t], 0);
         }
     }
     dots[i] = c;
@@ -427,13 +445,12 @@ void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* 
     // take one row block per workgroup and leave the balancing to the
     // dispatcher, which refills a CU as its workgroups retire: measured faster
     // than resident workgroups striding over the rows (Q8_0 lm_head 81% -> 85%
-    // of HBM peak). Q3_K, VALU-bound with a per-workgroup staging prologue,
-    // does best with twice the resident count striding.
+    // of HBM peak).
     const int64_t cu = cu_count(), m = (w.m + cu * RPB - 1) / (cu * RPB);
     const int64_t fit = cu * resident_blocks(kern, lds);
     const int64_t nblk = (w.m + RPB - 1) / RPB;
     int64_t g = m * cu;
-    if (g > fit) g = KQ::UNIT >= 128 ? 2 * fit : nblk;
+    if (g > fit) g = nblk;
     if (g > w.m) g = w.m;
     const unsigned grid = (unsigned)g;
     const int64_t share = w.m / g;
@@ -460,8 +477,7 @@ int launch_kind(const Weight& w, const Weight* w2, const int8_t* xq, const float
     if (nu <= (int64_t)(L) * (B)) { launch_t<KQ, L, B, true>(w, w2, xq, xs, y, s); return OK; }
     if constexpr (KQ::UNIT >= 64) {
         if (w.n <= MAX_XL) {
-            if (KQ::UNIT >= 128) { UQ_TRYX(16, 1) }
-            UQ_TRYX(4, 1) UQ_TRYX(4, 2) UQ_TRYX(4, 3) UQ_TRYX(8, 3) UQ_TRYX(16, 3) UQ_TRYX(32, 3) UQ_TRYX(64, 3)
+            UQ_TRYX(4, 1) UQ_TRYX(4, 2) UQ_TRYX(4, 3) UQ_TRYX(8, 3) UQ_TRYX(8, 4) UQ_TRYX(16, 3) UQ_TRYX(32, 3) UQ_TRYX(64, 3)
             UQ_TRYX(64, 4) UQ_TRYX(64, 6) UQ_TRYX(64, 8)
         }
     }

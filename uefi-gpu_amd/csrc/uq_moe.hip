@@ -660,7 +660,7 @@ void moe_launch_t(const uq_moe* m, const MoeDev& d, hipStream_t s) {
                        sd);
 }
 
-int unit_of(uint32_t kind) { return kind == KIND_Q3_K ? 128 : kind == KIND_Q4_K ? 64 : 16; }
+int unit_of(uint32_t kind) { return kind == KIND_Q8_0 ? 16 : 64; }
 
 int moe_launch(const uq_moe* m, const MoeDev& d, hipStream_t s) {
     const int D = m->D, F = m->F;
@@ -674,9 +674,9 @@ int moe_launch(const uq_moe* m, const MoeDev& d, hipStream_t s) {
     }
     if (m->kind == KIND_Q3_K && m->shared_kind == KIND_Q8_0) {
         UQ_MOE(Q3K, 1, Q8, 8, 8, 1, 1)
-        UQ_MOE(Q3K, 2, Q8, 16, 8, 1, 1)
-        UQ_MOE(Q3K, 2, Q8, 16, 16, 1, 2)
-        UQ_MOE(Q3K, 2, Q8, 16, 32, 1, 4)
+        UQ_MOE(Q3K, 2, Q8, 8, 8, 2, 1)
+        UQ_MOE(Q3K, 2, Q8, 8, 16, 2, 2)
+        UQ_MOE(Q3K, 4, Q8, 16, 32, 2, 4)
     }
     if (m->kind == KIND_Q4_K && m->shared_kind == KIND_Q8_0) {
         UQ_MOE(Q4K, 2, Q8, 8, 16, 1, 1)

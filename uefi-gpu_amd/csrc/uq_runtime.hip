@@ -262,10 +262,11 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
         off_d = off_sc + align256(blocks * 16);
         total = off_d + align256(blocks * 4);
     } else {
+        // Q3_K: per superblock four units of 16 + 12 bytes, then d
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
-        off_sc = align256(blocks * 96);
-        off_d = off_sc + align256(blocks * 16);
+        off_sc = align256(blocks * 64);
+        off_d = off_sc + align256(blocks * 48);
         total = off_d + align256(blocks * 2);
     }
     UQ_CHECK_HIP(hipMalloc(&w.alloc, total));

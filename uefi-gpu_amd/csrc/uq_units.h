@@ -77,6 +77,8 @@ struct Q4K {
         x.xl = sum16(x.a1, sum16(x.a0, 0));
         x.xh = sum16(x.b1, sum16(x.b0, 0));
     }
+    // the staged 16-value sum of group g of the row (used as is)
+    static UQ_DEV int stage16(int, int sum) { return sum; }
     // from an activation staged with its 16-value sums s16 (LDS)
     static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
         const int4* p = (const int4*)(xq + (size_t)u * 64);
@@ -145,145 +147,159 @@ struct Q4K {
     }
 };
 
-// Q3_K unit: half n of a superblock = 128 values = 4 activation blocks j.
-// Block j's 32 values use qs[32n .. 32n+31] bits 2j..2j+1 and hmask[0..31]
-// bit 4n+j; value = low2 - 4*(1-hbit) = (low2 | hbit << 2) - 4; each 16
-// values carry a 6-bit scale s (factor s - 32). Planes (repacked at upload,
-// byte-verified): q[sb][96] = hmask | qs (non-temporal loads), sc[sb][16] =
-// the sixteen (s - 32) as signed bytes, d[sb] fp16. The activation scales and
-// the sums of each 16 activations (for the -4 offset) are formed once at load.
+// Q3_K unit: a quarter of a superblock = 64 consecutive values = activation
+// blocks 2u and 2u+1 = the four 16-value sub-blocks 4p..4p+3 of the GGUF
+// superblock (p = u mod 4), each with its 6-bit scale s (factor s - 32). GGUF
+// value = low2 - 4*(1 - hbit) = v3 - 4 with v3 = low2 | hbit << 2 in 0..7.
+// Planes (repacked at upload, byte-verified), per unit:
+//   q[u][16]: words A_t, t = 0..3; byte b of A_t holds value 16c + 4t + b of
+//             sub-block c as: bits 0-2 v3 (c = 0), bit 3 hbit (c = 1), bits
+//             4-6 v3 (c = 2), bit 7 hbit (c = 3);
+//   p[u][12]: words B_0, B_1 with the low2 of sub-blocks 1 and 3: byte b of
+//             B_a holds t = 2a at bits 0-1 (c = 1) and 4-5 (c = 3), t = 2a+1 at
+//             bits 2-3 and 6-7; then the four s - 32 as signed bytes;
+//   d[sb]:    fp16.
+// Sub-blocks 0 and 2 assemble with one AND per word (2 at 16x scale), 1 and 3
+// with one AND-OR of B and the once-shifted A (3 at 16x scale). Each lane's
+// loads are one 16-byte and one 12-byte piece per unit, contiguous across
+// the lanes of a row, plus the superblock's d.
 struct Q3K {
-    static constexpr int UNIT = 128;
-    struct X { int4 v[8]; double s[4]; int sx[8]; };
-    static UQ_DEV int dot16(const int4& w, const int4& xv, int c) {
-        c = uq_dot4(w.x, xv.x, c); c = uq_dot4(w.y, xv.y, c);
-        c = uq_dot4(w.z, xv.z, c); return uq_dot4(w.w, xv.w, c);
+    static constexpr int UNIT = 64;
+    // v: the unit's 64 activations by sub-block; s0, s1: the two block
+    // scales; c: per sub-block c the start of its dot, -4 * GS(c) * (sum of
+    // its 16 activations), GS = 1 for sub-blocks 0-1 and 16 for 2-3
+    struct X { int4 v[4]; double s0, s1; int4 c; };
+    static UQ_DEV int gs_corr(int c, int sum) { return uq_mul24(sum, c >= 2 ? -64 : -4); }
+    // the staged 16-value sum of group g of the row, as the dot's start
+    static UQ_DEV int stage16(int g, int sum) { return gs_corr(g & 3, sum); }
+    static UQ_DEV int sum16(const int4& v) {
+        const int ones = 0x01010101;
+        int c = uq_dot4(ones, v.x, 0);
+        c = uq_dot4(ones, v.y, c);
+        c = uq_dot4(ones, v.z, c);
+        return uq_dot4(ones, v.w, c);
     }
     static UQ_DEV void load_x(X& x, const int8_t* xq, const float* xs, int u) {
-        const int4* p = (const int4*)(xq + (size_t)u * 128);
+        const int4* p = (const int4*)(xq + (size_t)u * 64);
 #pragma unroll
-        for (int k = 0; k < 8; k++) x.v[k] = p[k];
-#pragma unroll
-        for (int k = 0; k < 4; k++) x.s[k] = (double)xs[4 * u + k];
-        const int ones = 0x01010101;
-#pragma unroll
-        for (int k = 0; k < 8; k++) x.sx[k] = dot16(make_int4(ones, ones, ones, ones), x.v[k], 0);
+        for (int k = 0; k < 4; k++) x.v[k] = p[k];
+        x.s0 = (double)xs[2 * u];
+        x.s1 = (double)xs[2 * u + 1];
+        x.c = make_int4(gs_corr(0, sum16(x.v[0])), gs_corr(1, sum16(x.v[1])), gs_corr(2, sum16(x.v[2])),
+                        gs_corr(3, sum16(x.v[3])));
     }
+    // from an activation staged with stage16's starts (LDS)
     static UQ_DEV void load_x_pre(X& x, const int8_t* xq, const float* xs, const int* s16, int u) {
-        const int4* p = (const int4*)(xq + (size_t)u * 128);
+        const int4* p = (const int4*)(xq + (size_t)u * 64);
 #pragma unroll
-        for (int k = 0; k < 8; k++) x.v[k] = p[k];
-#pragma unroll
-        for (int k = 0; k < 4; k++) x.s[k] = (double)xs[4 * u + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) x.sx[k] = s16[8 * u + k];
+        for (int k = 0; k < 4; k++) x.v[k] = p[k];
+        x.s0 = (double)xs[2 * u];
+        x.s1 = (double)xs[2 * u + 1];
+        x.c = *(const int4*)(s16 + 4 * u);
     }
-    // The hmask plane is repacked at upload: GGUF bit 4n+j of a byte (the
-    // high bit of value 128n + 32j + l, l the byte index) moves to bit
-    // 2 + 2j + n for j < 3 and to bit n for j = 3, so that group j of unit n
-    // assembles from one AND of the (for unit 1 once-shifted) hmask word and
-    // one AND-OR with the 2-bit field, with the value scaled by GS[j] = 1, 4,
-    // 16 (j = 3: one more shift each side, scale 1).
-    static UQ_DEV int hpos(int b) { const int n = b >> 2, j = b & 3; return j < 3 ? 2 + 2 * j + n : n; }
-    static UQ_DEV uint32_t hpack(uint32_t h) {
-        uint32_t r = 0;
-        for (int b = 0; b < 8; b++) r |= ((h >> b) & 0x01010101u) << hpos(b);
-        return r;
-    }
-    static UQ_DEV uint32_t hunpack(uint32_t h) {
-        uint32_t r = 0;
-        for (int b = 0; b < 8; b++) r |= ((h >> hpos(b)) & 0x01010101u) << b;
-        return r;
-    }
-    template <int j>
-    static UQ_DEV uint32_t v3(uint32_t q, uint32_t hh) {
-        if (j == 0) return (q & 0x03030303u) | (hh & 0x04040404u);
-        if (j == 1) return (q & 0x0C0C0C0Cu) | (hh & 0x10101010u);
-        if (j == 2) return (q & 0x30303030u) | (hh & 0x40404040u);
-        return ((q >> 6) & 0x03030303u) | ((hh << 2) & 0x04040404u);
-    }
-    template <int j>
-    static UQ_DEV int4 extract(const int4& q, const int4& hh) {
-        return make_int4((int)v3<j>((uint32_t)q.x, (uint32_t)hh.x), (int)v3<j>((uint32_t)q.y, (uint32_t)hh.y),
-                         (int)v3<j>((uint32_t)q.z, (uint32_t)hh.z), (int)v3<j>((uint32_t)q.w, (uint32_t)hh.w));
-    }
-    static UQ_DEV int4 shr1(const int4& h) {
-        return make_int4((int)((uint32_t)h.x >> 1), (int)((uint32_t)h.y >> 1), (int)((uint32_t)h.z >> 1),
-                         (int)((uint32_t)h.w >> 1));
-    }
-    struct W { int4 h0, h1, q0, q1; uint32_t sc0, sc1; uint16_t d; };
-    // row base pointers (nu = 2 * superblocks per row)
-    struct R { const uint8_t* blk; const uint8_t* sc; const uint16_t* d; };
+    struct W { int4 a; int3 p; uint16_t d; };
+    // row base pointers (nu = 4 * superblocks per row)
+    struct R { const uint8_t* a; const uint8_t* p; const uint16_t* d; };
     static UQ_DEV R row_ptr(const WArgs& w, int64_t row, int64_t nu) {
-        const int64_t sb0 = row * (nu >> 1);
-        return R{(const uint8_t*)w.qs + sb0 * 96, w.sc + sb0 * 16, w.d + sb0};
+        return R{(const uint8_t*)w.qs + row * nu * 16, w.sc + row * nu * 12, w.d + row * (nu >> 2)};
     }
     static UQ_DEV W load_u(const R& r, int u) {
-        const int sb = u >> 1, n = u & 1;
-        const uint8_t* blk = r.blk + sb * 96;
-        const uint8_t* q = blk + 32 + 32 * n;
-        const uint2 sc = *(const uint2*)(r.sc + sb * 16 + 8 * n);
-        return W{uq_ntload16(blk), uq_ntload16(blk + 16), uq_ntload16(q), uq_ntload16(q + 16), sc.x, sc.y, r.d[sb]};
+        return W{uq_ntload16(r.a + (int64_t)u * 16), uq_ntload12(r.p + (int64_t)u * 12), r.d[u >> 2]};
     }
     static UQ_DEV W load_w(const WArgs& w, int64_t row, int64_t nu, int u) { return load_u(row_ptr(w, row, nu), u); }
-    // Group j of the unit: D = GS[j] * (sum of the 16 (value+4) x products)
-    // - 4 * GS[j] * sum(x), started from that correction (the accumulator of
-    // the first dot4); T = s0 * D0 + s1 * D1 = GS[j] * (s0 i0 + s1 i1) in
-    // 24-bit multiplies (|D| <= 16 * 16 * 4 * 127 < 2^23). d*(s-32) is exact
-    // in f32 (11-bit x 6-bit), so the block's (d*s0)*i0 + (d*s1)*i1 is
-    // d*(s0*i0 + s1*i1), and (d / GS[j]) * T is that same double exactly.
-    template <int j>
-    static UQ_DEV double group(const int4& q0, const int4& q1, const int4& hh0, const int4& hh1, uint32_t scw,
-                               const int4& xa, const int4& xb, int sa, int sb, double dd, double xsj) {
-        constexpr int GS = j == 1 ? 4 : (j == 2 ? 16 : 1);
-        const int4 w0 = extract<j>(q0, hh0), w1 = extract<j>(q1, hh1);
-        const int d0 = dot16(w0, xa, uq_mul24(sa, -4 * GS));
-        const int d1 = dot16(w1, xb, uq_mul24(sb, -4 * GS));
-        const int b = 16 * (j & 1);
-        const int t = uq_mul24((int)(int8_t)(scw >> b), d0) + uq_mul24((int)(int8_t)(scw >> (b + 8)), d1);
-        return xsj * ((dd * (1.0 / GS)) * (double)t);
-    }
-    static UQ_DEV double dot(const W& wv, const X& x, int u) {
-        const int n = u & 1;
+    static UQ_DEV int lane4(const int4& v, int t) { return t == 0 ? v.x : (t == 1 ? v.y : (t == 2 ? v.z : v.w)); }
+    // The unit's dot: per word t the four sub-block dwords, then the scales.
+    // T0 = s0*D0 + s1*D1 (GS 1) and T1 = s2*D2 + s3*D3 (GS 16) are exact
+    // integers (|D| <= 16 * 4 * 16 * 127, |s| <= 32); d*(s-32) is exact in
+    // f32 (11-bit x 6-bit), so the blocks' sums of (d*s)*D equal d*T, and
+    // d * xs is exact in double.
+    static UQ_DEV double dot_v(const W& wv, const int4* xv, const int4& c, double xs0, double xs1) {
+        int D0 = c.x, D1 = c.y, D2 = c.z, D3 = c.w;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t A = (uint32_t)lane4(wv.a, t);
+            const uint32_t Bw = (uint32_t)(t < 2 ? wv.p.x : wv.p.y);
+            const uint32_t B = (t & 1) ? Bw >> 2 : Bw;
+            const uint32_t As = A >> 1;
+            const int w0 = (int)(A & 0x07070707u), w2 = (int)(A & 0x70707070u);
+            const int w1 = (int)((B & 0x03030303u) | (As & 0x04040404u));
+            const int w3 = (int)((B & 0x30303030u) | (As & 0x40404040u));
+            D0 = uq_dot4(w0, lane4(xv[0], t), D0);
+            D1 = uq_dot4(w1, lane4(xv[1], t), D1);
+            D2 = uq_dot4(w2, lane4(xv[2], t), D2);
+            D3 = uq_dot4(w3, lane4(xv[3], t), D3);
+        }
+        const int s = wv.p.z;
+        const int s0 = (int)(int8_t)s, s1 = (int)(int8_t)(s >> 8), s2 = (int)(int8_t)(s >> 16), s3 = s >> 24;
+        const int T0 = uq_mul24(s0, D0) + uq_mul24(s1, D1);
+        const int T1 = uq_mul24(s2, D2) + uq_mul24(s3, D3);
         const double dd = (double)uq_half(wv.d);
-        const int4 hh0 = n ? shr1(wv.h0) : wv.h0, hh1 = n ? shr1(wv.h1) : wv.h1;
-        double acc = group<0>(wv.q0, wv.q1, hh0, hh1, wv.sc0, x.v[0], x.v[1], x.sx[0], x.sx[1], dd, x.s[0]);
-        acc += group<1>(wv.q0, wv.q1, hh0, hh1, wv.sc0, x.v[2], x.v[3], x.sx[2], x.sx[3], dd, x.s[1]);
-        acc += group<2>(wv.q0, wv.q1, hh0, hh1, wv.sc1, x.v[4], x.v[5], x.sx[4], x.sx[5], dd, x.s[2]);
-        acc += group<3>(wv.q0, wv.q1, hh0, hh1, wv.sc1, x.v[6], x.v[7], x.sx[6], x.sx[7], dd, x.s[3]);
-        return acc;
+        return (dd * xs0) * (double)T0 + (dd * (xs1 * (1.0 / 16))) * (double)T1;
     }
+    static UQ_DEV double dot(const W& wv, const X& x, int = 0) { return dot_v(wv, x.v, x.c, x.s0, x.s1); }
     static UQ_DEV double term(const WArgs& w, int64_t row, int64_t nu, int u, const X& x) {
         return dot(load_w(w, row, nu, u), x, u);
     }
-    // dot against an activation staged in LDS with its 16-value sums; block j's
-    // 32 activations are read just before they are used (a compiler barrier
-    // keeps the four blocks' reads from being hoisted together)
+    // dot against an activation staged in LDS with stage16's starts
     static UQ_DEV double dot_lds(const W& wv, const int8_t* lx, const float* lxs, const int* ls16, int u) {
-        const int n = u & 1;
-        const double dd = (double)uq_half(wv.d);
-        const int4* xv = (const int4*)(lx + (size_t)u * 128);
-        const int4 hh0 = n ? shr1(wv.h0) : wv.h0, hh1 = n ? shr1(wv.h1) : wv.h1;
-        double acc = 0.0;
-#define UQ_Q3K_GROUP(J, SCW)                                                                                    \
-        {                                                                                                        \
-            asm volatile("" ::: "memory");                                                                       \
-            const int4 xa = xv[2 * J], xb = xv[2 * J + 1];                                                       \
-            const int sa = ls16[8 * u + 2 * J], sb = ls16[8 * u + 2 * J + 1];                                    \
-            acc += group<J>(wv.q0, wv.q1, hh0, hh1, SCW, xa, xb, sa, sb, dd, (double)lxs[4 * u + J]);            \
-        }
-        UQ_Q3K_GROUP(0, wv.sc0)
-        UQ_Q3K_GROUP(1, wv.sc0)
-        UQ_Q3K_GROUP(2, wv.sc1)
-        UQ_Q3K_GROUP(3, wv.sc1)
-#undef UQ_Q3K_GROUP
-        return acc;
+        const int4* p = (const int4*)(lx + (size_t)u * 64);
+        const int4 xv[4] = {p[0], p[1], p[2], p[3]};
+        const int4 c = *(const int4*)(ls16 + 4 * u);
+        const float2 xs = *(const float2*)(lxs + 2 * u);
+        return dot_v(wv, xv, c, (double)xs.x, (double)xs.y);
     }
     // ggml Q3_K 6-bit scale k (0..15) of the 12 packed bytes b
-    static UQ_DEV int scale6_k(const uint8_t* b, int k) {
+    static UQ_HD int scale6_k(const uint8_t* b, int k) {
         const int low = k < 8 ? (b[k] & 0xF) : (b[k - 8] >> 4);
         const int high = (b[8 + (k & 3)] >> (2 * (k >> 2))) & 3;
         return low | (high << 4);
+    }
+    // GGUF superblock g (hmask 32, qs 64, scales 12, d 2): low 2 bits and
+    // high bit of value i (0..255)
+    static UQ_HD int gguf_low2(const uint8_t* g, int i) {
+        const int n = i >> 7, j = (i >> 5) & 3, l = i & 31;
+        return (g[32 + 32 * n + l] >> (2 * j)) & 3;
+    }
+    static UQ_HD int gguf_hbit(const uint8_t* g, int i) {
+        const int n = i >> 7, j = (i >> 5) & 3, l = i & 31;
+        return (g[l] >> (4 * n + j)) & 1;
+    }
+    // Unit p's plane words from GGUF superblock g: A[4], P[3]
+    static UQ_HD void pack_unit(const uint8_t* g, int p, uint32_t* A, uint32_t* P) {
+        for (int t = 0; t < 4; t++) {
+            uint32_t a = 0;
+            for (int b = 0; b < 4; b++) {
+                const int i = 64 * p + 4 * t + b;  // + 16c
+                const uint32_t v0 = gguf_low2(g, i) | gguf_hbit(g, i) << 2;
+                const uint32_t v2 = gguf_low2(g, i + 32) | gguf_hbit(g, i + 32) << 2;
+                const uint32_t byte = v0 | (uint32_t)gguf_hbit(g, i + 16) << 3 | v2 << 4 |
+                                      (uint32_t)gguf_hbit(g, i + 48) << 7;
+                a |= byte << (8 * b);
+            }
+            A[t] = a;
+        }
+        for (int h = 0; h < 2; h++) {
+            uint32_t w = 0;
+            for (int b = 0; b < 4; b++) {
+                const int ie = 64 * p + 4 * (2 * h) + b, io = ie + 4;
+                const uint32_t byte = gguf_low2(g, ie + 16) | gguf_low2(g, ie + 48) << 4 |
+                                      gguf_low2(g, io + 16) << 2 | gguf_low2(g, io + 48) << 6;
+                w |= byte << (8 * b);
+            }
+            P[h] = w;
+        }
+        uint32_t s = 0;
+        for (int c = 0; c < 4; c++) s |= (uint32_t)(uint8_t)(int8_t)(scale6_k(g + 96, 4 * p + c) - 32) << (8 * c);
+        P[2] = s;
+    }
+    // low 2 bits and high bit of value 16c + 4t + b of a unit from its plane words
+    static UQ_HD void unit_parts(const uint32_t* A, const uint32_t* P, int c, int t, int b, int& low2, int& hbit) {
+        const uint32_t a = (A[t] >> (8 * b)) & 0xff;
+        const uint32_t bb = ((P[t >> 1] >> (8 * b)) & 0xff) >> (2 * (t & 1));
+        if (c == 0) { low2 = a & 3; hbit = (a >> 2) & 1; }
+        else if (c == 2) { low2 = (a >> 4) & 3; hbit = (a >> 6) & 1; }
+        else if (c == 1) { low2 = bb & 3; hbit = (a >> 3) & 1; }
+        else { low2 = (bb >> 4) & 3; hbit = a >> 7; }
     }
 };
 

@@ -121,9 +121,9 @@ __global__ __launch_bounds__(WG) void k_q4k_verify(const int8_t* __restrict__ q,
     if (miss) atomicAdd(bad, miss);
 }
 // Q3_K: 110-byte GGUF superblock (hmask 32, qs 64, 12 packed scale bytes, d 2)
-// -> four 64-value units (Q3K::pack_unit): q[blk][4][16] (words A), p[blk][4][12]
-// (words B and the four scales - 32), d[blk]. The verify kernel rebuilds the
-// GGUF bytes from the planes (hmask, qs, the 12 scale bytes, d).
+// -> four 64-value units (Q3K::pack_unit): q[blk][4][16] (words A), p[blk][4][16]
+// (words B, the four scales - 32, d). The verify kernel rebuilds the GGUF
+// bytes from the planes (hmask, qs, the 12 scale bytes, d in every unit).
 __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ src, int64_t blocks,
                                                    int8_t* __restrict__ q, int8_t* __restrict__ sc,
                                                    uint16_t* __restrict__ d) {
@@ -131,14 +131,13 @@ __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ s
     if (blk >= blocks) return;
     const uint8_t* g = src + blk * 110;
     uint32_t* qa = (uint32_t*)q + blk * 16;
-    uint32_t* pw = (uint32_t*)sc + blk * 12;
+    uint32_t* pw = (uint32_t*)sc + blk * 16;
     for (int p = 0; p < 4; p++) {
-        uint32_t A[4], P[3];
+        uint32_t A[4], P[4];
         Q3K::pack_unit(g, p, A, P);
         for (int t = 0; t < 4; t++) qa[4 * p + t] = A[t];
-        for (int k = 0; k < 3; k++) pw[3 * p + k] = P[k];
+        for (int k = 0; k < 4; k++) pw[4 * p + k] = P[k];
     }
-    d[blk] = (uint16_t)(g[108] | (g[109] << 8));
 }
 __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const int8_t* __restrict__ sc,
                                                    const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
@@ -147,12 +146,14 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
     if (blk >= blocks) return;
     const uint8_t* g = src + blk * 110;
     const uint32_t* qa = (const uint32_t*)q + blk * 16;
-    const uint32_t* pw = (const uint32_t*)sc + blk * 12;
+    const uint32_t* pw = (const uint32_t*)sc + blk * 16;
     uint8_t hm[32] = {}, qs[64] = {};
     int v[16];
+    unsigned miss = 0;
     for (int p = 0; p < 4; p++) {
         const uint32_t A[4] = {qa[4 * p], qa[4 * p + 1], qa[4 * p + 2], qa[4 * p + 3]};
-        const uint32_t P[3] = {pw[3 * p], pw[3 * p + 1], pw[3 * p + 2]};
+        const uint32_t P[4] = {pw[4 * p], pw[4 * p + 1], pw[4 * p + 2], pw[4 * p + 3]};
+        miss += P[3] != ((uint32_t)g[108] | (uint32_t)g[109] << 8);
         for (int c = 0; c < 4; c++) {
             v[4 * p + c] = (int)(int8_t)(P[2] >> (8 * c)) + 32;
             for (int t = 0; t < 4; t++)
@@ -165,7 +166,6 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
                 }
         }
     }
-    unsigned miss = 0;
     for (int j = 0; j < 32; j++) miss += hm[j] != g[j];
     for (int j = 0; j < 64; j++) miss += qs[j] != g[32 + j];
     for (int k = 0; k < 16; k++) miss += v[k] < 0 || v[k] > 63;
@@ -175,8 +175,6 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
         for (int gr = 0; gr < 4; gr++) b |= ((v[4 * gr + m] >> 4) & 3) << (2 * gr);
         miss += (uint8_t)b != g[104 + m];
     }
-    miss += (uint8_t)(d[blk] & 0xff) != g[108];
-    miss += (uint8_t)(d[blk] >> 8) != g[109];
     if (miss) atomicAdd(bad, miss);
 }
 
@@ -394,9 +392,9 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
         const int64_t un = (row * (K / 256)) * 4 + b / 4;
         const int cc = (int)(b & 3);
         const uint32_t* qa = (const uint32_t*)w.qs + un * 4;
-        const uint32_t* pw = (const uint32_t*)w.sc + un * 3;
+        const uint32_t* pw = (const uint32_t*)w.sc + un * 4;
         const uint32_t A[4] = {qa[0], qa[1], qa[2], qa[3]};
-        const uint32_t P[3] = {pw[0], pw[1], pw[2]};
+        const uint32_t P[4] = {pw[0], pw[1], pw[2], pw[3]};
         const int* xp = (const int*)x;
         for (int t = 0; t < 4; t++) {
             int v = 0;

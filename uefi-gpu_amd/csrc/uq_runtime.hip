@@ -262,12 +262,12 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
         off_d = off_sc + align256(blocks * 16);
         total = off_d + align256(blocks * 4);
     } else {
-        // Q3_K: per superblock four units of 16 + 12 bytes, then d
+        // Q3_K: per superblock four units of 16 + 16 bytes (d inside the second)
         const size_t blocks = (size_t)(n / 256 * m);
         off_q = 0;
         off_sc = align256(blocks * 64);
-        off_d = off_sc + align256(blocks * 48);
-        total = off_d + align256(blocks * 2);
+        off_d = off_sc;
+        total = off_sc + align256(blocks * 64);
     }
     UQ_CHECK_HIP(hipMalloc(&w.alloc, total));
     w.alloc_bytes = total;

@@ -78,6 +78,30 @@ def test_q4k_matvec_qwen_shapes(gpu, N, K):
     assert ulps(y, ref).max() <= 1
 
 
+# the Q3_K sweep (bench leg q3k): Qwen2.5-1.5B projection shapes, lm_head included
+@pytest.mark.parametrize("N,K", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151936, 1536)])
+def test_q3k_matvec_qwen_shapes(gpu, N, K):
+    raw = uq.synth_quant(uq.KIND_Q3_K, 0x5EED0021 + N, N, K)
+    x = uq.synth_normal(0x5EED0031 + K, K)
+    w = uq.Weight(uq.KIND_Q3_K, K, N, raw)
+    y = uq.matvec(w, x)
+    ref = O.matvec(O.Q3_K, raw, K, N, x)
+    assert tol_ok(y, ref)
+    assert ulps(y, ref).max() <= 1
+
+
+# K-quant rows of 1 to 64 superblocks (every lane geometry of the LDS-staged
+# kernel: 4 lanes x 1..3 units up to 64 lanes x 8) with row counts that leave
+# partial row blocks
+@pytest.mark.parametrize("kind", [uq.KIND_Q3_K, uq.KIND_Q4_K])
+@pytest.mark.parametrize("m,n", [(1, 256), (7, 512), (33, 768), (65, 2048), (19, 4096), (3, 16384)])
+def test_kquant_matvec_ragged_shapes(gpu, kind, m, n):
+    raw = uq.synth_quant(kind, 97 * m + n + kind, m, n)
+    x = uq.synth_normal(n + 5, n, 0.0, 3.0)
+    w = uq.Weight(kind, n, m, raw)
+    assert ulps(uq.matvec(w, x), O.matvec(kind, raw, n, m, x)).max() <= 1
+
+
 @pytest.mark.parametrize("N,K", [(768, 2048), (2048, 768)])
 def test_q3k_matvec_moe_shapes(gpu, N, K):
     raw = uq.synth_quant(uq.KIND_Q3_K, 0x5EED0004 + N, N, K)
@@ -97,12 +121,12 @@ def test_q8_matvec_ragged_shapes(gpu, m, n):
     assert ulps(uq.matvec(w, x), O.matvec(O.Q8_0, raw, n, m, x)).max() <= 1
 
 
-# the fused gate/up pair: Q8_0 and Q4_K at the Qwen2.5-1.5B FFN (2 x 8960 x
-# 1536), Q3_K at the MoE expert FFN (2 x 768 x 2048), plus ragged row counts
+# the fused gate/up pair: Q8_0, Q4_K and Q3_K at the Qwen2.5-1.5B FFN (2 x 8960
+# x 1536), Q3_K at the MoE expert FFN (2 x 768 x 2048), plus ragged row counts
 # that leave a partial row block in the last workgroup
 @pytest.mark.parametrize("kind,N,K", [(uq.KIND_Q8_0, 8960, 1536), (uq.KIND_Q4_K, 8960, 1536),
-                                      (uq.KIND_Q3_K, 768, 2048), (uq.KIND_Q4_K, 37, 512),
-                                      (uq.KIND_Q3_K, 45, 768)])
+                                      (uq.KIND_Q3_K, 8960, 1536), (uq.KIND_Q3_K, 768, 2048),
+                                      (uq.KIND_Q4_K, 37, 512), (uq.KIND_Q3_K, 45, 768)])
 def test_gateup_fused_silu(gpu, kind, N, K):
     import ctypes
     rg = uq.synth_quant(kind, 71 + N, N, K)

@@ -214,21 +214,27 @@ struct Q3K {
     // integers (|D| <= 16 * 4 * 16 * 127, |s| <= 32); d*(s-32) is exact in
     // f32 (11-bit x 6-bit), so the blocks' sums of (d*s)*D equal d*T, and
     // d * xs is exact in double.
+    // The four sub-block dwords of word t (values 4t..4t+3 of each
+    // sub-block as int8 lanes, v3 scaled by GS = 1, 1, 16, 16) from A_t and
+    // the B word pair holding t.
+    static UQ_HD void words(uint32_t A, uint32_t Bw, int t, int* w) {
+        const uint32_t B = (t & 1) ? Bw >> 2 : Bw;
+        const uint32_t As = A >> 1;
+        w[0] = (int)(A & 0x07070707u);
+        w[1] = (int)((B & 0x03030303u) | (As & 0x04040404u));
+        w[2] = (int)(A & 0x70707070u);
+        w[3] = (int)((B & 0x30303030u) | (As & 0x40404040u));
+    }
     static UQ_DEV double dot_v(const W& wv, const int4* xv, const int4& c, double xs0, double xs1) {
         int D0 = c.x, D1 = c.y, D2 = c.z, D3 = c.w;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const uint32_t A = (uint32_t)lane4(wv.a, t);
-            const uint32_t Bw = (uint32_t)(t < 2 ? wv.p.x : wv.p.y);
-            const uint32_t B = (t & 1) ? Bw >> 2 : Bw;
-            const uint32_t As = A >> 1;
-            const int w0 = (int)(A & 0x07070707u), w2 = (int)(A & 0x70707070u);
-            const int w1 = (int)((B & 0x03030303u) | (As & 0x04040404u));
-            const int w3 = (int)((B & 0x30303030u) | (As & 0x40404040u));
-            D0 = uq_dot4(w0, lane4(xv[0], t), D0);
-            D1 = uq_dot4(w1, lane4(xv[1], t), D1);
-            D2 = uq_dot4(w2, lane4(xv[2], t), D2);
-            D3 = uq_dot4(w3, lane4(xv[3], t), D3);
+            int w[4];
+            words((uint32_t)lane4(wv.a, t), (uint32_t)(t < 2 ? wv.p.x : wv.p.y), t, w);
+            D0 = uq_dot4(w[0], lane4(xv[0], t), D0);
+            D1 = uq_dot4(w[1], lane4(xv[1], t), D1);
+            D2 = uq_dot4(w[2], lane4(xv[2], t), D2);
+            D3 = uq_dot4(w[3], lane4(xv[3], t), D3);
         }
         const int s = wv.p.z;
         const int s0 = (int)(int8_t)s, s1 = (int)(int8_t)(s >> 8), s2 = (int)(int8_t)(s >> 16), s3 = s >> 24;

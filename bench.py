@@ -43,14 +43,42 @@ def q8_bytes(N, K):
     return N * (K // 32) * 34 + K + (K // 32) * 4 + 4 * N
 
 
+# AMD x86 family numbers of the server cores (AMD's published family/model
+# assignments): 0x17 Zen/Zen 2, 0x19 Zen 3/Zen 4, 0x1A Zen 5
+AMD_FAMILIES = {0x17: {(0x00, 0x2F): "Zen / Zen+ (EPYC 7001)", (0x30, 0x3F): "Zen 2 (EPYC 7002, Rome)"},
+                0x19: {(0x00, 0x0F): "Zen 3 (EPYC 7003, Milan)", (0x10, 0x1F): "Zen 4 (EPYC 9004, Genoa)",
+                       (0xA0, 0xAF): "Zen 4c (EPYC 9004, Bergamo)"},
+                0x1A: {(0x00, 0x1F): "Zen 5 (EPYC 9005, Turin)"}}
+
+
 def cpu_model():
+    """The first core's model string from /proc/cpuinfo with its x86 family,
+    model and stepping (a VM may report only a generic name such as "AMD
+    EPYC"; family/model still identify the core), the L3-visible cache size
+    and the clock the kernel reports."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break
+            k, _, v = line.partition(":")
+            fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return platform.processor()
+        return platform.processor()
+    name = fields.get("model name", platform.processor())
+    try:
+        fam, mod, step = int(fields["cpu family"]), int(fields["model"]), int(fields["stepping"])
+    except (KeyError, ValueError):
+        return name
+    out = "%s (family 0x%X model 0x%X stepping %d" % (name, fam, mod, step)
+    for (lo, hi), arch in AMD_FAMILIES.get(fam, {}).items():
+        if "AMD" in fields.get("vendor_id", "") + name and lo <= mod <= hi:
+            out += ": " + arch
+    if "cache size" in fields:
+        out += ", cache %s" % fields["cache size"]
+    if "cpu MHz" in fields:
+        out += ", %s MHz" % fields["cpu MHz"].split(".")[0]
+    return out + ")"
 
 
 def _oracle():
@@ -203,7 +231,8 @@ def mfma_probe():
     SIMD with and without the VALU work the prefill kernels put beside their
     MFMAs (kinds 3-6): fp64 MFMAs with an fp16 -> double operand conversion each,
     int8 MFMAs beside the per-block f32 rescale."""
-    r = {"int8_TOPS": round(uq.probe_mfma(0), 1), "fp16_TFLOPS": round(uq.probe_mfma(1), 1),
+    r = {"int8_TOPS": round(uq.probe_mfma(0), 1), "int8_32x32x32_TOPS": round(uq.probe_mfma(9), 1),
+         "int8_16x16x64_TOPS": round(uq.probe_mfma(10), 1), "fp16_TFLOPS": round(uq.probe_mfma(1), 1),
          "fp64_TFLOPS": round(uq.probe_mfma(2), 1)}
     one = {k: uq.probe_mfma(kind) for k, kind in (("fp64", 3), ("fp64_and_conv", 4), ("conv_only", 5),
                                                   ("int8", 6), ("int8_and_rescale", 7), ("rescale_only", 8))}
@@ -213,7 +242,8 @@ def mfma_probe():
     r["one_wave_per_simd"] = {k: round(v, 1) for k, v in one.items()}
     r["one_wave_per_simd"]["fp64_overlap"] = overlap(one["fp64"], one["fp64_and_conv"], one["conv_only"])
     r["one_wave_per_simd"]["int8_overlap"] = overlap(one["int8"], one["int8_and_rescale"], one["rescale_only"])
-    r["note"] = ("independent chains of v_mfma_i32_16x16x32_i8 / v_mfma_f32_16x16x32_f16 / v_mfma_f64_16x16x4_f64 "
+    r["note"] = ("independent chains of v_mfma_i32_16x16x32_i8 (int8_TOPS) / v_mfma_i32_32x32x32_i8 / "
+                 "v_mfma_i32_16x16x64_i8 / v_mfma_f32_16x16x32_f16 / v_mfma_f64_16x16x4_f64 "
                  "on register operands, 16 waves per CU, same box; one_wave_per_simd: 16 MFMAs per iteration on "
                  "4 chains and/or the VALU work beside them (fp64: 16 fp16->double operand conversions; int8: "
                  "convert, scale product, fma of 16 f32 accumulators), rates of the same MFMA count; overlap: "
@@ -456,8 +486,8 @@ def main():
         result["decode"] = decode_bench(keep=decode_state)
         result["prefill_gemm"] = prefill_gemm_bench()
         pg = result["prefill_gemm"]
-        pg["measured_16x16x32_peak_TOPS"] = result["mfma_probe"]["int8_TOPS"]
-        pg["frac_of_measured_peak"] = round(pg["aggregate_TOPS"] / result["mfma_probe"]["int8_TOPS"], 4)
+        pg["frac_of_int8_peak"] = round(pg["aggregate_TOPS"] / pg["int8_mfma_peak_TOPS"], 4)
+        pg["measured_32x32x32_TOPS"] = result["mfma_probe"]["int8_32x32x32_TOPS"]
         result["prefill_attention"] = prefill_attention_bench()
         result["q4k_sweep"] = q4k_sweep()
         result["q3k_sweep"] = q3k_sweep()

@@ -227,7 +227,9 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
  * double B-operand conversion per MFMA, 5: those conversions alone; 6: int8
  * MFMAs alone, 7: beside a convert / scale product / fma per f32 accumulator
  * (the prefill GEMM's rescale), 8: that rescale alone. Whether a kind's VALU
- * work overlaps the matrix core: 1/rate(4) vs 1/rate(3) + 1/rate(5). */
+ * work overlaps the matrix core: 1/rate(4) vs 1/rate(3) + 1/rate(5).
+ * 16 waves per CU again: 9: v_mfma_i32_32x32x32_i8, 10: v_mfma_i32_16x16x64_i8
+ * (tera int8 ops/s). */
 int uq_probe_mfma(int kind, double* tera_ops);
 
 /* ---------------------------------------------------------------- Qwen2 dense decoder */

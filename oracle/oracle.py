@@ -429,7 +429,7 @@ class MoeLayer:
                      gate=ctypes.cast(self.g, ctypes.POINTER(_u8p)), up=ctypes.cast(self.u, ctypes.POINTER(_u8p)),
                      down=ctypes.cast(self.d, ctypes.POINTER(_u8p)), shared_kind=shared_kind,
                      sh_gate=p(sh_gate, _u8p), sh_up=p(sh_up, _u8p), sh_down=p(sh_down, _u8p),
-                     sh_scale=p(sh_scale, _f32p))
+                     sh_scale=None if sh_scale is None else p(sh_scale, _f32p))
 
     def ffn(self, x, router_logits):
         out = np.empty(self.m.dim, np.float32)

@@ -832,7 +832,8 @@ static float act_sigmoid(float x) { float e = uqo_expf(-x); float d = 1.0f + e; 
 /* frontier_forward.rs:164-199 with int8 activations per 32 for every expert
  * matvec: per selected expert down(silu(gate x) * (up x)); shared expert the
  * same; out = sum over rank order of weight*value (frontier_cpu_axpy.rs:13-21,
- * separate multiply then add), then += sigmoid(shexp_gate . x) * shared. */
+ * separate multiply then add), then += sigmoid(shexp_gate . x) * shared
+ * (weight 1 when sh_scale is NULL: no ffn_gate_inp_shexp tensor). */
 int uqo_moe_ffn(const uqo_moe* mo, const float* x, const float* router_logits, float* out,
                 int32_t* ids_out, float* weights_out) {
     const int D = mo->dim, F = mo->ff, K = mo->top_k;
@@ -860,10 +861,12 @@ int uqo_moe_ffn(const uqo_moe* mo, const float* x, const float* router_logits, f
         uqo_matvec(kind, wd, F, D, fs, fq, val);
         if (!all_finite(val, D)) { rc = -3; break; }
         float weight;
-        if (shared) {
+        if (shared && mo->sh_scale) {
             double acc = 0.0;
             for (int i = 0; i < D; i++) acc += (double)mo->sh_scale[i] * (double)x[i];
             weight = act_sigmoid((float)acc);
+        } else if (shared) {
+            weight = 1.0f;              /* a model without ffn_gate_inp_shexp: the shared expert unscaled */
         } else {
             weight = wts[k];
         }

@@ -116,7 +116,7 @@ typedef struct {
     const uint8_t* const* down;    /* [experts] dim x ff   */
     uint32_t shared_kind;          /* UQO_Q8_0 */
     const uint8_t *sh_gate, *sh_up, *sh_down;
-    const float   *sh_scale;       /* dim, f32: ffn_gate_inp_shexp */
+    const float   *sh_scale;       /* dim, f32: ffn_gate_inp_shexp (NULL: weight 1) */
 } uqo_moe;
 
 int uqo_moe_route(const float* logits, int experts, int top_k, int32_t* ids, float* weights);

@@ -2,15 +2,18 @@
 (oracle/uq_oracle.c uqo_refo_*, the f32 operation orders of the reference's
 decode-graph kernels) on the 28-layer Qwen2.5-1.5B-architecture synthetic
 model of qwen25_decode.json (seed 0x5EED0002), teacher-forced: the 512-token
-prompt token by token, then 8 steps fed [first_id] + ids[:7] of that fixture.
+prompt token by token, then all 128 decode steps of that fixture, fed
+[first_id] + ids[:127] (the build's own greedy ids, so the forced run is the
+free-running greedy run of the exact contract).
 
-Saved for the 9 positions 511..519 (the prompt's last token, then the forced
+Saved for the 129 positions 511..639 (the prompt's last token, then the forced
 steps), once with an f32 KV cache (the reference's) and once with the cache
 rounded to fp16 (this build's format):
   idx        the compared vocabulary ids per position: the 64 largest logits
-             of the f32-cache run, then 1024 fixed seeded ids
+             of the f32-cache run, then 448 fixed seeded ids
   ref_f32, ref_f16   those logits
   absmax_*, argmax_*, margin_*  max |logit|, argmax and top-2 margin per run
+  argmax_exact, margin_exact    the same of the exact-double oracle
   exact_dev  max |exact-oracle logit - reference-order logit| / max |logit|
              over the compared ids (fp16 cache), for the record
 
@@ -38,9 +41,9 @@ def main():
     t = uq.synth_qwen2(cfg, seed)
     arrays = {k: v[3] for k, v in t.items()}
     prompt = uq.synth_tokens(seed, n, cfg["vocab"])
-    forced = [g["first_id"]] + g["ids"][:7]
+    forced = [g["first_id"]] + g["ids"][:127]
     rng = np.random.default_rng(0x5EED0077)
-    sample = np.sort(rng.choice(cfg["vocab"], 1024, replace=False))
+    sample = np.sort(rng.choice(cfg["vocab"], 448, replace=False))
     runs = {}
     for name, kv16 in (("f32", False), ("f16", True)):
         t0 = time.time()
@@ -74,9 +77,20 @@ def main():
         out["margin_" + name] = (s[:, -1] - s[:, -2]).astype(np.float32)
     dev = np.abs(np.take_along_axis(exact, idx, 1) - out["ref_f16"]).max(1) / out["absmax_f16"]
     out["exact_dev"] = dev.astype(np.float32)
+    out["argmax_exact"] = exact.argmax(1).astype(np.int32)
+    s = np.sort(exact, 1)
+    out["margin_exact"] = (s[:, -1] - s[:, -2]).astype(np.float32)
     out["forced"] = np.array(forced, np.int32)
     np.savez_compressed(os.path.join(HERE, "qwen25_refo.npz"), **out)
     print("exact vs reference-order (fp16 cache) max dev per position:", np.round(dev, 4))
+    for k in ("f32", "f16"):
+        agree = out["argmax_exact"] == out["argmax_" + k]
+        rel = out["margin_" + k] / out["absmax_" + k]
+        print("ids equal to the %s-cache reference order: %d of %d; smallest top-2 margin/max|logit| %.2e, "
+              "largest where they differ %.2e" % (k, agree.sum(), agree.size, rel.min(),
+                                                  rel[~agree].max() if (~agree).any() else 0.0))
+    agree = out["argmax_f32"] == out["argmax_f16"]
+    print("f32-cache vs fp16-cache reference order: ids equal at %d of %d" % (agree.sum(), agree.size))
 
 
 if __name__ == "__main__":

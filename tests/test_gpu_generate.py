@@ -1,13 +1,15 @@
 """uq_generate (generate_one, driver/src/llm.rs:402-428) on the GPU: the same
-ids as prefill followed by device-fed decode steps, the stop-id and limit
-rules of the reference loop, and the eval runner over the reference's prompt
-files with a synthetic vocabulary."""
+ids as the oracle's prefill followed by its greedy decode chain, the same ids
+as the library's own prefill followed by device-fed decode steps, the stop-id
+and limit rules of the reference loop, and the eval runner over the
+reference's prompt files with a synthetic vocabulary."""
 import os
 
 import numpy as np
 import pytest
 
 import gguf_writer as W
+import oracle as O
 import uq
 import evalrun
 
@@ -19,10 +21,29 @@ CFG = dict(uq.QWEN25_15B, layers=2, max_seq=256)
 
 
 @pytest.fixture(scope="module")
-def model(gpu):
-    m = uq.Qwen2Model(CFG, uq.synth_qwen2(CFG, 0x6E0))
+def tensors():
+    return uq.synth_qwen2(CFG, 0x6E0)
+
+
+@pytest.fixture(scope="module")
+def model(gpu, tensors):
+    m = uq.Qwen2Model(CFG, tensors)
     yield m
     m.free()
+
+
+def oracle_chain(tensors, prompt, n):
+    """generate_one's loop (llm.rs:402-428) on the oracle decoder: prefill the
+    prompt, then feed each greedy id back as the next token."""
+    o = O.Model(CFG, {k: v[3] for k, v in tensors.items()})
+    rc, tok, _ = o.prefill(prompt)
+    assert rc == 0
+    ids = [tok]
+    for pos in range(len(prompt), len(prompt) + n - 1):
+        rc, tok, _ = o.decode(tok, pos)
+        assert rc == 0
+        ids.append(tok)
+    return np.array(ids, np.uint32)
 
 
 def reference_chain(model, prompt, n):
@@ -34,10 +55,11 @@ def reference_chain(model, prompt, n):
     return np.concatenate([[first], rest]).astype(np.uint32)
 
 
-def test_generate_matches_prefill_and_decode(model):
+def test_generate_matches_oracle_and_prefill_decode(model, tensors):
     prompt = evalrun.read_tokens(os.path.join(PROMPTS, "prompt_sentence.tokens"))
     ids, ended, pms, dms = model.generate(prompt, 40, stop=())
     assert len(ids) == 40 and not ended and pms > 0 and dms > 0
+    assert np.array_equal(ids, oracle_chain(tensors, prompt, 40))
     assert np.array_equal(ids, reference_chain(model, prompt, 40))
 
 

@@ -1,12 +1,24 @@
 """A Qwen2 model loaded from a GGUF file (uq_gguf_open + uq_model_load_gguf)
-decodes exactly like the same tensors set one by one (uq_model_set_tensor):
-same logits bits, same greedy ids. A file without output.weight (tied
-embeddings) uses token_embd.weight as the output matrix."""
+decodes like the oracle decoder over the same tensors (logits within 1 ulp,
+identical greedy ids) and exactly like the same tensors set one by one
+(uq_model_set_tensor): same logits bits, same ids. A file without
+output.weight (tied embeddings) uses token_embd.weight as the output matrix.
+A MoE layer read from a split model (uq_moe_load_gguf) matches the oracle's
+Forward::ffn over the same expert bytes."""
 import numpy as np
 import pytest
 
+import oracle as O
 import uq
 import gguf_writer as W
+
+
+def ulps(a, b):
+    a = a.view(np.int32).astype(np.int64)
+    b = b.view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+    b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    return np.abs(a - b)
 
 CFG = dict(layers=2, dim=256, hidden=512, heads=4, kv_heads=2, head_dim=64, vocab=1024, max_seq=128,
            eps=1e-6, theta=1e6)
@@ -38,6 +50,17 @@ def test_gguf_model_matches_direct_tensors(gpu, tmp_path, tie):
     got = uq.Qwen2Model.from_gguf(str(p), CFG["max_seq"])
     f0, l0, i0 = run(ref)
     f1, l1, i1 = run(got)
+    # the oracle decoder over the tensors the file holds (frontier_gguf.rs:86-137 reads them back by name)
+    ora = O.Model(CFG, {k: v[3] for k, v in tensors.items()})
+    rc, of, ol = ora.decode(7, 0, want_logits=True)
+    assert rc == 0 and of == f1
+    assert ulps(l1, ol).max() <= 1
+    tok, oids = of, []
+    for pos in range(1, 1 + len(i1)):
+        rc, tok, _ = ora.decode(tok, pos)
+        assert rc == 0
+        oids.append(tok)
+    assert list(i1) == oids
     assert f0 == f1
     assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
     assert np.array_equal(i0, i1)
@@ -94,21 +117,30 @@ def moe_shards(cfg, seed, tmp_path, gate_inp=True):
 @pytest.mark.gpu
 @pytest.mark.parametrize("kind,gate_inp", [(uq.KIND_Q3_K, True), (uq.KIND_Q4_K, False)])
 def test_moe_bank_from_split_gguf(gpu, tmp_path, kind, gate_inp):
-    """uq_moe_load_gguf over a ModelIndex gives the same layer as
-    uq_moe_set_expert / uq_moe_set_shared of the same bytes: identical ids and
-    weights, bit-identical outputs."""
+    """uq_moe_load_gguf over a ModelIndex matches the oracle's Forward::ffn
+    (frontier_forward.rs:164-199) over the same expert bytes: identical ids,
+    bit-identical weights, outputs within 1 ulp; and it gives the same layer
+    as uq_moe_set_expert / uq_moe_set_shared of those bytes, bit for bit."""
     cfg = dict(uq.MOE_CONFIG, dim=512, ff=256, experts=16, top_k=4, expert_kind=kind)
     (ex, sh, gi), paths = moe_shards(cfg, 0x5EED00C1 + kind, tmp_path, gate_inp)
     shards = [uq.Gguf.open(p) for p in reversed(paths)]
     ix = uq.GgufIndex(shards)
     a = uq.MoeLayer(cfg, ex, sh, gi)
     b = uq.MoeLayer.from_gguf(cfg, ix, 0)
+    o = O.MoeLayer(cfg["dim"], cfg["ff"], cfg["experts"], cfg["top_k"], cfg["expert_kind"],
+                   [e[0] for e in ex], [e[1] for e in ex], [e[2] for e in ex], cfg["shared_kind"],
+                   sh[0], sh[1], sh[2], gi)
     try:
         for step in range(6):
             x = uq.synth_normal(0x5EED00C2 + 100 * step, cfg["dim"])
             lg = uq.synth_normal(0x5EED00C3 + 100 * step, cfg["experts"])
             oa, ia, wa = a.ffn(x, lg)
             ob, ib, wb = b.ffn(x, lg)
+            rc, oo, io, wo = o.ffn(x, lg)
+            assert rc == 0
+            assert list(ib) == list(io), step
+            assert np.array_equal(wb.view(np.uint32), wo.view(np.uint32))
+            assert ulps(ob, oo).max() <= 1, step
             assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
             assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32))
     finally:
@@ -137,8 +169,10 @@ def test_moe_load_rejects_wrong_shapes(gpu, tmp_path):
 @pytest.mark.gpu
 def test_load_weight_whole_and_expert_slices(gpu, tmp_path):
     """uq_gguf_load_weight: a rank-2 tensor whole and the rows of single
-    experts of a rank-3 frontier-kind tensor, each equal (bit for bit, through
-    uq_linear) to uploading those bytes directly."""
+    experts of a rank-3 frontier-kind tensor, each within 1 ulp of the oracle's
+    exactly summed fp32-activation linear over the expert's rows
+    (frontier_backend.rs:98-128 picks an expert's rows by offset), and equal
+    (bit for bit, through uq_linear) to uploading those bytes directly."""
     n, rows, E = 512, 24, 3
     iq = uq.synth_quant(uq.KIND_IQ4_NL, 0x5EED00C5, rows * E, n)
     q8 = uq.synth_quant(uq.KIND_Q8_0, 0x5EED00C6, 40, n)
@@ -153,11 +187,15 @@ def test_load_weight_whole_and_expert_slices(gpu, tmp_path):
     for e in range(E):
         a = g.load_weight(ie, e)
         b = uq.Weight(uq.KIND_IQ4_NL, n, rows, iq[e * rows * rb:(e + 1) * rows * rb])
-        assert np.array_equal(uq.linear(a, x).view(np.uint32), uq.linear(b, x).view(np.uint32))
+        ya = uq.linear(a, x)
+        assert ulps(ya, O.linear(uq.KIND_IQ4_NL, iq[e * rows * rb:(e + 1) * rows * rb], n, rows, x)).max() <= 1
+        assert np.array_equal(ya.view(np.uint32), uq.linear(b, x).view(np.uint32))
         a.free()
         b.free()
     a, b = g.load_weight(iw), uq.Weight(uq.KIND_Q8_0, n, 40, q8)
-    assert np.array_equal(uq.linear(a, x).view(np.uint32), uq.linear(b, x).view(np.uint32))
+    ya = uq.linear(a, x)
+    assert ulps(ya, O.linear(uq.KIND_Q8_0, q8, n, 40, x)).max() <= 1
+    assert np.array_equal(ya.view(np.uint32), uq.linear(b, x).view(np.uint32))
     with pytest.raises(uq.UqError):
         g.load_weight(ie)                              # rank 3 needs an expert id
     with pytest.raises(uq.UqError):

@@ -3,6 +3,7 @@ head mapping, SwiGLU, output head) against an independent numpy float64
 restatement of driver/src/llm.rs:339-388 that only shares the int8 activation
 quantization rule, and checks prefill/decode consistency inside the oracle."""
 import numpy as np
+import pytest
 
 import oracle as O
 import uq
@@ -110,12 +111,16 @@ def test_oracle_prefill_matches_decode_chain():
     assert c.prefill(toks, want_logits=True)[1] == nxt_p
 
 
-def test_oracle_moe_matches_numpy_restatement():
+@pytest.mark.parametrize("gated", [True, False])
+def test_oracle_moe_matches_numpy_restatement(gated):
     """frontier_forward.rs:164-199 restated in numpy float64 around the shared
     int8 activation rule: softmax, stable top-k, p/sum weights, SwiGLU experts,
-    rank-ordered combine, sigmoid-gated shared expert."""
+    rank-ordered combine, sigmoid-gated shared expert (weight 1 for a layer
+    without ffn_gate_inp_shexp)."""
     cfg = dict(dim=256, ff=256, experts=8, top_k=2, expert_kind=uq.KIND_Q8_0, shared_kind=uq.KIND_Q8_0)
     ex, sh, gi = uq.synth_moe(cfg, 3)
+    if not gated:
+        gi = None
     om = O.MoeLayer(cfg["dim"], cfg["ff"], cfg["experts"], cfg["top_k"], cfg["expert_kind"],
                     [e[0] for e in ex], [e[1] for e in ex], [e[2] for e in ex], cfg["shared_kind"],
                     sh[0], sh[1], sh[2], gi)
@@ -140,7 +145,8 @@ def test_oracle_moe_matches_numpy_restatement():
             return deq(d, D, F) @ np_quant(mid)
         for r, e in enumerate(order):
             ref += wts[r] * expert(*ex[e])
-        ref += 1 / (1 + np.exp(-(gi.astype(np.float64) @ x.astype(np.float64)))) * expert(*sh)
+        sw = 1.0 if gi is None else 1 / (1 + np.exp(-(gi.astype(np.float64) @ x.astype(np.float64))))
+        ref += sw * expert(*sh)
         assert np.abs(out - ref).max() < 2e-3 * np.abs(ref).max()
 
 

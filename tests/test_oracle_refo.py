@@ -99,6 +99,47 @@ def test_attention_sequential_pv_known_answer():
     assert out[5] == ((third * F(1)) + (third * F(2))) + (third * F(3))
 
 
+def prefill_fmaf_case(blocks=4):
+    """One Q8_0 row and one token whose per-block terms c_b * s_b are 2^24,
+    3 * f32(1/3) = 1 + 2^-25, 1 (and 0 for a fourth block): the row's result
+    separates the summation orders of a prefill GEMM row."""
+    entries = {0: (0x3C00, {0: 1}), 1: (0x3C00, {0: 3}), 2: (0x3C00, {0: 1})}
+    row = q8_row(blocks, entries)
+    qx = np.zeros(32 * blocks, np.int8)
+    qx[[0, 32, 64]] = 1
+    xs = np.ones(blocks, F)
+    xs[0] = F(2 ** 24)
+    xs[1] = np.uint32(0x3EAAAAAB).view(F)
+    return row, xs, qx
+
+
+@pytest.mark.parametrize("blocks", [3, 4])
+def test_prefill_gemm_sequential_fmaf_known_answer(blocks):
+    # prefill_gemm (gpu_prefill.cu:10-36): f = fmaf((float)c_b, dw_b * dx_b, f)
+    # for b = 0, 1, ... in order (lines 29-30). Terms 2^24, 1 + 2^-25, 1:
+    #   fmaf chain:   2^24 -> rn(2^24 + 1 + 2^-25) = 2^24 + 2
+    #                      -> rn(2^24 + 3) = 2^24 + 4 (tie to even)  = 16777220
+    #   mul then add: rn(1 + 2^-25) = 1, 2^24 + 1 -> 2^24 twice     = 16777216
+    #   fmaf, reversed block order: 1 -> rn(2 + 2^-25) = 2 -> 2^24 + 2 = 16777218
+    #   exact sum 2^24 + 2 + 2^-25                                  -> 16777218
+    row, xs, qx = prefill_fmaf_case(blocks)
+    y = O.prefill_gemm(row, 32 * blocks, 1, xs[None], qx[None], 1)
+    assert y[0, 0] == F(16777220.0)
+    c = np.array([1, 3, 1, 0][:blocks], np.float64)
+    terms = c * xs.astype(np.float64)                 # c_b * s_b, exact in double
+    seq = F(0)
+    mul_add = F(0)
+    rev = F(0)
+    for b in range(blocks):
+        seq = F(np.float64(seq) + terms[b])           # one rounding of an exact double: fmaf
+        mul_add = F(mul_add + F(terms[b]))
+        rev = F(np.float64(rev) + terms[blocks - 1 - b])
+    assert (seq, mul_add, rev) == (F(16777220.0), F(16777216.0), F(16777218.0))
+    assert F(terms.sum()) == F(16777218.0)
+    # the decode contract (exact double sum, rounded once) gives the exact form
+    assert O.matvec_q(O.Q8_0, row, 32 * blocks, 1, xs, qx)[0] == F(16777218.0)
+
+
 def test_attention_matches_float64():
     rng = np.random.default_rng(7)
     hd, kvd, pos = 128, 256, 300

@@ -1,7 +1,8 @@
 // Probes used by the benchmark: a plain streaming read and a plain copy of a
 // known number of bytes (the achievable HBM rate on the box and the
 // calibration of the FETCH_SIZE / WRITE_SIZE counters), and matrix-core
-// throughput loops (the achievable int8 / fp16 / fp64 MFMA rates).
+// throughput loops (the achievable int8 / fp16 / fp64 MFMA rates, int8 in
+// its 16x16x32, 32x32x32 and 16x16x64 forms).
 #include "uq_internal.h"
 #include "../../include/uq.h"
 
@@ -46,6 +47,38 @@ __global__ __launch_bounds__(256) void k_probe_mfma_i8(int iters, int* __restric
     for (int i = 0; i < iters; i++)
 #pragma unroll
         for (int k = 0; k < PC; k++) c[k] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c[k], 0, 0, 0);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+    if (s == 0x7fffffff) sink[blockIdx.x] = s;
+}
+// gfx950's K = 32 int8 form on 32 x 32 tiles (v_mfma_i32_32x32x32_i8, one
+// 32-value block per instruction) and the K = 64 form on 16 x 16 tiles
+// (v_mfma_i32_16x16x64_i8, two blocks): 16-byte operands per lane.
+typedef int pv16i __attribute__((ext_vector_type(16)));
+__global__ __launch_bounds__(256) void k_probe_mfma_i8_32x32(int iters, int* __restrict__ sink) {
+    const pv4i a = {(int)(threadIdx.x & 7), 1, 2, 3}, b = {3, 2, 1, (int)((threadIdx.x >> 3) & 7)};
+    pv16i c[PC / 2];
+#pragma unroll
+    for (int k = 0; k < PC / 2; k++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) c[k][r] = 0;
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int k = 0; k < PC / 2; k++) c[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[k], 0, 0, 0);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < PC / 2; k++) s += c[k][0] + c[k][5] + c[k][10] + c[k][15];
+    if (s == 0x7fffffff) sink[blockIdx.x] = s;
+}
+__global__ __launch_bounds__(256) void k_probe_mfma_i8_16x16x64(int iters, int* __restrict__ sink) {
+    const pv4i a = {(int)(threadIdx.x & 7), 1, 2, 3}, b = {3, 2, 1, (int)((threadIdx.x >> 3) & 7)};
+    pv4i c[PC];
+#pragma unroll
+    for (int k = 0; k < PC; k++) c[k] = pv4i{0, 0, 0, 0};
+    for (int i = 0; i < iters; i++)
+#pragma unroll
+        for (int k = 0; k < PC; k++) c[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[k], 0, 0, 0);
     int s = 0;
 #pragma unroll
     for (int k = 0; k < PC; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
@@ -209,15 +242,17 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
 
 int uq_probe_mfma(int kind, double* tera_ops) {
     if (!uq_stream()) return set_error(ERR_ARG, "uq_init has not been called");
-    if (kind < 0 || kind > 8 || !tera_ops) return set_error(ERR_ARG, "probe_mfma: kind 0..8");
+    if (kind < 0 || kind > 10 || !tera_ops) return set_error(ERR_ARG, "probe_mfma: kind 0..10");
     hipStream_t s = (hipStream_t)uq_stream();
-    const bool f64 = kind >= 2 && kind <= 5, one_wave = kind >= 3;
-    // ops per wave instruction: 2*16*16*32 (int8, fp16), 2*16*16*4 (fp64)
-    const double ops = f64 ? 2.0 * 16 * 16 * 4 : 2.0 * 16 * 16 * 32;
-    const int iters = kind == 2 ? 256 : kind >= 3 && kind <= 5 ? 512 : 2048;
+    const bool f64 = kind >= 2 && kind <= 5, one_wave = kind >= 3 && kind <= 8;
+    // ops per wave instruction: 2*16*16*32 (int8, fp16), 2*16*16*4 (fp64),
+    // 2*32*32*32 and 2*16*16*64 (the K = 32 and K = 64 int8 forms)
+    const double ops = f64 ? 2.0 * 16 * 16 * 4 : kind == 9 ? 2.0 * 32 * 32 * 32 : kind == 10 ? 2.0 * 16 * 16 * 64
+                                                                                              : 2.0 * 16 * 16 * 32;
+    const int iters = kind == 2 ? 256 : kind >= 3 && kind <= 5 ? 512 : kind >= 9 ? 1024 : 2048;
     // 16 waves per CU, or one wave per SIMD (16 MFMAs per iteration, not PC)
     const unsigned grid = (one_wave ? 1u : 4u) * (unsigned)cu_count();
-    const int per_iter = one_wave ? 16 : PC;
+    const int per_iter = one_wave ? 16 : kind == 9 ? PC / 2 : PC;
     int* sink = nullptr;
     UQ_CHECK_HIP(hipMalloc(&sink, 4 * (size_t)grid));
     auto launch = [&]() {
@@ -230,7 +265,9 @@ int uq_probe_mfma(int kind, double* tera_ops) {
         case 5: hipLaunchKernelGGL((k_probe_f64_1w<false, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
         case 6: hipLaunchKernelGGL((k_probe_i8_1w<true, false>), dim3(grid), dim3(256), 0, s, iters, sink); break;
         case 7: hipLaunchKernelGGL((k_probe_i8_1w<true, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
-        default: hipLaunchKernelGGL((k_probe_i8_1w<false, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 8: hipLaunchKernelGGL((k_probe_i8_1w<false, true>), dim3(grid), dim3(256), 0, s, iters, sink); break;
+        case 9: hipLaunchKernelGGL(k_probe_mfma_i8_32x32, dim3(grid), dim3(256), 0, s, iters, sink); break;
+        default: hipLaunchKernelGGL(k_probe_mfma_i8_16x16x64, dim3(grid), dim3(256), 0, s, iters, sink); break;
         }
     };
     hipEvent_t e0, e1;

@@ -367,7 +367,8 @@ def probe_mfma(kind):
     """Achievable matrix-core rate: kind 0 int8 (TOPS), 1 fp16, 2 fp64 (TFLOP/s); one
     wave per SIMD: 3 fp64 MFMAs, 4 with an fp16 operand conversion per MFMA, 5 the
     conversions alone; 6 int8 MFMAs, 7 beside the per-block f32 rescale, 8 the
-    rescale alone (rates of the same MFMA count)."""
+    rescale alone (rates of the same MFMA count); 16 waves per CU: 9 the int8
+    32x32x32 form, 10 the int8 16x16x64 form (TOPS)."""
     t = ctypes.c_double()
     _check(lib().uq_probe_mfma(kind, ctypes.byref(t)))
     return t.value

@@ -10,7 +10,7 @@ Saved for the 129 positions 511..639 (the prompt's last token, then the forced
 steps), once with an f32 KV cache (the reference's) and once with the cache
 rounded to fp16 (this build's format):
   idx        the compared vocabulary ids per position: the 64 largest logits
-             of the f32-cache run, then 448 fixed seeded ids
+             of the f32-cache run, then 192 fixed seeded ids
   ref_f32, ref_f16   those logits
   absmax_*, argmax_*, margin_*  max |logit|, argmax and top-2 margin per run
   argmax_exact, margin_exact    the same of the exact-double oracle
@@ -43,7 +43,7 @@ def main():
     prompt = uq.synth_tokens(seed, n, cfg["vocab"])
     forced = [g["first_id"]] + g["ids"][:127]
     rng = np.random.default_rng(0x5EED0077)
-    sample = np.sort(rng.choice(cfg["vocab"], 448, replace=False))
+    sample = np.sort(rng.choice(cfg["vocab"], 192, replace=False))
     runs = {}
     for name, kv16 in (("f32", False), ("f16", True)):
         t0 = time.time()

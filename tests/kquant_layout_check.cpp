@@ -1,13 +1,17 @@
-// Host build of the Q3_K unit code of the device header (Q3K::pack_unit,
-// Q3K::unit_parts, Q3K::words: the same source the repack, verify and matvec
-// kernels compile) checked against the oracle on seeded GGUF rows:
+// Host build of the K-quant layout code of the device header (Q3K::pack_unit,
+// Q3K::unit_parts, Q3K::words, Q3KSB::pack/unpack, sb_geom/sb_piece: the same source the repack, verify and matvec kernels
+// compile) checked against the oracle on seeded GGUF rows:
 //  * unit_parts(pack_unit(g)) returns every value's low 2 bits and high bit;
 //  * the per-16 integer dots formed from words() (the matvec's assembly, each
 //    sub-block's dot started from -4 * GS * sum(x)) equal GS times the
 //    oracle's uqo_q3k_block_dots;
 //  * the row sum d*xs0*(s0*D0 + s1*D1) + d*(xs1/16)*(s2*D2 + s3*D3) over the
 //    units, with the scales and d read from the packed words, rounds to the
-//    oracle's uqo_matvec_x output within 1 ulp.
+//    oracle's uqo_matvec_x output within 1 ulp;
+//  * every unit word above is taken after a round trip through the row-block
+//    pieces (Q3KSB::pack, then Q3KSB::unpack), which returns the words exactly;
+//  * sb_geom / sb_piece place every piece of every superblock of a weight at
+//    a distinct 16-byte slot inside blocks * LB * P * 16 bytes.
 // Exit status 0 when every check holds.
 #include "../uefi-gpu_amd/csrc/uq_units.h"
 #include <cmath>
@@ -30,7 +34,28 @@ static int dot4(int a, int b, int c) {
 
 int main() {
     std::mt19937 rng(0x5EED0003u);
-    long bad_parts = 0, bad_dots = 0, bad_rows = 0, rows_total = 0;
+    long bad_parts = 0, bad_dots = 0, bad_rows = 0, rows_total = 0, bad_sb = 0, bad_geom = 0;
+    // row-block geometry: pieces of distinct (row, superblock, piece) land on
+    // distinct slots inside the allocation
+    for (int n : {256, 768, 1536, 2048, 3072, 6144, 8960, 16384}) {
+        for (int m : {1, 7, 10, 11, 100}) {
+            const uq::SbGeom g = uq::sb_geom(n, m);
+            if (!g.LB || g.RB * g.S > g.LB || g.RB < 1 || 8 * (g.LB - g.RB * g.S) > g.LB && g.LB < 256) {
+                bad_geom++;
+                continue;
+            }
+            for (int P : {7}) {
+                const int64_t slots = g.blocks * g.LB * P;
+                std::vector<char> seen((size_t)slots, 0);
+                for (int r = 0; r < m; r++)
+                    for (int sb = 0; sb < g.S; sb++)
+                        for (int k = 0; k < P; k++) {
+                            const int64_t o = uq::sb_piece(r, sb, k, g.S, g.LB, g.RB, P);
+                            if (o % 16 || o < 0 || o / 16 >= slots || seen[(size_t)(o / 16)]++) bad_geom++;
+                        }
+            }
+        }
+    }
     for (int n : {256, 768, 1536, 2048}) {
         const int m = 24, nsb = n / 256;
         std::vector<uint8_t> w((size_t)m * nsb * 110);
@@ -53,9 +78,14 @@ int main() {
             double acc = 0.0;
             for (int sb = 0; sb < nsb; sb++) {
                 const uint8_t* g = w.data() + ((size_t)r * nsb + sb) * 110;
+                uint32_t UA[4][4], UP[4][4], UA2[4][4], UP2[4][4], pw[28];
+                for (int p = 0; p < 4; p++) uq::Q3K::pack_unit(g, p, UA[p], UP[p]);
+                uq::Q3KSB::pack(UA, UP, pw);
+                uq::Q3KSB::unpack(pw, UA2, UP2);
+                bad_sb += std::memcmp(UA, UA2, sizeof(UA)) != 0 || std::memcmp(UP, UP2, sizeof(UP)) != 0;
                 for (int p = 0; p < 4; p++) {
-                    uint32_t A[4], P[4];
-                    uq::Q3K::pack_unit(g, p, A, P);
+                    const uint32_t* A = UA2[p];
+                    const uint32_t* P = UP2[p];
                     for (int c = 0; c < 4; c++)
                         for (int t = 0; t < 4; t++)
                             for (int b = 0; b < 4; b++) {
@@ -101,5 +131,6 @@ int main() {
     }
     printf("parts differing: %ld, dots differing: %ld, rows beyond 1 ulp: %ld of %ld\n", bad_parts, bad_dots,
            bad_rows, rows_total);
-    return bad_parts || bad_dots || bad_rows;
+    printf("row-block round trips differing: %ld, geometry faults: %ld\n", bad_sb, bad_geom);
+    return bad_parts || bad_dots || bad_rows || bad_sb || bad_geom;
 }

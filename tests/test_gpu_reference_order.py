@@ -65,8 +65,17 @@ def test_two_layers_full_shape_teacher_forced(gpu):
 
 def test_28_layers_after_512_prompt_teacher_forced(gpu):
     """The 28-layer model of qwen25_decode.json: the GPU prefill of the
-    512-token prompt, then 8 decode steps fed the fixture's tokens, against
-    tests/golden/qwen25_refo.npz (made by tests/golden/make_refo_golden.py)."""
+    512-token prompt, then all 128 decode steps fed the fixture's tokens (the
+    build's own greedy ids, so the forced run is the free-running one),
+    against tests/golden/qwen25_refo.npz (made by
+    tests/golden/make_refo_golden.py): 129 positions, compared with the
+    reference-order decoder with the KV cache in f32 and in fp16.
+
+    Graded: the GPU's greedy ids equal the exact oracle's at every position;
+    the logits stay within the measured deviation bound of the reference
+    order; where the reference-order top-2 margin exceeds twice the step's
+    deviation the ids agree; and the count of positions whose ids agree with
+    the reference order is the fixture's (the exact oracle's) count."""
     import json
     g = json.load(open(os.path.join(HERE, "golden", "qwen25_decode.json")))
     f = np.load(os.path.join(HERE, "golden", "qwen25_refo.npz"))
@@ -75,17 +84,26 @@ def test_28_layers_after_512_prompt_teacher_forced(gpu):
     try:
         prompt = uq.synth_tokens(g["seed"], g["prompt_len"], cfg["vocab"])
         ids = [m.prefill(prompt)]
-        logits = [m.logits()]
+        logits = [m.logits()[f["idx"][0]]]
         for i, tok in enumerate(f["forced"]):
             ids.append(m.decode_step(int(tok), g["prompt_len"] + i))
-            logits.append(m.logits())
+            logits.append(m.logits()[f["idx"][i + 1]])
     finally:
         m.free()
+    n = len(f["forced"]) + 1
+    assert n == 129 and len(ids) == n
     assert ids[:-1] == [int(t) for t in f["forced"]]       # the fixture's tokens are this build's greedy ids
-    for k, bound in (("f16", 0.06), ("f32", 0.1)):
-        for p, lg in enumerate(logits):
-            got = lg[f["idx"][p]]
+    assert ids == [int(t) for t in f["argmax_exact"]]      # and the exact oracle's, at all 129 positions
+    # measured over the 129 positions (exact oracle vs reference order): fp16
+    # cache max 0.047, median 0.028; f32 cache max 0.257, median 0.047
+    for k, bound in (("f16", 0.06), ("f32", 0.3)):
+        agree = 0
+        for p, got in enumerate(logits):
             d = float(np.abs(got - f["ref_" + k][p]).max() / f["absmax_" + k][p])
             assert d <= bound, (k, p, d)
             if f["margin_" + k][p] / f["absmax_" + k][p] > 2 * d:
                 assert ids[p] == int(f["argmax_" + k][p]), (k, p, d)
+            agree += ids[p] == int(f["argmax_" + k][p])
+        want = int((f["argmax_exact"] == f["argmax_" + k]).sum())
+        assert agree == want, (k, agree, want)
+        print("%s-cache reference order: greedy ids equal at %d of %d positions" % (k, agree, n))

@@ -1,6 +1,7 @@
-"""The Q3_K unit code of the device header (uefi-gpu_amd/csrc/uq_units.h:
-Q3K::pack_unit, unit_parts and words, the source of the upload repack, its
-verify kernel and the matvec's 3-bit assembly) built for the host and checked
+"""The K-quant layout code of the device header (uefi-gpu_amd/csrc/uq_units.h:
+Q3K::pack_unit, unit_parts and words, the row-block Q3KSB::pack/unpack and
+sb_geom/sb_piece, the source of the upload repacks, their
+verify kernels and the matvecs' bit assembly) built for the host and checked
 against the oracle (uqo_q3k_block_dots, uqo_matvec_x; oracle/uq_oracle.c, whose
 Q3_K decode follows ggml's dequantize_row_q3_K and is pinned by the byte-literal
 known-answer blocks of test_oracle_core.py) on seeded GGUF rows of 1 to 8
@@ -31,3 +32,4 @@ def test_q3k_unit_layout_matches_oracle(tmp_path):
     r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout
     assert "parts differing: 0, dots differing: 0, rows beyond 1 ulp: 0 of 96" in r.stdout
+    assert "row-block round trips differing: 0, geometry faults: 0" in r.stdout

@@ -45,9 +45,9 @@ int64_t row_bytes(uint32_t kind, int64_t n);  // GGUF bytes of one row, <0 if in
 // Device-resident weight. The frontier kinds (F32, BF16, Q6_K, IQ3_XXS,
 // IQ4_NL, IQ4_XS) use the planes of their FrontierLayout: qs = body units,
 // sc = aux bytes, d = fp16 block scales. Q8_0 is split into an int8 plane qs[m][n] and an
-// fp16 scale plane d[m][n/32]; Q4_K keeps the 144-byte superblocks (16-byte
-// aligned already); Q3_K is split into quants q[m][n/256][96] (hmask 32 B +
-// qs 64 B), packed 6-bit scales sc[m][n/256][12] and fp16 d[m][n/256].
+// fp16 scale plane d[m][n/32]; Q4_K and Q3_K use the unit planes of Q4K /
+// Q3K (qs, sc, d); lm_head-sized Q3_K weights use the row-block layout of
+// Q3KSB in qs alone.
 struct Weight {
     uint32_t kind = 0;
     int64_t n = 0, m = 0;   // n = K (input length), m = N (output rows)
@@ -57,6 +57,9 @@ struct Weight {
     const uint16_t* d = nullptr;   // Q8_0 / Q3_K fp16 scales
     const uint8_t* sc = nullptr;   // Q3_K packed scales
     int64_t gguf_bytes = 0;        // bytes of the original GGUF tensor
+    // Q3_K in the row-block layout (uq_units.h, SbGeom): lane slots and rows
+    // per block, 0 for the unit planes
+    int sb_lb = 0, sb_rb = 0;
 };
 
 // Compute units of the current device (queried once).
@@ -95,6 +98,10 @@ void launch_q4k_verify(const int8_t* q, const uint8_t* scm, const uint32_t* dm, 
 void launch_q3k_repack(const uint8_t* gguf, int64_t blocks, int8_t* q, int8_t* sc, uint16_t* d, hipStream_t s);
 void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, const uint8_t* gguf, int64_t blocks,
                        unsigned* mismatches, hipStream_t s);
+// Q3_K into the row-block layout (lb slots, rb rows per block) at dst
+// (zeroed beforehand), then the byte-for-byte rebuild check into *bad.
+void launch_sb_repack(uint32_t kind, const uint8_t* gguf, int64_t n, int64_t m, int lb, int rb, uint8_t* dst,
+                      unsigned* bad, hipStream_t s);
 // y[m] = W x for any kind; gate/up fusion writes silu(gate)*up when w2 != null.
 int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s);
 int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStream_t s);

@@ -139,20 +139,15 @@ __global__ __launch_bounds__(WG) void k_q3k_repack(const uint8_t* __restrict__ s
         for (int k = 0; k < 4; k++) pw[4 * p + k] = P[k];
     }
 }
-__global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const int8_t* __restrict__ sc,
-                                                   const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
-                                                   int64_t blocks, unsigned* __restrict__ bad) {
-    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
-    if (blk >= blocks) return;
-    const uint8_t* g = src + blk * 110;
-    const uint32_t* qa = (const uint32_t*)q + blk * 16;
-    const uint32_t* pw = (const uint32_t*)sc + blk * 16;
+// Bytes of GGUF superblock g that the four units' words A, P do not rebuild
+// (hmask, qs, the 12 scale bytes, d in every unit).
+__device__ unsigned q3k_units_miss(const uint32_t (&A4)[4][4], const uint32_t (&P4)[4][4], const uint8_t* g) {
     uint8_t hm[32] = {}, qs[64] = {};
     int v[16];
     unsigned miss = 0;
     for (int p = 0; p < 4; p++) {
-        const uint32_t A[4] = {qa[4 * p], qa[4 * p + 1], qa[4 * p + 2], qa[4 * p + 3]};
-        const uint32_t P[4] = {pw[4 * p], pw[4 * p + 1], pw[4 * p + 2], pw[4 * p + 3]};
+        const uint32_t* A = A4[p];
+        const uint32_t* P = P4[p];
         miss += P[3] != ((uint32_t)g[108] | (uint32_t)g[109] << 8);
         for (int c = 0; c < 4; c++) {
             v[4 * p + c] = (int)(int8_t)(P[2] >> (8 * c)) + 32;
@@ -175,6 +170,61 @@ __global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q,
         for (int gr = 0; gr < 4; gr++) b |= ((v[4 * gr + m] >> 4) & 3) << (2 * gr);
         miss += (uint8_t)b != g[104 + m];
     }
+    return miss;
+}
+__global__ __launch_bounds__(WG) void k_q3k_verify(const int8_t* __restrict__ q, const int8_t* __restrict__ sc,
+                                                   const uint16_t* __restrict__ d, const uint8_t* __restrict__ src,
+                                                   int64_t blocks, unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const uint32_t* qa = (const uint32_t*)q + blk * 16;
+    const uint32_t* pw = (const uint32_t*)sc + blk * 16;
+    uint32_t A[4][4], P[4][4];
+    for (int p = 0; p < 4; p++)
+        for (int t = 0; t < 4; t++) {
+            A[p][t] = qa[4 * p + t];
+            P[p][t] = pw[4 * p + t];
+        }
+    const unsigned miss = q3k_units_miss(A, P, src + blk * 110);
+    if (miss) atomicAdd(bad, miss);
+}
+
+// Row-block layout (Q3KSB): one thread per GGUF superblock writes its P
+// pieces; the verify kernel rebuilds the GGUF bytes from the pieces. The
+// padding slots of the allocation are zeroed before the repack.
+struct SbArgs {
+    int S, LB, RB;
+};
+__global__ __launch_bounds__(WG) void k_q3k_sb_repack(const uint8_t* __restrict__ src, int64_t blocks, SbArgs g,
+                                                      uint8_t* __restrict__ dst) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const int64_t r = blk / g.S;
+    const int sbi = (int)(blk - r * g.S);
+    uint32_t A[4][4], P[4][4], w[28];
+    for (int u = 0; u < 4; u++) Q3K::pack_unit(src + blk * 110, u, A[u], P[u]);
+    Q3KSB::pack(A, P, w);
+    for (int k = 0; k < Q3KSB::P; k++)
+        *(int4*)(dst + sb_piece(r, sbi, k, g.S, g.LB, g.RB, Q3KSB::P)) =
+            make_int4((int)w[4 * k], (int)w[4 * k + 1], (int)w[4 * k + 2], (int)w[4 * k + 3]);
+}
+__global__ __launch_bounds__(WG) void k_q3k_sb_verify(const uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                      int64_t blocks, SbArgs g, unsigned* __restrict__ bad) {
+    const int64_t blk = (int64_t)blockIdx.x * WG + threadIdx.x;
+    if (blk >= blocks) return;
+    const int64_t r = blk / g.S;
+    const int sbi = (int)(blk - r * g.S);
+    uint32_t w[28], A[4][4], P[4][4];
+    for (int k = 0; k < Q3KSB::P; k++) {
+        const int4 v = *(const int4*)(dst + sb_piece(r, sbi, k, g.S, g.LB, g.RB, Q3KSB::P));
+        w[4 * k] = (uint32_t)v.x;
+        w[4 * k + 1] = (uint32_t)v.y;
+        w[4 * k + 2] = (uint32_t)v.z;
+        w[4 * k + 3] = (uint32_t)v.w;
+    }
+    Q3KSB::unpack(w, A, P);
+    // the 2 bytes after d are padding and hold zero
+    unsigned miss = q3k_units_miss(A, P, src + blk * 110) + ((w[27] >> 16) != 0);
     if (miss) atomicAdd(bad, miss);
 }
 
@@ -362,11 +412,121 @@ __global__ __launch_bounds__(WG) void k_matvec_xl(WArgs w, WArgs w2, const int8_
     }
 }
 
+// ---------------------------------------------------------------- row-block matvec
+// Q3KSB layout: lane t owns slot t % LB of row block
+// blockIdx.x * (blockDim.x / LB) + t / LB, i.e. one superblock of one row, and
+// loads its P pieces, each wave instruction covering 1 KB of consecutive
+// bytes. The activation, its scales and its 16-value sums are staged in LDS
+// per superblock with strides of 272, 48 and 80 bytes, so the 16-byte reads
+// of lanes on different superblocks fall on different banks. Each lane's
+// double term goes to LDS and one thread per row adds its row's S terms in
+// superblock order (the same exact double terms as the unit kernels; only
+// the order of the double additions differs).
+constexpr int SB_X = 272, SB_XS = 12, SB_S16 = 20;
+inline size_t sb_lds_bytes(int S, int nthr, bool pair) {
+    return (size_t)S * (SB_X + 4 * SB_XS + 4 * SB_S16) + (size_t)nthr * 8 * (pair ? 2 : 1);
+}
+template <class KS> struct SbDot;
+template <> struct SbDot<Q3KSB> {
+    static UQ_DEV int stage16(int g, int sum) { return Q3K::gs_corr(g & 3, sum); }
+    static UQ_DEV double dot(const int4 (&w)[Q3KSB::P], const int8_t* lx, const float* lxs, const int* l16) {
+        const double dd = (double)uq_half((uint16_t)((uint32_t)w[6].w & 0xffff));
+        double acc = 0.0;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int4 A = w[u], Bq = w[4 + (u >> 1)];
+            const uint32_t B0 = (uint32_t)((u & 1) ? Bq.z : Bq.x), B1 = (uint32_t)((u & 1) ? Bq.w : Bq.y);
+            const int4* xp = (const int4*)(lx + 64 * u);
+            const int4 xv[4] = {xp[0], xp[1], xp[2], xp[3]};
+            const int4 c = *(const int4*)(l16 + 4 * u);
+            const float2 xs = *(const float2*)(lxs + 2 * u);
+            int D0 = c.x, D1 = c.y, D2 = c.z, D3 = c.w;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int wd[4];
+                Q3K::words((uint32_t)Q3K::lane4(A, t), t < 2 ? B0 : B1, t, wd);
+                D0 = uq_dot4(wd[0], Q3K::lane4(xv[0], t), D0);
+                D1 = uq_dot4(wd[1], Q3K::lane4(xv[1], t), D1);
+                D2 = uq_dot4(wd[2], Q3K::lane4(xv[2], t), D2);
+                D3 = uq_dot4(wd[3], Q3K::lane4(xv[3], t), D3);
+            }
+            const uint32_t win = Q3KSB::scale_window((uint32_t)w[6].x, (uint32_t)w[6].y, (uint32_t)w[6].z, u);
+            const int s0 = Q3KSB::scale_field(win, 0), s1 = Q3KSB::scale_field(win, 1);
+            const int s2 = Q3KSB::scale_field(win, 2), s3 = Q3KSB::scale_field(win, 3);
+            const int T0 = uq_mul24(s0, D0) + uq_mul24(s1, D1);
+            const int T1 = uq_mul24(s2, D2) + uq_mul24(s3, D3);
+            acc += (dd * (double)xs.x) * (double)T0 + (dd * ((double)xs.y * (1.0 / 16))) * (double)T1;
+        }
+        return acc;
+    }
+};
+
+template <class KS, bool GATEUP>
+__global__ __launch_bounds__(WG) void k_matvec_sb(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                  const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                  float* __restrict__ y, int64_t rows, int64_t blocks, SbArgs g) {
+    extern __shared__ __attribute__((aligned(16))) int8_t sb_lds[];
+    constexpr int P = KS::P;
+    const int S = g.S, LB = g.LB, RB = g.RB, K = 256 * S;
+    int8_t* lx = sb_lds;
+    float* lxs = (float*)(sb_lds + S * SB_X);
+    int* l16 = (int*)(lxs + SB_XS * S);
+    double* part = (double*)(l16 + SB_S16 * S);
+    const int tid = threadIdx.x, nthr = blockDim.x, bpw = nthr / LB;
+    for (int gi = tid; gi < K / 16; gi += nthr) {
+        const int4 v = ((const int4*)xq)[gi];
+        const int sb = gi >> 4, wi = gi & 15;
+        *(int4*)(lx + sb * SB_X + 16 * wi) = v;
+        l16[sb * SB_S16 + wi] = SbDot<KS>::stage16(wi, Q3K::sum16(v));
+    }
+    for (int b = tid; b < K / 32; b += nthr) lxs[(b >> 3) * SB_XS + (b & 7)] = xs[b];
+    __syncthreads();
+    const int64_t blk = (int64_t)blockIdx.x * bpw + tid / LB;
+    const int j = tid % LB, rr = j / S, s = j - rr * S;
+    const bool valid = rr < RB && blk * RB + rr < rows;
+    // a block past the last one (grid rounding) reads the last block's slot
+    const int64_t bl = blk < blocks ? blk : blocks - 1;
+    const uint8_t* base = w + (bl * P * LB + j) * 16;
+    int4 wv[P], wv2[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) wv[k] = uq_ntload16(base + (int64_t)k * LB * 16);
+    if (GATEUP) {
+        const uint8_t* base2 = w2 + (bl * P * LB + j) * 16;
+#pragma unroll
+        for (int k = 0; k < P; k++) wv2[k] = uq_ntload16(base2 + (int64_t)k * LB * 16);
+    }
+    const int8_t* xsb = lx + s * SB_X;
+    const float* xssb = lxs + s * SB_XS;
+    const int* s16 = l16 + s * SB_S16;
+    const double v = SbDot<KS>::dot(wv, xsb, xssb, s16);
+    part[tid] = valid ? v : 0.0;
+    if (GATEUP) {
+        const double v2 = SbDot<KS>::dot(wv2, xsb, xssb, s16);
+        part[nthr + tid] = valid ? v2 : 0.0;
+    }
+    __syncthreads();
+    if (tid < bpw * RB) {
+        const int bb = tid / RB, r = tid - bb * RB;
+        const int64_t row = ((int64_t)blockIdx.x * bpw + bb) * RB + r;
+        if (row < rows) {
+            const double* pr = part + bb * LB + r * S;
+            double a = 0.0, a2 = 0.0;
+            for (int q = 0; q < S; q++) a += pr[q];
+            if (GATEUP) {
+                for (int q = 0; q < S; q++) a2 += pr[nthr + q];
+                y[row] = uq_silu_mul((float)a, (float)a2);
+            } else {
+                y[row] = (float)a;
+            }
+        }
+    }
+}
+
 // Integer per-block dots (test surface for the int32 work): Q8_0 per 32-block,
 // Q4_K per 32 sub-block (q 0..15), Q3_K per 16 sub-block (q3 -4..3); one thread
 // per (row, block), using the same int8 dot primitive as the matvec.
 __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const int8_t* __restrict__ xq,
-                                                   int32_t* __restrict__ dots, int64_t rows, int64_t K) {
+                                                   int32_t* __restrict__ dots, int64_t rows, int64_t K, SbArgs sb) {
     const int bsz = kind == KIND_Q3_K ? 16 : 32;
     const int64_t nb = K / bsz;
     const int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x;
@@ -374,6 +534,34 @@ __global__ __launch_bounds__(WG) void k_block_dots(WArgs w, uint32_t kind, const
     const int64_t row = i / nb, b = i % nb;
     const int8_t* x = xq + b * bsz;
     int c = 0;
+    if (sb.LB) {
+        // row-block layout (Q3_K): the superblock's pieces, then its unit words
+        const int sbi = (int)(b / 16), k = (int)(b % 16);
+        uint32_t wd[4 * Q3KSB::P];
+        for (int p = 0; p < Q3KSB::P; p++) {
+            const int4 v = *(const int4*)((const uint8_t*)w.qs + sb_piece(row, sbi, p, sb.S, sb.LB, sb.RB, Q3KSB::P));
+            wd[4 * p] = (uint32_t)v.x;
+            wd[4 * p + 1] = (uint32_t)v.y;
+            wd[4 * p + 2] = (uint32_t)v.z;
+            wd[4 * p + 3] = (uint32_t)v.w;
+        }
+        const int* xp = (const int*)x;
+        uint32_t A[4][4], Pw[4][4];
+        Q3KSB::unpack(wd, A, Pw);
+        const int u = k >> 2, cc = k & 3;
+        for (int t = 0; t < 4; t++) {
+            int v = 0;
+            for (int bb = 0; bb < 4; bb++) {
+                int low2, hbit;
+                Q3K::unit_parts(A[u], Pw[u], cc, t, bb, low2, hbit);
+                v |= (low2 | hbit << 2) << (8 * bb);
+            }
+            c = uq_dot4(v, xp[t], c);
+            c -= 4 * uq_dot4(0x01010101, xp[t], 0);
+        }
+        dots[i] = c;
+        return;
+    }
     if (kind == KIND_Q8_0) {
         const int4* p = (const int4*)(w.qs + i * 32);
         const int4* xp = (const int4*)x;
@@ -463,6 +651,29 @@ void launch_t(const Weight& w, const Weight* w2, const int8_t* xq, const float* 
     }
 }
 
+// Row-block layout: one block per LB-lane group, the largest group count per
+// workgroup (of 256 threads at most) that still gives two workgroups per CU.
+template <class KS>
+int launch_sb(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
+    const SbGeom g = sb_geom(w.n, w.m);
+    if (g.LB != w.sb_lb || g.RB != w.sb_rb || (w2 && (w2->sb_lb != w.sb_lb || w2->sb_rb != w.sb_rb)))
+        return set_error(ERR_SHAPE, "matvec: row-block geometry differs from the upload's");
+    int bpw = WG / g.LB;
+    while (bpw > 1 && (g.blocks + bpw - 1) / bpw < 2 * (int64_t)cu_count()) bpw /= 2;
+    const int nthr = bpw * g.LB;
+    const unsigned grid = (unsigned)((g.blocks + bpw - 1) / bpw);
+    const size_t lds = sb_lds_bytes(g.S, nthr, w2 != nullptr);
+    const SbArgs a{g.S, g.LB, g.RB};
+    const uint8_t* q = (const uint8_t*)w.qs;
+    if (w2)
+        hipLaunchKernelGGL((k_matvec_sb<KS, true>), dim3(grid), dim3(nthr), lds, s, q, (const uint8_t*)w2->qs, xq, xs, y,
+                           w.m, g.blocks, a);
+    else
+        hipLaunchKernelGGL((k_matvec_sb<KS, false>), dim3(grid), dim3(nthr), lds, s, q, nullptr, xq, xs, y, w.m,
+                           g.blocks, a);
+    return OK;
+}
+
 // Lane-group size per row from the number of units per row: small rows use
 // short groups (more rows per wave), long rows spread over a full wave.
 template <class KQ>
@@ -528,6 +739,15 @@ void launch_q3k_verify(const int8_t* q, const int8_t* sc, const uint16_t* d, con
                        unsigned* bad, hipStream_t s) {
     hipLaunchKernelGGL(k_q3k_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, q, sc, d, gguf, blocks, bad);
 }
+void launch_sb_repack(uint32_t kind, const uint8_t* gguf, int64_t n, int64_t m, int lb, int rb, uint8_t* dst,
+                      unsigned* bad, hipStream_t s) {
+    const int64_t blocks = n / 256 * m;
+    const SbArgs g{(int)(n / 256), lb, rb};
+    if (kind != KIND_Q3_K) return;
+    hipLaunchKernelGGL(k_q3k_sb_repack, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, gguf, blocks, g, dst);
+    hipLaunchKernelGGL(k_q3k_sb_verify, dim3(grid_for(blocks, WG)), dim3(WG), 0, s, (const uint8_t*)dst, gguf,
+                       blocks, g, bad);
+}
 
 namespace {
 // The job table of weights sharing K: the resident workgroups of the chip are
@@ -591,10 +811,11 @@ int launch_matvec_multi(const Weight* const* ws, const Weight* const* w2s, float
 int launch_matvec(const Weight& w, const Weight* w2, const int8_t* xq, const float* xs, float* y, hipStream_t s) {
     if (w2 && (w2->kind != w.kind || w2->n != w.n || w2->m != w.m))
         return set_error(ERR_SHAPE, "gate/up pair: shapes differ");
+    if (w2 && (w2->sb_lb != 0) != (w.sb_lb != 0)) return set_error(ERR_SHAPE, "gate/up pair: device layouts differ");
     switch (w.kind) {
     case KIND_Q8_0: return launch_kind<Q8>(w, w2, xq, xs, y, s);
     case KIND_Q4_K: return launch_kind<Q4K>(w, w2, xq, xs, y, s);
-    case KIND_Q3_K: return launch_kind<Q3K>(w, w2, xq, xs, y, s);
+    case KIND_Q3_K: return w.sb_lb ? launch_sb<Q3KSB>(w, w2, xq, xs, y, s) : launch_kind<Q3K>(w, w2, xq, xs, y, s);
     default: return set_error(ERR_QUANT_TYPE, "matvec: unsupported kind");
     }
 }
@@ -605,7 +826,8 @@ int launch_block_dots(const Weight& w, const int8_t* xq, int32_t* dots, hipStrea
     const int bsz = w.kind == KIND_Q3_K ? 16 : 32;
     const int64_t items = w.m * (w.n / bsz);
     WArgs a{w.qs, w.d, w.sc};
-    hipLaunchKernelGGL(k_block_dots, dim3(grid_for(items, WG)), dim3(WG), 0, s, a, w.kind, xq, dots, w.m, w.n);
+    const SbArgs sb{(int)(w.n / 256), w.sb_lb, w.sb_rb};
+    hipLaunchKernelGGL(k_block_dots, dim3(grid_for(items, WG)), dim3(WG), 0, s, a, w.kind, xq, dots, w.m, w.n, sb);
     return OK;
 }
 

@@ -5,6 +5,7 @@
 // semaphores; here one HIP stream per process carries every launch and
 // hipStreamSynchronize is the completion poll.
 #include "uq_internal.h"
+#include "uq_units.h"
 #include "../../include/uq.h"
 
 #include <algorithm>
@@ -251,7 +252,19 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
     w.gguf_bytes = rb * m;
     size_t total = 0;
     size_t off_q = 0, off_d = 0, off_sc = 0;
-    if (kind == KIND_Q8_0) {
+    // lm_head-sized Q3_K weights (row blocks for eight workgroups per CU)
+    // take the row-block layout; expert banks keep the unit planes that the
+    // MoE kernels address by expert row
+    SbGeom sg;
+    if (kind == KIND_Q3_K && !bank) {
+        sg = sb_geom(n, m);
+        if (!sg.LB || sg.blocks < 8 * (int64_t)cu_count()) sg = SbGeom();
+    }
+    if (sg.LB) {
+        w.sb_lb = sg.LB;
+        w.sb_rb = sg.RB;
+        total = align256((size_t)sg.blocks * sg.LB * Q3KSB::P * 16);
+    } else if (kind == KIND_Q8_0) {
         off_q = 0;
         off_d = align256((size_t)(n * m));
         total = off_d + align256((size_t)(n / 32 * m) * 2);
@@ -273,16 +286,21 @@ int upload_weight(uint32_t kind, int64_t n, int64_t m, const void* gguf, size_t 
     w.alloc_bytes = total;
     uint8_t* base = (uint8_t*)w.alloc;
     w.qs = (const int8_t*)(base + off_q);
-    w.d = (const uint16_t*)(base + off_d);
-    if (kind != KIND_Q8_0) w.sc = base + off_sc;
+    if (!sg.LB) {
+        w.d = (const uint16_t*)(base + off_d);
+        if (kind != KIND_Q8_0) w.sc = base + off_sc;
+    }
     int rc = OK;
     {
         void* staging = nullptr;
         hipError_t e = hipMalloc(&staging, (size_t)w.gguf_bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(staging, gguf, (size_t)w.gguf_bytes, hipMemcpyHostToDevice, s);
         if (e == hipSuccess) e = hipMemsetAsync(g_ctx.dcount, 0, sizeof(unsigned), s);
+        if (e == hipSuccess && sg.LB) e = hipMemsetAsync(w.alloc, 0, total, s);  // the padding slots
         if (e == hipSuccess) {
-            if (kind == KIND_Q8_0) {
+            if (sg.LB) {
+                launch_sb_repack(kind, (const uint8_t*)staging, n, m, sg.LB, sg.RB, (uint8_t*)w.alloc, g_ctx.dcount, s);
+            } else if (kind == KIND_Q8_0) {
                 launch_q8_repack((const uint8_t*)staging, m, n / 32, (int8_t*)w.qs, (uint16_t*)w.d, s);
                 launch_q8_verify(w.qs, w.d, (const uint8_t*)staging, m, n / 32, g_ctx.dcount, s);
             } else if (kind == KIND_Q4_K) {

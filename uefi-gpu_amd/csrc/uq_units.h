@@ -136,7 +136,7 @@ struct Q4K {
         return dot(wv, x, u);
     }
     // ggml get_scale_min_k4: 12 packed bytes b -> scale and min of sub-block k
-    static UQ_DEV void scale_min_k4(const uint8_t* b, int k, int& sc, int& m) {
+    static UQ_HD void scale_min_k4(const uint8_t* b, int k, int& sc, int& m) {
         if (k < 4) {
             sc = b[k] & 63;
             m = b[k + 4] & 63;
@@ -308,6 +308,99 @@ struct Q3K {
         else if (c == 2) { low2 = (a >> 4) & 3; hbit = (a >> 6) & 1; }
         else if (c == 1) { low2 = bb & 3; hbit = (a >> 3) & 1; }
         else { low2 = (bb >> 4) & 3; hbit = a >> 7; }
+    }
+};
+
+// ---------------------------------------------------------------- row-block layout
+// lm_head-sized Q3_K weights are stored in row blocks in which one lane owns
+// one whole superblock and moves it as 16-byte pieces only. A block
+// has LB lane slots (64, 128 or 256) holding RB = LB / S rows of S = K / 256
+// superblocks (slot j = row-in-block * S + superblock; slots from RB * S on
+// are padding); piece k of slot j sits at block * LB * P * 16 + k * LB * 16 +
+// j * 16, so one load instruction of a wave reads 64 consecutive pieces, a
+// kilobyte of whole cache lines. Q3KSB, P = 7: pieces 0..3 the A words of
+// the four 64-value units (the Q3K unit words), piece 4 the B words of units
+// 0 and 1, piece 5 those of units 2 and 3, piece 6 the sixteen scales - 32
+// as signed 6-bit fields (unit u's four at bits 24u + 6c of the first 96
+// bits) and d in the low half of the last word: 112 bytes for GGUF's 110.
+// (The same layout for Q4_K, its 144-byte superblock verbatim in 9 pieces,
+// measured 70-71% of 8 TB/s on lm_head against 76-77% for the Q4K unit
+// planes, and 74-75% with the dots removed: its access pattern, not its
+// arithmetic, bounds it, so Q4_K keeps the unit planes.)
+struct SbGeom {
+    int S = 0, LB = 0, RB = 0;  // superblocks per row, lane slots and rows per block
+    int64_t blocks = 0;         // row blocks (the last one may hold padding rows)
+};
+// The smallest block (64, 128 or 256 slots) leaving at most 1/8 of its slots
+// idle (S <= 64; else no row-block layout).
+inline SbGeom sb_geom(int64_t n, int64_t m) {
+    SbGeom g;
+    if (n % 256 || n / 256 > 64 || m <= 0) return g;
+    g.S = (int)(n / 256);
+    for (int lb = 64; lb <= 256; lb *= 2) {
+        const int rb = lb / g.S;
+        if (rb >= 1 && 8 * (lb - rb * g.S) <= lb) {
+            g.LB = lb;
+            g.RB = rb;
+            break;
+        }
+    }
+    if (!g.LB) {
+        g.LB = 256;
+        g.RB = 256 / g.S;
+    }
+    g.blocks = (m + g.RB - 1) / g.RB;
+    return g;
+}
+// Byte offset of piece k of superblock s of row r.
+UQ_HD int64_t sb_piece(int64_t r, int s, int k, int S, int LB, int RB, int P) {
+    const int64_t b = r / RB;
+    const int j = (int)(r - b * RB) * S + s;
+    return ((b * P + k) * LB + j) * 16;
+}
+
+struct Q3KSB {
+    static constexpr int P = 7;
+    // the eight Q3K unit words A[u][4], B[u][2], the scales - 32 as signed
+    // bytes S[u] and d, into the seven pieces (28 words)
+    static UQ_HD void pack(const uint32_t A[4][4], const uint32_t Pw[4][4], uint32_t* w) {
+        for (int u = 0; u < 4; u++)
+            for (int t = 0; t < 4; t++) w[4 * u + t] = A[u][t];
+        for (int u = 0; u < 4; u++) {
+            w[16 + 2 * u] = Pw[u][0];
+            w[17 + 2 * u] = Pw[u][1];
+        }
+        uint32_t f[3] = {0, 0, 0};
+        for (int u = 0; u < 4; u++)
+            for (int c = 0; c < 4; c++) {
+                const uint32_t v = (Pw[u][2] >> (8 * c)) & 63;  // low 6 bits of the signed byte
+                const int bit = 24 * u + 6 * c;
+                f[bit >> 5] |= v << (bit & 31);
+                if ((bit & 31) > 26) f[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
+            }
+        w[24] = f[0];
+        w[25] = f[1];
+        w[26] = f[2];
+        w[27] = Pw[0][3] & 0xffff;
+    }
+    // unit u's 24-bit scale window (four signed 6-bit fields at 6c)
+    static UQ_HD uint32_t scale_window(uint32_t f0, uint32_t f1, uint32_t f2, int u) {
+        const uint64_t lo = (uint64_t)f0 | (uint64_t)f1 << 32, hi = (uint64_t)f1 | (uint64_t)f2 << 32;
+        return u == 0 ? f0 : u == 1 ? (uint32_t)(lo >> 24) : u == 2 ? (uint32_t)(hi >> 16) : f2 >> 8;
+    }
+    static UQ_HD int scale_field(uint32_t win, int c) { return (int)(win << (26 - 6 * c)) >> 26; }
+    // the inverse of pack: unit words with P[u][2] the signed scale bytes and P[u][3] = d
+    static UQ_HD void unpack(const uint32_t* w, uint32_t A[4][4], uint32_t Pw[4][4]) {
+        for (int u = 0; u < 4; u++) {
+            for (int t = 0; t < 4; t++) A[u][t] = w[4 * u + t];
+            Pw[u][0] = w[16 + 2 * u];
+            Pw[u][1] = w[17 + 2 * u];
+            const uint32_t win = scale_window(w[24], w[25], w[26], u);
+            uint32_t sb = 0;
+            for (int c = 0; c < 4; c++) sb |= (uint32_t)(uint8_t)(int8_t)scale_field(win, c) << (8 * c);
+            Pw[u][2] = sb;
+            Pw[u][3] = w[27] & 0xffff;
+        }
     }
 };
 

@@ -185,23 +185,46 @@ def decode_bench(prompt_len=512, steps=128, keep=None):
             "model_upload_s": round(t_load, 1), "first_ids": [int(first)] + [int(i) for i in ids[:7]]}
 
 
+# VALU lane-operations per second of the chip: 256 CUs x 4 SIMDs x 16 lanes
+# x 2.4 GHz (packed FP32 not used). The prefill GEMM keeps the reference's
+# per-block f32 update, a convert and an fmaf per output and 32-block on the
+# VALU (the scale product comes from an f32 outer-product MFMA), so
+# 2 x M x N x K/32 lane-operations bound each launch from below.
+VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9
+
+
 def prefill_gemm_bench(tokens=512, reps=20):
     """512-token Q8_0 prefill GEMMs (N x K) 1536x1536, 256x1536, 8960x1536 gate+up
-    pair (one fused launch), 1536x8960 on int8 MFMA: TOPS = 2*M*N*K / time."""
+    pair (one fused launch), 1536x8960 on int8 MFMA: TOPS = 2*M*N*K / time,
+    against the 5.0 POPS int8 peak and each launch's VALU floor. The model runs
+    q|k|v as one N = 2048 launch over the shared input: that launch and the
+    model layer's four launches are reported beside the shapes above."""
     out = {}
     tot_ops, tot_ms = 0, 0.0
-    for name, N, K, pair in SHAPES[:4]:
+    layer_ops, layer_ms = 0, 0.0
+    shapes = SHAPES[:4] + [("attn_q|k|v", 2048, 1536, False)]
+    for name, N, K, pair in shapes:
         w = uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0xABC + N + K, N, K))
         w2 = uq.Weight(uq.KIND_Q8_0, K, N, uq.synth_quant(uq.KIND_Q8_0, 0xABD + N + K, N, K)) if pair else None
         ms = uq.time_prefill_gemm(w, w2, tokens, reps)
         ops = 2 * tokens * N * K * (2 if pair else 1)
-        out[name] = {"ms": round(ms, 4), "TOPS": round(ops / (ms / 1e3) / 1e12, 2)}
-        tot_ops += ops
-        tot_ms += ms
+        floor_us = 2 * tokens * N * (K // 32) * (2 if pair else 1) / VALU_LANE_OPS * 1e6
+        out[name] = {"ms": round(ms, 4), "TOPS": round(ops / (ms / 1e3) / 1e12, 2),
+                     "frac_of_int8_peak": round(ops / (ms / 1e3) / 1e12 / 5000.0, 4),
+                     "valu_floor_us": round(floor_us, 2), "frac_of_valu_floor": round(floor_us / (ms * 1e3), 3)}
+        if name != "attn_q|k|v":
+            tot_ops += ops
+            tot_ms += ms
+        if name != "attn_k/v":
+            # one layer of the model: q|k|v, o (the q/o shape), gate+up, down
+            layer_ops += ops
+            layer_ms += ms
         w.free()
         if w2:
             w2.free()
     out["aggregate_TOPS"] = round(tot_ops / (tot_ms / 1e3) / 1e12, 2)
+    out["model_layer_TOPS"] = round(layer_ops / (layer_ms / 1e3) / 1e12, 2)
+    out["model_layer_ms"] = round(layer_ms, 4)
     out["int8_mfma_peak_TOPS"] = 5000.0
     return out
 

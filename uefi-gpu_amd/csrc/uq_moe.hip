@@ -373,8 +373,18 @@ __global__ __launch_bounds__(GU_WG) void k_moe_gateup(MoeDev a, WArgs rg, WArgs 
         }
     };
     // route_par ends on a barrier that publishes L.p / L.sid and lxq / lxs,
-    // and leaves in `bad` the OR of every thread's non-finite flag
-    const float sum = route_par(a, lg, lg_hi, L, bad, quant_x);
+    // and leaves in `bad` the OR of every thread's non-finite flag. The
+    // shared expert's workgroups need no routing, only the quantized input:
+    // their own weight loads, issued first, would hold up their logits load
+    // and make them the launch's last workgroups (routing done at 4.6 us
+    // against 2.9 in the routed ones, in a stamped build).
+    float sum = 0.0f;
+    if (!shared) {
+        sum = route_par(a, lg, lg_hi, L, bad, quant_x);
+    } else {
+        if (t >= 64) quant_x();  // waves 1.. (quant_x's element index is t - 64)
+        __syncthreads();
+    }
     float v;
     if (!shared) {
         // routed expert: its weight loads go out before anything else waits

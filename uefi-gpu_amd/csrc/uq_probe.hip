@@ -3,6 +3,7 @@
 // calibration of the FETCH_SIZE / WRITE_SIZE counters), and matrix-core
 // throughput loops (the achievable int8 / fp16 / fp64 MFMA rates, int8 in
 // its 16x16x32, 32x32x32 and 16x16x64 forms).
+#include "uq_device.h"
 #include "uq_internal.h"
 #include "../../include/uq.h"
 
@@ -11,16 +12,22 @@
 namespace uq {
 namespace {
 
+// Each workgroup reads one contiguous chunk, its lanes on consecutive 16-byte
+// pieces with four non-temporal loads in flight per lane: the access form of
+// the lm_head matvec, so the rate is an achievable streaming-read ceiling.
 __global__ __launch_bounds__(256) void k_probe_read(const int4* __restrict__ src, int64_t n16, int* __restrict__ sink) {
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t b0 = (int64_t)blockIdx.x * per, b1 = b0 + per < n16 ? b0 + per : n16;
     int acc = 0;
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += 4 * stride) {
-        int4 v0 = src[i];
-        int4 v1 = i + stride < n16 ? src[i + stride] : make_int4(0, 0, 0, 0);
-        int4 v2 = i + 2 * stride < n16 ? src[i + 2 * stride] : make_int4(0, 0, 0, 0);
-        int4 v3 = i + 3 * stride < n16 ? src[i + 3 * stride] : make_int4(0, 0, 0, 0);
-        acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
-        acc ^= v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^ v3.w;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += 4 * 256) {
+        int4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int64_t j = i + 256 * u;
+            v[u] = uq_ntload16(src + (j < b1 ? j : b1 - 1));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     if (acc == 0x7fffffff) sink[blockIdx.x] = acc;  // keeps the loads live, never taken for zeroed memory
 }

@@ -27,10 +27,10 @@ import uq  # noqa: E402
 METRIC = "Q8_0 matvec HBM GB/s (% peak); bs=1 decode tok/s, Qwen2.5-1.5B shape"
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per lm_head launch (151936x1536 Q8_0), from rocprofv3 PMC passes
-# over this script: FETCH_SIZE 121,105.3 KiB x 2.0 + WRITE_SIZE 593.5 KiB x 1.0,
+# over this script: FETCH_SIZE 121,106.8 KiB x 1.99993 + WRITE_SIZE 593.5 KiB x 1.0,
 # factors from 1 GiB read/copy probe kernels in the same runs
 # (profiles/q8_matvec_lm_head_pmc.md).
-LM_HEAD_TRAFFIC_BYTES = 248_624_996
+LM_HEAD_TRAFFIC_BYTES = 248_626_178
 
 # (name, N rows, K, fused pair)
 SHAPES = [("attn_q/o", 1536, 1536, False), ("attn_k/v", 256, 1536, False),

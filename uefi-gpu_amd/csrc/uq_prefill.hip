@@ -95,14 +95,24 @@ constexpr int GBM = 32;                    // rows per workgroup tile
 // 32 x 64 grids leave SIMDs with one or two waves.
 template <int WM>
 constexpr int gemm_bn() { return WM == 2 ? 64 : 32; }
+// The stage's scales are one contiguous run, filled by whole-wave 16-byte
+// loads (one load per 256 floats, issued by waves 0 and 1): dw of the tile's
+// 32 rows per block (gate, then up for the pair), then dx of its tokens per
+// block. The narrow launches' stage time follows the count of load
+// instructions more than their bytes, and two 8-lane scale loads per wave
+// cost about as much as a full operand load.
 template <bool GU, int WM>
 struct GemmStageLds {
+    static constexpr int SW = 0, SW2 = GK_BLK * GBM, SX = GK_BLK * GBM * (GU ? 2 : 1);
+    static constexpr int NSC = SX + GK_BLK * gemm_bn<WM>();  // floats of scales
+    static constexpr int SC_LOADS = (NSC + 255) / 256;       // wave loads of them (<= 2)
     int8_t a[GBM * 128];
     int8_t a2[GU ? GBM * 128 : 16];
     int8_t b[gemm_bn<WM>() * 128];
-    float sw[GK_BLK * GBM];
-    float sw2[GU ? GK_BLK * GBM : 4];
-    float sx[GK_BLK * gemm_bn<WM>()];
+    float sc[NSC];
+    __device__ __forceinline__ const float* sw() const { return sc + SW; }
+    __device__ __forceinline__ const float* sw2() const { return sc + SW2; }
+    __device__ __forceinline__ const float* sx() const { return sc + SX; }
 };
 typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_load16(const void* g, void* lds_wave_base) { uq_lds_load16(g, lds_wave_base); }
@@ -112,14 +122,25 @@ __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 4)) &
 // Per-lane byte offsets of the stage loads from wave-uniform bases: each load
 // is a uniform 64-bit base (scalar registers, advanced once per stage by
 // scalar arithmetic) plus a 32-bit per-lane offset computed once, so the
-// loads take the scalar-base addressing form and a stage costs no per-lane
-// 64-bit address arithmetic. The offsets stay far below 2^32 (rows of the
-// tile times K <= 16384, or 16-byte scale chunks).
+// operand loads take the scalar-base addressing form and a stage costs no
+// per-lane 64-bit address arithmetic. The offsets stay far below 2^32 (rows
+// of the tile times K <= 16384, or scales of 4 blocks of rows n or tokens mp).
+// Scale float f = 256 * wave + 4 * lane of the stage's run: gate dw, up dw
+// (the pair) or dx, block f / 32 of the rows or f / BN of the tokens. Its
+// source is the gate-scale cursor plus a per-lane byte offset `so` (flat
+// addresses; the up and token scale planes are other allocations), which the
+// token-scale lanes move by `sstep` per stage: the gate cursor advances
+// 4 blocks of n floats, the token scales 4 blocks of mp. No per-lane pointer
+// select (a select among the cursors became a table in scratch memory).
 struct GemmSrc {
-    uint32_t a, b0, b1, sw, sx;
+    uint32_t a, b0, b1;
+    uint64_t so, sstep;
+    bool sload;
 };
 template <bool GU, int WM>
-__device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int wave, int lane) {
+__device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int64_t r0, int64_t t0, int wave, int lane) {
+    typedef GemmStageLds<GU, WM> St;
+    constexpr int BN = gemm_bn<WM>();
     const int K = (int)p.k;
     const int slot = lane & 7, row = 8 * wave + (lane >> 3);
     const int tk0 = 8 * WM * wave + (lane >> 3), tk1 = tk0 + 8;
@@ -127,8 +148,21 @@ __device__ __forceinline__ GemmSrc gemm_src(const PfGemmArgs& p, int wave, int l
     g.a = (uint32_t)(row * K + 16 * (slot ^ swz(row)));
     g.b0 = (uint32_t)(tk0 * K + 16 * (slot ^ swz(tk0)));
     g.b1 = (uint32_t)(tk1 * K + 16 * (slot ^ swz(tk1)));
-    g.sw = (uint32_t)(16 * (lane & 7));
-    g.sx = (uint32_t)(16 * (lane & 15));
+    const int f = 256 * wave + 4 * lane;
+    const uint64_t gate = (uint64_t)(p.w_ds + r0);
+    g.sload = wave < St::SC_LOADS && f < St::NSC;
+    g.so = 0;
+    g.sstep = 0;
+    if (f < St::SX) {
+        const bool up = GU && f >= St::SW2;
+        const int fw = up ? f - St::SW2 : f;
+        const uint64_t seg = up ? (uint64_t)(p.w2_ds + r0) : gate;
+        g.so = seg - gate + (uint64_t)(4 * ((fw / GBM) * p.n + fw % GBM));
+    } else {
+        const int fx = f - St::SX;
+        g.so = (uint64_t)(p.xst + t0) - gate + (uint64_t)(4 * ((fx / BN) * (int64_t)p.mp + fx % BN));
+        g.sstep = (uint64_t)(4 * GK_BLK * ((int64_t)p.mp - p.n));
+    }
     return g;
 }
 __device__ __forceinline__ const void* at(const void* base, uint32_t off) {
@@ -144,7 +178,6 @@ __device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g
     constexpr int BN = gemm_bn<WM>();
     const int slot = lane & 7;
     uint32_t oa = g.a, ob0 = g.b0, ob1 = g.b1;
-    int jw = wave;  // the scale block row this wave loads
     if (nblk < GK_BLK) {
         // chunk c = slot ^ swz(row) of block c/2; clamp the block, keep the half
         // (the shift is -32 * (blocks past the end) >= -(the chunk's own offset))
@@ -156,19 +189,29 @@ __device__ __forceinline__ void gemm_issue(const PfGemmArgs& p, const GemmSrc& g
         oa += shift(row);
         ob0 += shift(tk0);
         ob1 += shift(tk1);
-        jw = wave < nblk ? wave : nblk - 1;
     }
     const int64_t K = p.k, wa = r0 * K + kb * 32, wb = t0 * K + kb * 32;
     lds_load16(at(p.w_qs + wa, oa), S.a + wave * 1024);
     if (GU) lds_load16(at(p.w2_qs + wa, oa), S.a2 + wave * 1024);
     lds_load16(at(p.xq + wb, ob0), S.b + (WM * wave) * 1024);
     if (WM == 2) lds_load16(at(p.xq + wb, ob1), S.b + (2 * wave + 1) * 1024);
-    if (lane < GBM / 4) {
-        const int64_t ws = r0 + (kb + jw) * p.n;
-        lds_load16(at(p.w_ds + ws, g.sw), S.sw + wave * GBM);
-        if (GU) lds_load16(at(p.w2_ds + ws, g.sw), S.sw2 + wave * GBM);
+    typedef GemmStageLds<GU, WM> St;
+    if (wave < St::SC_LOADS) {
+        // the stage's scale run, blocks past the end clamped to the last one
+        const int f = 256 * wave + 4 * lane;
+        if (f < St::NSC) {
+            const float* src;
+            if (f < St::SX) {
+                const bool up = GU && f >= St::SW2;
+                const int fw = up ? f - St::SW2 : f, blk = fw / GBM < nblk ? fw / GBM : nblk - 1;
+                src = (up ? p.w2_ds : p.w_ds) + (kb + blk) * p.n + r0 + fw % GBM;
+            } else {
+                const int fx = f - St::SX, blk = fx / BN < nblk ? fx / BN : nblk - 1;
+                src = p.xst + (kb + blk) * (int64_t)p.mp + t0 + fx % BN;
+            }
+            lds_load16(src, S.sc + 256 * wave);
+        }
     }
-    if (lane < BN / 4) lds_load16(at(p.xst + t0 + (kb + jw) * (int64_t)p.mp, g.sx), S.sx + wave * BN);
 }
 
 
@@ -182,23 +225,17 @@ struct GemmCursor {
     const int8_t* a;
     const int8_t* a2;
     const int8_t* b;
-    const float* sw;
-    const float* sw2;
-    const float* sx;
-    __device__ __forceinline__ void advance(int64_t n, int mp) {
+    const float* sw;  // gate scales of the stage's first block (the scale loads' base)
+    __device__ __forceinline__ void advance(int64_t n) {
         a += GK_BLK * 32;
         b += GK_BLK * 32;
         sw += GK_BLK * n;
-        sx += GK_BLK * mp;
-        if (GU) {
-            a2 += GK_BLK * 32;
-            sw2 += GK_BLK * n;
-        }
+        if (GU) a2 += GK_BLK * 32;
     }
 };
 
 // The loads of the cursor's full stage (the same bytes gemm_issue loads for
-// a stage of four blocks; wave w loads scale block row w).
+// a stage of four blocks).
 template <bool GU, int WM>
 __device__ __forceinline__ void gemm_issue_full(const GemmCursor<GU>& c, const GemmSrc& g, GemmStageLds<GU, WM>& S,
                                                 int wave, int lane) {
@@ -207,11 +244,8 @@ __device__ __forceinline__ void gemm_issue_full(const GemmCursor<GU>& c, const G
     if (GU) lds_load16(at(c.a2, g.a), S.a2 + wave * 1024);
     lds_load16(at(c.b, g.b0), S.b + (WM * wave) * 1024);
     if (WM == 2) lds_load16(at(c.b, g.b1), S.b + (2 * wave + 1) * 1024);
-    if (lane < GBM / 4) {
-        lds_load16(at(c.sw, g.sw), S.sw + wave * GBM);
-        if (GU) lds_load16(at(c.sw2, g.sw), S.sw2 + wave * GBM);
-    }
-    if (lane < BN / 4) lds_load16(at(c.sx, g.sx), S.sx + wave * BN);
+    if (wave < GemmStageLds<GU, WM>::SC_LOADS && g.sload)
+        lds_load16((const void*)((uint64_t)c.sw + g.so), S.sc + 256 * wave);
 }
 
 // Wait until at most `n` vector-memory ops of this wave are outstanding
@@ -277,8 +311,8 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU, WM>& S, int j
         // product k = (gate k < 2 / up k >= 2) x (row tile k % 2)
         static_assert(NB == 1, "pair: one block per group");
         const int mk = (kq & 1) < WM ? (kq & 1) : 0;
-        const float bx = S.sx[j0 * BN + wc + li];
-        const float* sws = kq >= 2 ? S.sw2 : S.sw;
+        const float bx = S.sx()[j0 * BN + wc + li];
+        const float* sws = kq >= 2 ? S.sw2() : S.sw();
         const float ax = sws[j0 * GBM + rb + 16 * mk + li];
         v16f z16;
 #pragma unroll
@@ -294,11 +328,11 @@ __device__ __forceinline__ void gemm_blocks(const GemmStageLds<GU, WM>& S, int j
     } else {
         // one product per block of the group's 4, per row tile
         static_assert(NB == 4, "one outer-product MFMA per group and row tile");
-        const float bx = S.sx[(j0 + kq) * BN + wc + li];
+        const float bx = S.sx()[(j0 + kq) * BN + wc + li];
         v16f sc[WM];
 #pragma unroll
         for (int m = 0; m < WM; m++) {
-            const float ax = S.sw[(j0 + kq) * GBM + rb + 16 * m + li];
+            const float ax = S.sw()[(j0 + kq) * GBM + rb + 16 * m + li];
             v16f z16;
 #pragma unroll
             for (int r = 0; r < 16; r++) z16[r] = 0.0f;
@@ -323,7 +357,7 @@ __device__ __forceinline__ void gemm_block_tail(const GemmStageLds<GU, WM>& S, i
     const v4i z = {0, 0, 0, 0};
     const int gc = 2 * j + hi, tok = wc + li;
     const long bv = *(const long*)(S.b + tok * 128 + ((gc ^ swz(tok)) << 4) + sub);
-    const float x = S.sx[j * BN + wc + li];
+    const float x = S.sx()[j * BN + wc + li];
 #pragma unroll
     for (int m = 0; m < WM; m++) {
         const int row = rb + 16 * m + li;
@@ -331,9 +365,9 @@ __device__ __forceinline__ void gemm_block_tail(const GemmStageLds<GU, WM>& S, i
         const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(*(const long*)(S.a + off), bv, z, 0, 0, 0);
         v4i c2;
         if (GU) c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(*(const long*)(S.a2 + off), bv, z, 0, 0, 0);
-        const v4f w = *(const v4f*)(S.sw + j * GBM + rb + 16 * m + lm);
+        const v4f w = *(const v4f*)(S.sw() + j * GBM + rb + 16 * m + lm);
         v4f w2;
-        if (GU) w2 = *(const v4f*)(S.sw2 + j * GBM + rb + 16 * m + lm);
+        if (GU) w2 = *(const v4f*)(S.sw2() + j * GBM + rb + 16 * m + lm);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             f[m][q] = fmaf((float)c[q], w[q] * x, f[m][q]);
@@ -362,17 +396,16 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
     for (int m = 0; m < WM; m++)
 #pragma unroll
         for (int q = 0; q < 4; q++) f[m][q] = g[m][q] = 0.0f;
-    const GemmSrc src = gemm_src<GU, WM>(a, wave, lane);
-    GemmCursor<GU> cur{a.w_qs + r0 * a.k, GU ? a.w2_qs + r0 * a.k : nullptr, a.xq + t0 * a.k,
-                       a.w_ds + r0 + wave * a.n, GU ? a.w2_ds + r0 + wave * a.n : nullptr,
-                       a.xst + t0 + (int64_t)wave * a.mp};
+    GemmSrc src = gemm_src<GU, WM>(a, r0, t0, wave, lane);
+    GemmCursor<GU> cur{a.w_qs + r0 * a.k, GU ? a.w2_qs + r0 * a.k : nullptr, a.xq + t0 * a.k, a.w_ds + r0};
     // stage s's loads, issued in stage order: full stages from the cursor, a
     // partial last stage through the clamping issue
     auto issue = [&](int s) {
         GemmStageLds<GU, WM>& S = ring[s & (RG - 1)];
         if (s < nfull) {
             gemm_issue_full<GU, WM>(cur, src, S, wave, lane);
-            cur.advance(a.n, a.mp);
+            cur.advance(a.n);
+            src.so += src.sstep;
         } else {
             gemm_issue<GU, WM>(a, src, S, r0, t0, (int64_t)s * GK_BLK, nblk_of(s), wave, lane);
         }

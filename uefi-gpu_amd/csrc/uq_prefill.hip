@@ -39,17 +39,20 @@ __global__ __launch_bounds__(256) void k_transpose_scales(const uint16_t* __rest
 // One workgroup per token: x = embed(token) or x + residual (stored back),
 // RMSNorm, block-32 quant into xq[t][dim] and xsT[b][t].
 constexpr int PF_MAXD = 4096;  // model dim bound (uq_model_create: dim <= 4096, dim % 256 == 0)
-__global__ __launch_bounds__(256) void k_pf_norm(PfNormArgs a) {
-    __shared__ double part[4];
+// NC = dim / 256 chunks of 256 values, one per wave (float4 per lane, partial
+// sums of squares meeting in LDS): each wave issues only its chunk's loads
+// (instantiated per chunk count; a launch for the 4096 bound gave a 1536-wide
+// row 12 loads per wave, half of them clamped repeats).
+template <int NC>
+__global__ __launch_bounds__(64 * NC) void k_pf_norm(PfNormArgs a) {
+    __shared__ double part[NC];
     const int t = blockIdx.x;
     NormQuantArgs nq = a.nq;
     nq.x = a.x + (size_t)t * a.nq.dim;
     nq.residual = a.residual ? a.residual + (size_t)t * a.nq.dim : nullptr;
     nq.x_out = a.x + (size_t)t * a.nq.dim;
     if (a.tokens) nq.token = a.tokens + t;
-    // one token row per workgroup, spread over its four waves (256-value
-    // chunks, float4 per lane, partial sums of squares meeting in LDS)
-    NormQuantSplit<PF_MAXD / 256, 4> nw;
+    NormQuantSplit<NC, NC> nw;
     nw.issue(nq);
     nw.finish(nq, true, part, a.xq + (size_t)t * a.nq.dim, a.xst + t, a.mp);
 }
@@ -829,8 +832,16 @@ __global__ __launch_bounds__(256) void k_pf_attention(PfAttnArgs a) {
 void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float* dt, hipStream_t s) {
     hipLaunchKernelGGL(k_transpose_scales, dim3((unsigned)((rows * nb + 255) / 256)), dim3(256), 0, s, d, rows, nb, dt);
 }
+template <int NC>
+void pf_norm_nc(const PfNormArgs& a, int tokens, hipStream_t s) {
+    if constexpr (NC > 1) {
+        if (a.nq.dim / 256 < NC) return pf_norm_nc<NC - 1>(a, tokens, s);
+    }
+    hipLaunchKernelGGL(k_pf_norm<NC>, dim3(tokens), dim3(64 * NC), 0, s, a);
+}
 void launch_pf_norm(const PfNormArgs& a, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_norm, dim3(tokens), dim3(256), 0, s, a);
+    // dim % 256 == 0 and dim <= PF_MAXD (checked at model creation)
+    pf_norm_nc<PF_MAXD / 256>(a, tokens, s);
 }
 void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, float* xst, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_quant, dim3((unsigned)((k + 255) / 256), tokens), dim3(256), 0, s, x, k, mp, xq, xst);

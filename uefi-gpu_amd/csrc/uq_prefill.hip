@@ -513,57 +513,72 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(PfRopeArgs a) {
     const float* trig = a.trig + (size_t)pos * hd;
     uint16_t* kc = a.kcache + (size_t)pos * kvd;
     uint16_t* vc = a.vcache + (size_t)pos * kvd;
-    // items: q pairs, k pairs, v values; NI per thread per pass, every load of
-    // a pass issued before any arithmetic (indices clamped, a missing bias read
-    // from the RoPE row instead and not used)
-    constexpr int NI = 5;
-    const int nr = qpairs + kpairs, n = nr + kvd;
+    // items: groups of 4 consecutive q pairs (j..j+3 with their partners
+    // j+half..), of 4 k pairs, of 4 v values (head_dim % 64 == 0, so a group
+    // stays inside one half of a head); NI per thread per pass, every float4
+    // load of a pass issued before any arithmetic (indices clamped, a missing
+    // bias read from the RoPE row instead and not used). Six 16-byte loads per
+    // group where one scalar item took six 4-byte loads.
+    constexpr int NI = 2;
+    const int qg = qpairs / 4, ng = (qpairs + kpairs) / 4, n = ng + kvd / 4;
     for (int i0 = threadIdx.x; i0 < n; i0 += 256 * NI) {
-        float x0[NI], x1[NI], b0[NI], b1[NI], c0[NI], c1[NI];
+        float4 x0[NI], x1[NI], b0[NI], b1[NI], c0[NI], c1[NI];
 #pragma unroll
         for (int u = 0; u < NI; u++) {
             const int i = i0 + 256 * u, ic = i < n ? i : n - 1;
-            const bool rope = ic < nr, isq = ic < qpairs;
-            const int p = isq ? ic : ic - qpairs;
+            const bool rope = ic < ng, isq = ic < qg;
+            const int p = 4 * (isq ? ic : ic - qg);
             const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
-            const int e = ic - nr;
+            const int e = 4 * (ic - ng);
             const float* base = isq ? q : k;
             const float* bias = isq ? a.bq : a.bk;
             const float* pa = rope ? base + ia : v + e;
             const float* pb = rope ? base + ib : v + e;
             const float* bsel = rope ? bias : a.bv;
             const int bi0 = rope ? ia : e, bi1 = rope ? ib : e;
-            x0[u] = *pa;
-            x1[u] = *pb;
-            b0[u] = *(bsel ? bsel + bi0 : trig);
-            b1[u] = *(bsel ? bsel + bi1 : trig);
-            c0[u] = trig[rope ? j : 0];
-            c1[u] = trig[rope ? half + j : 0];
+            x0[u] = *(const float4*)pa;
+            x1[u] = *(const float4*)pb;
+            b0[u] = *(const float4*)(bsel ? bsel + bi0 : trig);
+            b1[u] = *(const float4*)(bsel ? bsel + bi1 : trig);
+            c0[u] = *(const float4*)(trig + (rope ? j : 0));
+            c1[u] = *(const float4*)(trig + (rope ? half + j : 0));
         }
 #pragma unroll
         for (int u = 0; u < NI; u++) {
             const int i = i0 + 256 * u;
             if (i >= n) break;
-            if (i < nr) {
-                const bool isq = i < qpairs;
-                const int p = isq ? i : i - qpairs;
+            const float xa[4] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w}, xb[4] = {x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+            const float ba[4] = {b0[u].x, b0[u].y, b0[u].z, b0[u].w}, bb[4] = {b1[u].x, b1[u].y, b1[u].z, b1[u].w};
+            const float ca[4] = {c0[u].x, c0[u].y, c0[u].z, c0[u].w}, cb[4] = {c1[u].x, c1[u].y, c1[u].z, c1[u].w};
+            if (i < ng) {
+                const bool isq = i < qg;
+                const int p = 4 * (isq ? i : i - qg);
                 const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
                 const bool hb = isq ? a.bq != nullptr : a.bk != nullptr;
-                const float uu = hb ? x0[u] + b0[u] : x0[u];
-                const float ww = hb ? x1[u] + b1[u] : x1[u];
-                const float p0 = uu * c0[u], p1 = ww * c1[u], p2 = uu * c1[u], p3 = ww * c0[u];
-                const float ra = p0 - p1, rb = p2 + p3;
+                float ra[4], rb[4];
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const float uu = hb ? xa[m] + ba[m] : xa[m];
+                    const float ww = hb ? xb[m] + bb[m] : xb[m];
+                    const float p0 = uu * ca[m], p1 = ww * cb[m], p2 = uu * cb[m], p3 = ww * ca[m];
+                    ra[m] = p0 - p1;
+                    rb[m] = p2 + p3;
+                }
                 if (isq) {
-                    q[ia] = ra;
-                    q[ib] = rb;
+                    *(float4*)(q + ia) = make_float4(ra[0], ra[1], ra[2], ra[3]);
+                    *(float4*)(q + ib) = make_float4(rb[0], rb[1], rb[2], rb[3]);
                 } else {
-                    kc[ia] = uq_f16_rne(ra);
-                    kc[ib] = uq_f16_rne(rb);
+                    *(uint2*)(kc + ia) = make_uint2(uq_f16_rne(ra[0]) | (uint32_t)uq_f16_rne(ra[1]) << 16,
+                                                    uq_f16_rne(ra[2]) | (uint32_t)uq_f16_rne(ra[3]) << 16);
+                    *(uint2*)(kc + ib) = make_uint2(uq_f16_rne(rb[0]) | (uint32_t)uq_f16_rne(rb[1]) << 16,
+                                                    uq_f16_rne(rb[2]) | (uint32_t)uq_f16_rne(rb[3]) << 16);
                 }
             } else {
-                const int e = i - nr;
-                const float vb = a.bv ? x0[u] + b0[u] : x0[u];
-                vc[e] = uq_f16_rne(vb);
+                const int e = 4 * (i - ng);
+                uint16_t hv[4];
+#pragma unroll
+                for (int m = 0; m < 4; m++) hv[m] = uq_f16_rne(a.bv ? xa[m] + ba[m] : xa[m]);
+                *(uint2*)(vc + e) = make_uint2(hv[0] | (uint32_t)hv[1] << 16, hv[2] | (uint32_t)hv[3] << 16);
             }
         }
     }

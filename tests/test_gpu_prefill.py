@@ -29,13 +29,16 @@ def quant_rows(X):
 
 # (4096, 1536, 512) and (4096, 1568, 512) run the 32 x 64 workgroup tiles;
 # the others give grids of under four workgroups per CU and run the 32 x 32
-# tiles. A stage holds 4 blocks (K 128): K 160 is one full stage and a partial
-# one, 384 an odd count of full stages (the last one after the paired loop),
-# 416 three full stages and a partial one, 1568 twelve and a partial one on
-# the wide tiles.
+# tiles (1536 and 2048 rows at 450-512 tokens: the model's o, down and fused
+# q,k,v shapes). A stage holds 4 blocks (K 128): K 160 is one full stage and
+# a partial one, 384 an odd count of full stages (the last one after the
+# paired loop), 416 three full stages and a partial one, 1568 twelve and a
+# partial one.
 @pytest.mark.parametrize("N,K,T", [(1536, 1536, 512), (256, 1536, 77), (8960, 1536, 64), (1536, 8960, 40),
                                    (64, 32, 1), (128, 64, 130), (4096, 1536, 512),
-                                   (64, 160, 33), (128, 384, 70), (64, 416, 64), (4096, 1568, 512)])
+                                   (64, 160, 33), (128, 384, 70), (64, 416, 64), (4096, 1568, 512),
+                                   (1536, 1568, 512), (1536, 384, 500), (2048, 1536, 512), (2048, 416, 512),
+                                   (2048, 160, 450)])
 def test_prefill_gemm_bit_exact(gpu, N, K, T):
     raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED0003 + N, N, K)
     X = np.stack([uq.synth_normal(0x5EED0003 + t, K) for t in range(T)])
@@ -50,9 +53,9 @@ def test_prefill_gemm_bit_exact(gpu, N, K, T):
 # 2e-37, dw ~ 1e-2), zero, or large (x ~ 1e25), beside ordinary rows; the
 # scale product must be the f32 multiply with denormals kept on both the
 # outer-product MFMA path (full stages) and the VALU path (partial stage).
-@pytest.mark.parametrize("K", [1536, 416, 96])
-def test_prefill_gemm_extreme_scales(gpu, K):
-    N, T = 128, 64
+@pytest.mark.parametrize("N,K,T", [(128, 1536, 64), (128, 416, 64), (128, 96, 64), (1536, 1536, 512),
+                                   (2048, 416, 512)])
+def test_prefill_gemm_extreme_scales(gpu, N, K, T):
     raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED00E0 + K, N, K)
     mags = [1.0, 1e-35, 0.0, 1e25, 3e-33, 1e-36, 1e20, 1e-30]
     X = np.stack([uq.synth_normal(0x5EED00E1 + t, K) * np.float32(mags[t % len(mags)]) for t in range(T)])
@@ -66,31 +69,32 @@ def test_prefill_gemm_extreme_scales(gpu, K):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), ulps(y, ref).max()
 
 
-@pytest.mark.parametrize("blocks", [3, 4])
-def test_prefill_gemm_sequential_fmaf_known_answer(gpu, blocks):
+@pytest.mark.parametrize("blocks,N,T", [(3, 64, 2), (4, 64, 2), (3, 1536, 512), (8, 2048, 512)])
+def test_prefill_gemm_sequential_fmaf_known_answer(gpu, blocks, N, T):
     """Row 0 of the weight and token 0 give per-block terms 2^24, 1 + 2^-25,
     1 (then 0): the reference's in-order fmaf chain (gpu_prefill.cu:29-30)
     rounds to 16777220, a multiply-then-add chain to 16777216 and the reversed
     block order or the exact sum to 16777218. K 96 runs the partial-stage path,
-    K 128 one full stage."""
-    K, N = 32 * blocks, 64
+    K 128 one full stage; N 1536 / 2048 at 512 tokens the model's launch
+    shapes."""
+    K = 32 * blocks
     raw = uq.synth_quant(uq.KIND_Q8_0, 0x5EED00E2, N, K).copy()
     rb = K // 32 * 34
     row = np.zeros((blocks, 34), np.uint8)
     row[:, 0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
     row[0, 2], row[1, 2], row[2, 2] = 1, 3, 1
     raw[:rb] = row.reshape(-1)
-    qx = np.zeros((2, K), np.int8)
+    qx = np.zeros((T, K), np.int8)
+    xs = np.ones((T, blocks), np.float32)
     qx[0, [0, 32, 64]] = 1
-    qx[1] = O.quant_act(uq.synth_normal(0x5EED00E3, K))[0]
-    xs = np.ones((2, blocks), np.float32)
     xs[0, 0] = 2.0 ** 24
     xs[0, 1] = np.uint32(0x3EAAAAAB).view(np.float32)
-    xs[1] = O.quant_act(uq.synth_normal(0x5EED00E3, K))[1]
+    for t in range(1, T):
+        qx[t], xs[t] = O.quant_act(uq.synth_normal(0x5EED00E3 + t, K))
     w = uq.Weight(uq.KIND_Q8_0, K, N, raw)
     y = uq.prefill_gemm(w, qx, xs)
     assert y[0, 0] == np.float32(16777220.0)
-    ref = O.prefill_gemm(raw, K, N, xs, qx, 2)
+    ref = O.prefill_gemm(raw, K, N, xs, qx, T)
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), ulps(y, ref).max()
 
 

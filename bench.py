@@ -155,7 +155,7 @@ def decode_bench(prompt_len=512, steps=128, keep=None):
     512-token prompt of seeded uniform ids through the int8-MFMA prefill, then
     `steps` decode steps (one hipGraph launch each, greedy id fed back on the
     device) timed with HIP events. Prefill is timed on the host clock around
-    the synchronous call. `keep` (a dict) receives what the CPU decode
+    the synchronous call (4 warm-up calls, then the minimum and median of 5). `keep` (a dict) receives what the CPU decode
     baseline needs: the tensors, the prompt's KV cache and the ids."""
     cfg = dict(uq.QWEN25_15B, max_seq=1024)
     t0 = time.perf_counter()
@@ -163,9 +163,12 @@ def decode_bench(prompt_len=512, steps=128, keep=None):
     model = uq.Qwen2Model(cfg, tensors)
     t_load = time.perf_counter() - t0
     prompt = uq.synth_tokens(0x5EED0002, prompt_len, cfg["vocab"])
-    model.prefill(prompt)                             # warm-up
+    # warm-up: after the idle model upload the first prefills run while the
+    # clocks ramp (4.95, 4.77, 4.63, 4.53 ms by HIP events on consecutive calls)
+    for _ in range(4):
+        model.prefill(prompt)
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         first = model.prefill(prompt)
         times.append(time.perf_counter() - t0)
@@ -182,6 +185,7 @@ def decode_bench(prompt_len=512, steps=128, keep=None):
             "steps": steps, "weight_bytes_per_token": weight_bytes,
             "effective_GBs": round((weight_bytes * steps + kv_bytes) / (ms / 1e3) / 1e9, 1),
             "prefill_tok_s": round(prompt_len / t_prefill, 1), "prefill_ms": round(t_prefill * 1e3, 3),
+            "prefill_ms_median": round(sorted(times)[len(times) // 2] * 1e3, 3),
             "model_upload_s": round(t_load, 1), "first_ids": [int(first)] + [int(i) for i in ids[:7]]}
 
 

@@ -13,6 +13,10 @@ struct LayerDev {
     Weight qkv;  // q|k|v rows of one layer in one Q8_0 weight
     // fp16 weight scales transposed to [k/32][rows] for the prefill GEMM
     float *qkv_dt = nullptr, *o_dt = nullptr, *g_dt = nullptr, *u_dt = nullptr, *d_dt = nullptr;
+    // the prefill's q|k|v copy with the RoPE partners adjacent (PfRopeEpi):
+    // int8 rows, and the permuted q|k|v bias; qkv_dt is in the same row order
+    int8_t* qkv_pq = nullptr;
+    float* qkv_pb = nullptr;
 };
 
 struct Model {

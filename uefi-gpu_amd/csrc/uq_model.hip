@@ -329,9 +329,40 @@ int Model::build_prefill() {
         launch_transpose_scales(w.d, w.m, w.n / 32, *dt, stream);
         return OK;
     };
+    // q|k|v row order of the prefill copy: within each q and k head, row 2j + e
+    // = output j + e * hd/2 (the RoPE pair adjacent); v unchanged
+    std::vector<int> perm((size_t)nqkv);
+    const int hd = c.head_dim, half = hd / 2;
+    for (int r = 0; r < nqkv; r++) {
+        if (r < c.dim + kvd) {
+            const int base = r < c.dim ? 0 : c.dim, w = r - base;
+            perm[r] = base + (w / hd) * hd + (w % hd) / 2 + (w % 2) * half;
+        } else {
+            perm[r] = r;
+        }
+    }
+    int* dperm = nullptr;
+    if (int rc = alloc(&dperm, (size_t)nqkv)) return rc;
+    UQ_CHECK_HIP(hipMemcpyAsync(dperm, perm.data(), 4 * (size_t)nqkv, hipMemcpyHostToDevice, stream));
+    float *dt_tmp = nullptr, *bias_tmp = nullptr;
+    if (int rc = alloc(&dt_tmp, (size_t)nqkv * (c.dim / 32))) return rc;
+    if (int rc = alloc(&bias_tmp, (size_t)nqkv)) return rc;
     for (int l = 0; l < c.layers; l++) {
         LayerDev& L = layers[l];
-        if (int rc = tr(L.qkv, &L.qkv_dt)) return rc;
+        launch_transpose_scales(L.qkv.d, L.qkv.m, L.qkv.n / 32, dt_tmp, stream);
+        if (int rc = alloc(&L.qkv_dt, (size_t)nqkv * (c.dim / 32))) return rc;
+        launch_gather_cols(dt_tmp, c.dim / 32, nqkv, dperm, L.qkv_dt, stream);
+        if (int rc = alloc(&L.qkv_pq, (size_t)nqkv * c.dim)) return rc;
+        launch_gather_rows(L.qkv.qs, c.dim, dperm, nqkv, L.qkv_pq, stream);
+        const char* bn[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+        const int boff[3] = {0, c.dim, c.dim + kvd}, blen[3] = {c.dim, kvd, kvd};
+        for (int i = 0; i < 3; i++) {
+            const float* b = vec(lname(l, bn[i]));
+            if (b) UQ_CHECK_HIP(hipMemcpyAsync(bias_tmp + boff[i], b, 4 * (size_t)blen[i], hipMemcpyDeviceToDevice, stream));
+            else UQ_CHECK_HIP(hipMemsetAsync(bias_tmp + boff[i], 0, 4 * (size_t)blen[i], stream));
+        }
+        if (int rc = alloc(&L.qkv_pb, (size_t)nqkv)) return rc;
+        launch_gather_cols(bias_tmp, 1, nqkv, dperm, L.qkv_pb, stream);
         if (int rc = tr(*weight(lname(l, "attn_output.weight")), &L.o_dt)) return rc;
         if (int rc = tr(*weight(lname(l, "ffn_gate.weight")), &L.g_dt)) return rc;
         if (int rc = tr(*weight(lname(l, "ffn_up.weight")), &L.u_dt)) return rc;
@@ -387,10 +418,15 @@ int Model::prefill(const uint32_t* tokens, int n, uint32_t* next) {
     for (int l = 0; l < c.layers; l++) {
         const LayerDev& L = layers[l];
         norm(l, vec(lname(l, "attn_norm.weight")), l == 0);
-        if (gemm(L.qkv, L.qkv_dt, nullptr, nullptr, PY)) return fail(ERR_SHAPE, "prefill: q|k|v rows not a multiple of 64");
-        PfRopeArgs ra{PY, nqkv, vec(lname(l, "attn_q.bias")), vec(lname(l, "attn_k.bias")), vec(lname(l, "attn_v.bias")),
-                      trig, kcache + l * kvl, vcache + l * kvl, 0, c.heads, c.kv_heads, c.head_dim};
-        launch_pf_rope_kv(ra, n, s);
+        {
+            // q|k|v GEMM on the permuted copy with the bias + RoPE + KV epilogue
+            PfGemmArgs ga{L.qkv_pq, L.qkv_dt, nullptr, nullptr, PXQ, PXST, PY, L.qkv.m, L.qkv.n, mp, nullptr, nullptr};
+            ga.rope = 1;
+            ga.re = PfRopeEpi{PY, nqkv, L.qkv_pb, vec(lname(l, "attn_q.bias")) != nullptr,
+                              vec(lname(l, "attn_k.bias")) != nullptr, vec(lname(l, "attn_v.bias")) != nullptr, trig,
+                              kcache + l * kvl, vcache + l * kvl, n, 0, c.heads, c.kv_heads, c.head_dim};
+            if (launch_pf_gemm(ga, s)) return fail(ERR_SHAPE, "prefill: q|k|v rows not a multiple of 64");
+        }
         // head_dim 128: the attention epilogue quantizes its output for the o GEMM
         const bool fused_quant = c.head_dim == 128;
         PfAttnArgs aa{PY, nqkv, kcache + l * kvl, vcache + l * kvl, PATT, n, 0, c.max_seq, c.heads, c.kv_heads, c.head_dim,

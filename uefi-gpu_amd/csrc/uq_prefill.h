@@ -19,6 +19,24 @@ struct PfNormArgs {
     int mp;
 };
 
+// The q|k|v GEMM's bias + RoPE + KV epilogue (prefill_rope, gpu_prefill.cu:
+// 73-81, fused into the GEMM): the weight's rows are permuted so that within
+// every q and k head row 2j + e holds the head's output j + e * head_dim/2
+// (the RoPE partners adjacent: a lane's 4 consecutive rows are two pairs);
+// v rows keep their order. The bias is permuted likewise (a region without a
+// bias adds nothing). q is written rotated to q[t][...] in the original order,
+// k and v rounded to fp16 into the caches at position p0 + t, for t < n.
+struct PfRopeEpi {
+    float* q;                // rows [mp][stride]; their q part is written
+    int stride;
+    const float* bias;       // permuted q|k|v bias (one float per row)
+    int hb_q, hb_k, hb_v;    // which regions have a bias
+    const float* trig;       // RoPE table [position][head_dim]: cos | sin
+    uint16_t* kcache;        // this layer
+    uint16_t* vcache;
+    int n, p0, heads, kv_heads, head_dim;
+};
+
 struct PfGemmArgs {
     const int8_t* w_qs;      // [n][k]
     const float* w_ds;       // weight scales widened to f32, transposed [k/32][n]
@@ -33,16 +51,9 @@ struct PfGemmArgs {
     // [mp][n] and scales [n/32][mp] (the next GEMM's input planes), or null
     int8_t* yq;
     float* yst;
-};
-
-struct PfRopeArgs {
-    float* qkv;              // rows [n][stride]: q | k | v
-    int stride;
-    const float *bq, *bk, *bv;
-    const float* trig;
-    uint16_t* kcache;        // this layer
-    uint16_t* vcache;
-    int p0, heads, kv_heads, head_dim;
+    // the q|k|v launch only (rows permuted as PfRopeEpi says), instead of y
+    int rope;
+    PfRopeEpi re;
 };
 
 struct PfAttnArgs {
@@ -66,7 +77,10 @@ void launch_transpose_scales(const uint16_t* d, int64_t rows, int64_t nb, float*
 void launch_pf_norm(const PfNormArgs& a, int tokens, hipStream_t s);
 void launch_pf_quant(const float* x, int64_t k, int tokens, int mp, int8_t* xq, float* xst, hipStream_t s);
 int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s);
-void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s);
+// dst row r = src row perm[r] (rows of rowb bytes, rowb % 16 == 0), and the
+// same gather on the columns of a [nb][m] float plane
+void launch_gather_rows(const int8_t* src, int64_t rowb, const int* perm, int64_t m, int8_t* dst, hipStream_t s);
+void launch_gather_cols(const float* src, int64_t nb, int64_t m, const int* perm, float* dst, hipStream_t s);
 int launch_pf_attention(const PfAttnArgs& a, hipStream_t s);
 
 }  // namespace uq

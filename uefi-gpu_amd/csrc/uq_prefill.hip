@@ -379,6 +379,52 @@ __device__ __forceinline__ void gemm_block_tail(const GemmStageLds<GU, WM>& S, i
     }
 }
 
+// The q|k|v launch's epilogue (PfRopeEpi): a lane's 4 consecutive permuted
+// rows r..r+3 of token t are two RoPE pairs (outputs j, j + hd/2 and j + 1,
+// j + 1 + hd/2 of one head) or 4 v values. Per pair, as prefill_rope
+// (gpu_prefill.cu:73-81): u = x + bias, w = x' + bias', then u*cos - w*sin and
+// u*sin + w*cos with each product rounded, q kept f32, k and v rounded to fp16.
+__device__ __forceinline__ void rope_store(const PfRopeEpi& e, int64_t t, int r, const float (&v)[4]) {
+    if (t >= e.n) return;  // padding tokens: no cache row past the prompt is written
+    const int hd = e.head_dim, half = hd / 2, dim = e.heads * hd, kvd = e.kv_heads * hd;
+    const int pos = e.p0 + (int)t;
+    const float4 b4 = *(const float4*)(e.bias + r);
+    const float bx[4] = {b4.x, b4.y, b4.z, b4.w};
+    if (r < dim + kvd) {
+        const bool isq = r < dim, hb = isq ? e.hb_q != 0 : e.hb_k != 0;
+        const int w0 = isq ? r : r - dim, h = w0 / hd, j = (w0 % hd) / 2;
+        const float* tr = e.trig + (size_t)pos * hd;
+        const float2 cc = *(const float2*)(tr + j), ss = *(const float2*)(tr + half + j);
+        const float c0[2] = {cc.x, cc.y}, c1[2] = {ss.x, ss.y};
+        float ra[2], rb[2];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const float uu = hb ? v[2 * p] + bx[2 * p] : v[2 * p];
+            const float ww = hb ? v[2 * p + 1] + bx[2 * p + 1] : v[2 * p + 1];
+            const float p0 = uu * c0[p], p1 = ww * c1[p], p2 = uu * c1[p], p3 = ww * c0[p];
+            ra[p] = p0 - p1;
+            rb[p] = p2 + p3;
+        }
+        const int ia = h * hd + j, ib = ia + half;
+        if (isq) {
+            float* qr = e.q + t * e.stride;
+            *(float2*)(qr + ia) = make_float2(ra[0], ra[1]);
+            *(float2*)(qr + ib) = make_float2(rb[0], rb[1]);
+        } else {
+            uint16_t* kr = e.kcache + (size_t)pos * kvd;
+            *(uint32_t*)(kr + ia) = uq_f16_rne(ra[0]) | (uint32_t)uq_f16_rne(ra[1]) << 16;
+            *(uint32_t*)(kr + ib) = uq_f16_rne(rb[0]) | (uint32_t)uq_f16_rne(rb[1]) << 16;
+        }
+    } else {
+        const int e0 = r - dim - kvd;
+        uint16_t hv[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) hv[m] = uq_f16_rne(e.hb_v ? v[m] + bx[m] : v[m]);
+        *(uint2*)(e.vcache + (size_t)pos * kvd + e0) =
+            make_uint2(hv[0] | (uint32_t)hv[1] << 16, hv[2] | (uint32_t)hv[3] << 16);
+    }
+}
+
 template <bool GU, int WM>
 __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
     // ring stages: the gate/up pair and the wide tiles fill two, one ahead
@@ -488,6 +534,10 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
 #pragma unroll
     for (int m = 0; m < WM; m++) {
         const int64_t t = t0 + wc + li, r = r0 + rb + 16 * m + lm;
+        if (!GU && a.rope) {
+            rope_store(a.re, t, (int)r, f[m]);
+            continue;
+        }
         float4 o;
         if (GU) {
             o = make_float4(uq_silu_mul(f[m][0], g[m][0]), uq_silu_mul(f[m][1], g[m][1]),
@@ -499,89 +549,23 @@ __global__ __launch_bounds__(256) void k_pf_gemm(PfGemmArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ RoPE + KV
-// One workgroup per token: q/k bias + RoPE (q in place), k and v rounded to
-// fp16 into the cache at position p0 + t (prefill_rope, gpu_prefill.cu:73-81).
-__global__ __launch_bounds__(256) void k_pf_rope_kv(PfRopeArgs a) {
-    const int t = blockIdx.x, pos = a.p0 + t;
-    const int hd = a.head_dim, half = hd / 2, kvd = a.kv_heads * hd;
-    const int qpairs = a.heads * half, kpairs = a.kv_heads * half;
-    float* row = a.qkv + (size_t)t * a.stride;
-    float* q = row;
-    const float* k = row + a.heads * hd;
-    const float* v = k + kvd;
-    const float* trig = a.trig + (size_t)pos * hd;
-    uint16_t* kc = a.kcache + (size_t)pos * kvd;
-    uint16_t* vc = a.vcache + (size_t)pos * kvd;
-    // items: groups of 4 consecutive q pairs (j..j+3 with their partners
-    // j+half..), of 4 k pairs, of 4 v values (head_dim % 64 == 0, so a group
-    // stays inside one half of a head); NI per thread per pass, every float4
-    // load of a pass issued before any arithmetic (indices clamped, a missing
-    // bias read from the RoPE row instead and not used). Six 16-byte loads per
-    // group where one scalar item took six 4-byte loads.
-    constexpr int NI = 2;
-    const int qg = qpairs / 4, ng = (qpairs + kpairs) / 4, n = ng + kvd / 4;
-    for (int i0 = threadIdx.x; i0 < n; i0 += 256 * NI) {
-        float4 x0[NI], x1[NI], b0[NI], b1[NI], c0[NI], c1[NI];
-#pragma unroll
-        for (int u = 0; u < NI; u++) {
-            const int i = i0 + 256 * u, ic = i < n ? i : n - 1;
-            const bool rope = ic < ng, isq = ic < qg;
-            const int p = 4 * (isq ? ic : ic - qg);
-            const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
-            const int e = 4 * (ic - ng);
-            const float* base = isq ? q : k;
-            const float* bias = isq ? a.bq : a.bk;
-            const float* pa = rope ? base + ia : v + e;
-            const float* pb = rope ? base + ib : v + e;
-            const float* bsel = rope ? bias : a.bv;
-            const int bi0 = rope ? ia : e, bi1 = rope ? ib : e;
-            x0[u] = *(const float4*)pa;
-            x1[u] = *(const float4*)pb;
-            b0[u] = *(const float4*)(bsel ? bsel + bi0 : trig);
-            b1[u] = *(const float4*)(bsel ? bsel + bi1 : trig);
-            c0[u] = *(const float4*)(trig + (rope ? j : 0));
-            c1[u] = *(const float4*)(trig + (rope ? half + j : 0));
-        }
-#pragma unroll
-        for (int u = 0; u < NI; u++) {
-            const int i = i0 + 256 * u;
-            if (i >= n) break;
-            const float xa[4] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w}, xb[4] = {x1[u].x, x1[u].y, x1[u].z, x1[u].w};
-            const float ba[4] = {b0[u].x, b0[u].y, b0[u].z, b0[u].w}, bb[4] = {b1[u].x, b1[u].y, b1[u].z, b1[u].w};
-            const float ca[4] = {c0[u].x, c0[u].y, c0[u].z, c0[u].w}, cb[4] = {c1[u].x, c1[u].y, c1[u].z, c1[u].w};
-            if (i < ng) {
-                const bool isq = i < qg;
-                const int p = 4 * (isq ? i : i - qg);
-                const int h = p / half, j = p % half, ia = h * hd + j, ib = ia + half;
-                const bool hb = isq ? a.bq != nullptr : a.bk != nullptr;
-                float ra[4], rb[4];
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const float uu = hb ? xa[m] + ba[m] : xa[m];
-                    const float ww = hb ? xb[m] + bb[m] : xb[m];
-                    const float p0 = uu * ca[m], p1 = ww * cb[m], p2 = uu * cb[m], p3 = ww * ca[m];
-                    ra[m] = p0 - p1;
-                    rb[m] = p2 + p3;
-                }
-                if (isq) {
-                    *(float4*)(q + ia) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-                    *(float4*)(q + ib) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-                } else {
-                    *(uint2*)(kc + ia) = make_uint2(uq_f16_rne(ra[0]) | (uint32_t)uq_f16_rne(ra[1]) << 16,
-                                                    uq_f16_rne(ra[2]) | (uint32_t)uq_f16_rne(ra[3]) << 16);
-                    *(uint2*)(kc + ib) = make_uint2(uq_f16_rne(rb[0]) | (uint32_t)uq_f16_rne(rb[1]) << 16,
-                                                    uq_f16_rne(rb[2]) | (uint32_t)uq_f16_rne(rb[3]) << 16);
-                }
-            } else {
-                const int e = 4 * (i - ng);
-                uint16_t hv[4];
-#pragma unroll
-                for (int m = 0; m < 4; m++) hv[m] = uq_f16_rne(a.bv ? xa[m] + ba[m] : xa[m]);
-                *(uint2*)(vc + e) = make_uint2(hv[0] | (uint32_t)hv[1] << 16, hv[2] | (uint32_t)hv[3] << 16);
-            }
-        }
-    }
+// ------------------------------------------------------------------ row gathers
+// The prefill copy of the q|k|v weight with the RoPE partners adjacent
+// (PfRopeEpi): dst row r = src row perm[r], 16 bytes per thread.
+__global__ __launch_bounds__(256) void k_gather_rows(const int8_t* __restrict__ src, int64_t rowb,
+                                                     const int* __restrict__ perm, int64_t m, int8_t* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, per = rowb / 16;
+    if (i >= m * per) return;
+    const int64_t r = i / per, c = i % per;
+    ((int4*)(dst + r * rowb))[c] = ((const int4*)(src + (int64_t)perm[r] * rowb))[c];
+}
+// dst[b][r] = src[b][perm[r]] on [nb][m] planes (the transposed scales, the bias)
+__global__ __launch_bounds__(256) void k_gather_cols(const float* __restrict__ src, int64_t nb, int64_t m,
+                                                     const int* __restrict__ perm, float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nb * m) return;
+    const int64_t b = i / m, r = i % m;
+    dst[i] = src[b * m + perm[r]];
 }
 
 // ------------------------------------------------------------------ causal attention
@@ -879,8 +863,12 @@ int launch_pf_gemm(const PfGemmArgs& a, hipStream_t s) {
     }
     return 0;
 }
-void launch_pf_rope_kv(const PfRopeArgs& a, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_rope_kv, dim3(tokens), dim3(256), 0, s, a);
+void launch_gather_rows(const int8_t* src, int64_t rowb, const int* perm, int64_t m, int8_t* dst, hipStream_t s) {
+    const int64_t n = m * (rowb / 16);
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, rowb, perm, m, dst);
+}
+void launch_gather_cols(const float* src, int64_t nb, int64_t m, const int* perm, float* dst, hipStream_t s) {
+    hipLaunchKernelGGL(k_gather_cols, dim3((unsigned)((nb * m + 255) / 256)), dim3(256), 0, s, src, nb, m, perm, dst);
 }
 int launch_pf_attention(const PfAttnArgs& a0, hipStream_t s) {
     PfAttnArgs a = a0;

@@ -300,9 +300,11 @@ class Model:
         for i in range(L):
             g = lambda s: tensors["blk.%d.%s" % (i, s)]
             ly = self.layers[i]
-            for f, nm in (("attn_norm", "attn_norm.weight"), ("ffn_norm", "ffn_norm.weight"),
-                          ("bq", "attn_q.bias"), ("bk", "attn_k.bias"), ("bv", "attn_v.bias")):
+            for f, nm in (("attn_norm", "attn_norm.weight"), ("ffn_norm", "ffn_norm.weight")):
                 setattr(ly, f, p(g(nm), _f32p))
+            for f, nm in (("bq", "attn_q.bias"), ("bk", "attn_k.bias"), ("bv", "attn_v.bias")):
+                b = tensors.get("blk.%d.%s" % (i, nm))  # a model may carry no bias (NULL)
+                setattr(ly, f, None if b is None else p(b, _f32p))
             for f, nm in (("wq", "attn_q.weight"), ("wk", "attn_k.weight"), ("wv", "attn_v.weight"),
                           ("wo", "attn_output.weight"), ("wg", "ffn_gate.weight"), ("wu", "ffn_up.weight"),
                           ("wd", "ffn_down.weight")):

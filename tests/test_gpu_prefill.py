@@ -134,6 +134,30 @@ def test_prefill_kv_capacity_not_tile_multiple(gpu, max_seq, n):
         assert np.array_equal(k, o.keys(layer, n)) and np.array_equal(v, o.values(layer, n))
 
 
+# models without some or all of the q/k/v biases (the prefill's fused RoPE
+# epilogue and decode's qkv kernel then add nothing: x + 0.0 would turn -0.0
+# into +0.0)
+@pytest.mark.parametrize("drop", [("attn_q.bias", "attn_k.bias", "attn_v.bias"), ("attn_k.bias",)])
+def test_prefill_and_decode_without_biases(gpu, drop):
+    t = {k: v for k, v in uq.synth_qwen2(SMALL, 91).items() if not k.endswith(drop)}
+    g, o = uq.Qwen2Model(SMALL, t), O.Model(SMALL, {k: v[3] for k, v in t.items()})
+    toks = uq.synth_tokens(91, 70, SMALL["vocab"])
+    first = g.prefill(toks)
+    rc, ofirst, olg = o.prefill(toks, want_logits=True)
+    assert rc == 0 and first == ofirst
+    assert ulps(g.logits(), olg).max() <= 1
+    for layer in range(SMALL["layers"]):
+        k, v = g.kv(layer, 70)
+        assert np.array_equal(k, o.keys(layer, 70)) and np.array_equal(v, o.values(layer, 70))
+    ids, _ = g.decode_run(first, 70, 12)
+    tok, ref = ofirst, []
+    for pos in range(70, 82):
+        rc, tok, _ = o.decode(tok, pos)
+        assert rc == 0
+        ref.append(tok)
+    assert list(ids) == ref
+
+
 def test_prefill_then_decode(gpu):
     g, o = build(SMALL, 33)
     toks = uq.synth_tokens(33, 50, SMALL["vocab"])

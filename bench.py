@@ -504,7 +504,8 @@ def main():
                 "down alone) instead of five"}
     read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
     result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
-                           "note": "plain int4 streaming read / copy of 1 GiB, same box"}
+                           "note": "streaming read of 1 GiB (one 28 KB chunk of non-temporal 16-byte loads per "
+                                   "workgroup) and plain int4 copy, same box"}
     result["mfma_probe"] = mfma_probe()
     for w in weights:
         w.free()

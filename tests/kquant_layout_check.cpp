@@ -40,7 +40,14 @@ int main() {
     for (int n : {256, 768, 1536, 2048, 3072, 6144, 8960, 16384}) {
         for (int m : {1, 7, 10, 11, 100}) {
             const uq::SbGeom g = uq::sb_geom(n, m);
-            if (!g.LB || g.RB * g.S > g.LB || g.RB < 1 || 8 * (g.LB - g.RB * g.S) > g.LB && g.LB < 256) {
+            // whole waves, at least one row, and no block size of 1-4 waves
+            // with a smaller share of idle slots
+            bool worse = false;
+            for (int lb = 64; lb <= 256; lb += 64) {
+                const int rb = lb / (n / 256);
+                if (rb >= 1 && (int64_t)(lb - rb * g.S) * g.LB < (int64_t)(g.LB - g.RB * g.S) * lb) worse = true;
+            }
+            if (!g.LB || g.LB % 64 || g.LB > 256 || g.RB * g.S > g.LB || g.RB < 1 || worse) {
                 bad_geom++;
                 continue;
             }

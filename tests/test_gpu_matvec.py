@@ -102,14 +102,14 @@ def test_kquant_matvec_ragged_shapes(gpu, kind, m, n):
     assert ulps(uq.matvec(w, x), O.matvec(kind, raw, n, m, x)).max() <= 1
 
 
-# Q3_K weights with row blocks for eight workgroups per CU take the row-block
-# layout (one superblock per lane): blocks of 64 slots (K 768, 1536, 2048,
-# 4096, 16384), 128 (K 6144) and 256 (K 8960), row counts leaving a partial
-# last block, and 4, 2 and 1 blocks of 64, 128 and 256 slots per workgroup;
+# Q3_K weights with row blocks for eight workgroups per CU (2048 blocks) take
+# the row-block layout (one superblock per lane): blocks of 64 slots (K 2048,
+# 4096, 16384), 128 (K 10240), 192 (K 768, 1536, 6144) and 256 (K 8960), row
+# counts leaving a partial last block, and 4, 2 and 1 blocks per workgroup;
 # Q4_K at the same shapes runs the unit planes
 @pytest.mark.parametrize("kind", [uq.KIND_Q3_K, uq.KIND_Q4_K])
-@pytest.mark.parametrize("m,n", [(43018, 768), (20485, 1536), (40000, 1536), (16389, 2048), (8197, 4096),
-                                 (10241, 6144), (14340, 8960), (2050, 16384)])
+@pytest.mark.parametrize("m,n", [(131077, 768), (65541, 1536), (16389, 2048), (8197, 4096), (16387, 6144),
+                                 (14340, 8960), (6145, 10240), (2050, 16384)])
 def test_kquant_matvec_row_block_shapes(gpu, kind, m, n):
     raw = uq.synth_quant(kind, 131 * m + n + kind, m, n)
     x = uq.synth_normal(n + 9, n, 0.0, 2.0)
@@ -121,7 +121,7 @@ def test_kquant_matvec_row_block_shapes(gpu, kind, m, n):
     assert d.max() <= 1 and (d == 0).mean() > 0.999, (d.max(), (d == 0).mean())
 
 
-@pytest.mark.parametrize("kind,n,m", [(uq.KIND_Q3_K, 1536, 20485), (uq.KIND_Q3_K, 8960, 14340)])
+@pytest.mark.parametrize("kind,n,m", [(uq.KIND_Q3_K, 1536, 65541), (uq.KIND_Q3_K, 8960, 14340)])
 def test_block_dots_row_block_layout(gpu, kind, n, m):
     raw = uq.synth_quant(kind, 1000 + kind + m, m, n)
     x = uq.synth_normal(2000 + n, n)
@@ -156,7 +156,7 @@ def test_q8_matvec_ragged_shapes(gpu, m, n):
 @pytest.mark.parametrize("kind,N,K", [(uq.KIND_Q8_0, 8960, 1536), (uq.KIND_Q4_K, 8960, 1536),
                                       (uq.KIND_Q3_K, 8960, 1536), (uq.KIND_Q3_K, 768, 2048),
                                       (uq.KIND_Q4_K, 37, 512), (uq.KIND_Q3_K, 45, 768),
-                                      (uq.KIND_Q3_K, 20485, 1536)])
+                                      (uq.KIND_Q3_K, 65541, 1536)])
 def test_gateup_fused_silu(gpu, kind, N, K):
     import ctypes
     rg = uq.synth_quant(kind, 71 + N, N, K)

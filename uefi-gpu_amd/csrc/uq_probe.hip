@@ -12,24 +12,26 @@
 namespace uq {
 namespace {
 
-// Each workgroup reads one contiguous chunk, its lanes on consecutive 16-byte
-// pieces with four non-temporal loads in flight per lane: the access form of
-// the lm_head matvec, so the rate is an achievable streaming-read ceiling.
+// Each workgroup reads one 28 KB chunk: seven non-temporal 16-byte loads per
+// lane, lanes on consecutive pieces, all issued before the first is used; the
+// dispatcher refills the CUs as workgroups retire (the access form of the
+// lm_head matvecs). Of the read forms timed on MI355X (plain loads, LDS-DMA,
+// 64-1024-thread workgroups, 12-48 KB chunks, persistent grid-stride loops)
+// this one was the fastest at 131 MB, 249 MB and 1 GiB alike, so its rate is
+// the achievable streaming-read ceiling the matvecs are compared with.
+constexpr int PROBE_U = 7;
 __global__ __launch_bounds__(256) void k_probe_read(const int4* __restrict__ src, int64_t n16, int* __restrict__ sink) {
-    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
-    const int64_t b0 = (int64_t)blockIdx.x * per, b1 = b0 + per < n16 ? b0 + per : n16;
-    int acc = 0;
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += 4 * 256) {
-        int4 v[4];
+    const int64_t b0 = (int64_t)blockIdx.x * (PROBE_U * 256) + threadIdx.x;
+    int4 v[PROBE_U];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int64_t j = i + 256 * u;
-            v[u] = uq_ntload16(src + (j < b1 ? j : b1 - 1));
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < PROBE_U; u++) {
+        const int64_t j = b0 + 256 * u;
+        v[u] = uq_ntload16(src + (j < n16 ? j : n16 - 1));
     }
-    if (acc == 0x7fffffff) sink[blockIdx.x] = acc;  // keeps the loads live, never taken for zeroed memory
+    int acc = 0;
+#pragma unroll
+    for (int u = 0; u < PROBE_U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == 0x7fffffff) sink[blockIdx.x & 8191] = acc;  // keeps the loads live, never taken for zeroed memory
 }
 
 __global__ __launch_bounds__(256) void k_probe_copy(const int4* __restrict__ src, int4* __restrict__ dst, int64_t n16) {
@@ -220,13 +222,13 @@ int uq_probe_bandwidth(int64_t bytes, int reps, double* read_gbs, double* copy_g
     UQ_CHECK_HIP(hipMalloc(&b, n16 * 16));
     UQ_CHECK_HIP(hipMalloc(&sink, 4 * 8192));
     UQ_CHECK_HIP(hipMemsetAsync(a, 0, n16 * 16, s));
-    const unsigned grid = 8192;
+    const unsigned grid = 8192, rgrid = (unsigned)((n16 + PROBE_U * 256 - 1) / (PROBE_U * 256));
     hipEvent_t e0, e1;
     UQ_CHECK_HIP(hipEventCreate(&e0));
     UQ_CHECK_HIP(hipEventCreate(&e1));
-    hipLaunchKernelGGL(k_probe_read, dim3(grid), dim3(256), 0, s, a, n16, sink);
+    hipLaunchKernelGGL(k_probe_read, dim3(rgrid), dim3(256), 0, s, a, n16, sink);
     UQ_CHECK_HIP(hipEventRecord(e0, s));
-    for (int r = 0; r < reps; r++) hipLaunchKernelGGL(k_probe_read, dim3(grid), dim3(256), 0, s, a, n16, sink);
+    for (int r = 0; r < reps; r++) hipLaunchKernelGGL(k_probe_read, dim3(rgrid), dim3(256), 0, s, a, n16, sink);
     UQ_CHECK_HIP(hipEventRecord(e1, s));
     UQ_CHECK_HIP(hipEventSynchronize(e1));
     float ms = 0;

@@ -314,7 +314,7 @@ struct Q3K {
 // ---------------------------------------------------------------- row-block layout
 // lm_head-sized Q3_K weights are stored in row blocks in which one lane owns
 // one whole superblock and moves it as 16-byte pieces only. A block
-// has LB lane slots (64, 128 or 256) holding RB = LB / S rows of S = K / 256
+// has LB lane slots (1 to 4 whole waves) holding RB = LB / S rows of S = K / 256
 // superblocks (slot j = row-in-block * S + superblock; slots from RB * S on
 // are padding); piece k of slot j sits at block * LB * P * 16 + k * LB * 16 +
 // j * 16, so one load instruction of a wave reads 64 consecutive pieces, a
@@ -331,23 +331,21 @@ struct SbGeom {
     int S = 0, LB = 0, RB = 0;  // superblocks per row, lane slots and rows per block
     int64_t blocks = 0;         // row blocks (the last one may hold padding rows)
 };
-// The smallest block (64, 128 or 256 slots) leaving at most 1/8 of its slots
-// idle (S <= 64; else no row-block layout).
+// The block of 64, 128, 192 or 256 slots with the smallest share of idle
+// slots, the smaller block on a tie (S <= 64; else no row-block layout). At
+// K = 1536 (S = 6) that is 192 slots, 32 rows and none idle, where 64 slots
+// would leave 4 of every 64 idle and move 6.7% more bytes.
 inline SbGeom sb_geom(int64_t n, int64_t m) {
     SbGeom g;
     if (n % 256 || n / 256 > 64 || m <= 0) return g;
     g.S = (int)(n / 256);
-    for (int lb = 64; lb <= 256; lb *= 2) {
+    for (int lb = 64; lb <= 256; lb += 64) {
         const int rb = lb / g.S;
-        if (rb >= 1 && 8 * (lb - rb * g.S) <= lb) {
+        // idle share (lb - rb S) / lb below the best one's, cross-multiplied
+        if (rb >= 1 && (!g.LB || (int64_t)(lb - rb * g.S) * g.LB < (int64_t)(g.LB - g.RB * g.S) * lb)) {
             g.LB = lb;
             g.RB = rb;
-            break;
         }
-    }
-    if (!g.LB) {
-        g.LB = 256;
-        g.RB = 256 / g.S;
     }
     g.blocks = (m + g.RB - 1) / g.RB;
     return g;

@@ -424,7 +424,7 @@ def main():
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus %d is not supported "
+        print("bench.py measures one GPU; --gpus %d is not supported "
               "(the path's multi-GPU sharding is design-only)" % args.gpus, file=sys.stderr)
         sys.exit(2)
 

@@ -363,7 +363,7 @@ class Model:
 class RefoModel(Model):
     """The reference-order decoder: the f32 operation orders of the reference's
     decode-graph kernels (gpu_graph.rs:137-162), f32 KV cache (kv_fp16: the
-    cache rounded to fp16 as this build stores it). Token by token only."""
+    cache rounded to fp16 as the library stores it). Token by token only."""
 
     def __init__(self, cfg, tensors, kv_fp16=False):
         super().__init__(cfg, tensors)

@@ -982,7 +982,7 @@ int64_t uqo_frontier_fixture(uint32_t kind, int64_t n, uint8_t* out) {
 /* exp is uqo_expf (libm's algorithm) where the GPU kernels call CUDA's     */
 /* expf, whose steps are not reproduced; that and the host trig table are   */
 /* the only departures. kv_fp16 != 0 rounds cached K and V to fp16, the     */
-/* cache format of this build, to separate order effects from cache         */
+/* library's cache format, to separate order effects from cache             */
 /* precision.                                                               */
 
 struct uqo_refo {

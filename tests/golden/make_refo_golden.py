@@ -8,7 +8,7 @@ free-running greedy run of the exact contract).
 
 Saved for the 129 positions 511..639 (the prompt's last token, then the forced
 steps), once with an f32 KV cache (the reference's) and once with the cache
-rounded to fp16 (this build's format):
+rounded to fp16 (the library's format):
   idx        the compared vocabulary ids per position: the 64 largest logits
              of the f32-cache run, then 192 fixed seeded ids
   ref_f32, ref_f16   those logits

@@ -6,7 +6,7 @@ GPU runs, teacher-forced, with the oracle's reference-order decoder
 (uqo_refo_*: the f32 orders of fused_resnorm, quant_act, qkv/gateup/linear
 dp4a, rope_bias and fused_attention of the reference's decode graph,
 gpu_graph.rs:137-162), with the KV cache in f32 as the reference keeps it and
-rounded to fp16 as this build keeps it.
+rounded to fp16 as the library keeps it.
 
 What is graded, and why: int8 activation quantization is discontinuous. A
 last-ulp difference of two valid f32 orders occasionally moves one activation
@@ -92,7 +92,7 @@ def test_28_layers_after_512_prompt_teacher_forced(gpu):
         m.free()
     n = len(f["forced"]) + 1
     assert n == 129 and len(ids) == n
-    assert ids[:-1] == [int(t) for t in f["forced"]]       # the fixture's tokens are this build's greedy ids
+    assert ids[:-1] == [int(t) for t in f["forced"]]       # the fixture's tokens are the library's greedy ids
     assert ids == [int(t) for t in f["argmax_exact"]]      # and the exact oracle's, at all 129 positions
     # measured over the 129 positions (exact oracle vs reference order): fp16
     # cache max 0.047, median 0.028; f32 cache max 0.257, median 0.047

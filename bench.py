@@ -254,7 +254,7 @@ def prefill_attention_bench(tokens=512, heads=12, kv_heads=2, head_dim=128, reps
 
 
 def mfma_probe():
-    """Matrix-core rates on this box: 16 waves per CU (kinds 0-2), and one wave per
+    """Matrix-core rates on this GPU: 16 waves per CU (kinds 0-2), and one wave per
     SIMD with and without the VALU work the prefill kernels put beside their
     MFMAs (kinds 3-6): fp64 MFMAs with an fp16 -> double operand conversion each,
     int8 MFMAs beside the per-block f32 rescale."""
@@ -271,7 +271,7 @@ def mfma_probe():
     r["one_wave_per_simd"]["int8_overlap"] = overlap(one["int8"], one["int8_and_rescale"], one["rescale_only"])
     r["note"] = ("independent chains of v_mfma_i32_16x16x32_i8 (int8_TOPS) / v_mfma_i32_32x32x32_i8 / "
                  "v_mfma_i32_16x16x64_i8 / v_mfma_f32_16x16x32_f16 / v_mfma_f64_16x16x4_f64 "
-                 "on register operands, 16 waves per CU, same box; one_wave_per_simd: 16 MFMAs per iteration on "
+                 "on register operands, 16 waves per CU, same GPU; one_wave_per_simd: 16 MFMAs per iteration on "
                  "4 chains and/or the VALU work beside them (fp64: 16 fp16->double operand conversions; int8: "
                  "convert, scale product, fma of 16 f32 accumulators), rates of the same MFMA count; overlap: "
                  "share of the shorter part hidden under the longer (0 additive, 1 fully overlapped)")
@@ -505,7 +505,7 @@ def main():
     read_gbs, copy_gbs = uq.probe_bandwidth(1 << 30, 10)
     result["hbm_probe"] = {"stream_read_GBs": round(read_gbs, 1), "copy_GBs": round(copy_gbs, 1),
                            "note": "streaming read of 1 GiB (one 28 KB chunk of non-temporal 16-byte loads per "
-                                   "workgroup) and plain int4 copy, same box"}
+                                   "workgroup) and plain int4 copy, same GPU"}
     result["mfma_probe"] = mfma_probe()
     for w in weights:
         w.free()

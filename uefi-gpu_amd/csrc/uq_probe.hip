@@ -1,5 +1,5 @@
 // Probes used by the benchmark: a plain streaming read and a plain copy of a
-// known number of bytes (the achievable HBM rate on the box and the
+// known number of bytes (the achievable HBM rate on the device and the
 // calibration of the FETCH_SIZE / WRITE_SIZE counters), and matrix-core
 // throughput loops (the achievable int8 / fp16 / fp64 MFMA rates, int8 in
 // its 16x16x32, 32x32x32 and 16x16x64 forms).

@@ -353,6 +353,26 @@ def linear_sweep(n=2560, copies=3, reps=20):
     return out
 
 
+def launch_cost(reps=200):
+    """One Q8_0 matvec launch's mean duration between HIP events after
+    different predecessors (the sweep's small q/o and k/v launches)."""
+    mk = lambda n, k, seed: uq.Weight(uq.KIND_Q8_0, k, n, uq.synth_quant(uq.KIND_Q8_0, seed, n, k))
+    kv = [mk(256, 1536, 0x5EED0031 + i) for i in range(3)]
+    qo = mk(1536, 1536, 0x5EED0034)
+    lm = mk(151936, 1536, 0x5EED0035)
+    down = mk(1536, 8960, 0x5EED0036)
+    cases = [("k/v alone", [kv[0]], 0, reps), ("k/v after k/v (three copies)", kv, 1, reps),
+             ("q/o alone", [qo], 0, reps), ("k/v after q/o", [qo, kv[0]], 1, reps),
+             ("k/v after lm_head", [lm, kv[0]], 1, reps // 3), ("q/o after lm_head", [lm, qo], 1, reps // 3),
+             ("k/v after down", [down, kv[0]], 1, reps), ("lm_head alone", [lm], 0, reps // 3)]
+    out = {}
+    for name, ws, probe, r in cases:
+        tot, pm = uq.time_matvecs(ws, [0] * len(ws), 151936, r, 10, probe)
+        out[name] = {"probed_us": round(pm * 1000, 2), "round_us": round(tot * 1000 / r, 2)}
+    out["note"] = "mean of the probed launch between HIP events (the event records add their own time)"
+    return out
+
+
 def frontier_moe_bench(tokens=32, reps=3, experts=256, top_k=10, dim=2560, ff=640):
     """Device work of the frontier MoE block (Forward::ffn) per token: the F32
     router linear, then the 23-job table (10 routed experts' IQ3_XXS gate and
@@ -420,7 +440,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode leg")
     ap.add_argument("--leg", choices=["decode", "prefill", "attention", "probes", "q4k", "q3k", "moe", "linear",
-                                      "frontier_moe"],
+                                      "frontier_moe", "launches"],
                     help="run only this secondary leg and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -433,7 +453,8 @@ def main():
         leg = {"decode": decode_bench, "prefill": prefill_gemm_bench, "attention": prefill_attention_bench,
                "probes": mfma_probe,
                "q4k": q4k_sweep, "q3k": q3k_sweep,
-               "moe": moe_bench, "linear": linear_sweep, "frontier_moe": frontier_moe_bench}[args.leg]
+               "moe": moe_bench, "linear": linear_sweep, "frontier_moe": frontier_moe_bench,
+               "launches": launch_cost}[args.leg]
         print(json.dumps({args.leg: leg()}), flush=True)
         return
     weights, pairs, shape_of = [], [], []
